@@ -1,0 +1,125 @@
+// Internal runtime structures shared by the C-ABI layer, the kernel launchers
+// and the block compositions of libdrawinstant_hip.so.
+//
+// One di_ctx = one HIP device + one in-order HIP stream.  All device memory is
+// owned by the library and referenced from the host by opaque u64 handles (the
+// role GPUBuffer plays in wgsl-executor.js:45-55); a 4 KiB-bucketed free list
+// gives the BufferPool semantics of wgsl-executor.js:62-94.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/drawinstant.h"
+
+namespace di {
+
+struct Buffer {
+  void* ptr = nullptr;
+  uint64_t bytes = 0;  // requested size
+  uint64_t cap = 0;    // bucket-rounded capacity actually allocated
+};
+
+constexpr int kTimerSlots = 64;
+
+struct Ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int num_cus = 0;
+  int clock_khz = 0;
+  uint64_t hbm_bytes = 0;
+  // handle table
+  std::unordered_map<uint64_t, Buffer> bufs;
+  uint64_t next_handle = 1;
+  // pooled free list keyed by bucket capacity
+  std::map<uint64_t, std::vector<void*>> free_list;
+  uint64_t live = 0, peak = 0, allocs = 0, reserved = 0, limit = 0;
+  // timers
+  hipEvent_t ev_begin[kTimerSlots] = {};
+  hipEvent_t ev_end[kTimerSlots] = {};
+  bool ev_used[kTimerSlots] = {};
+  // kernel workspace (partials); grown on demand, never during graph capture
+  void* ws = nullptr;
+  uint64_t ws_bytes = 0;
+  // Zero-initialised words for cross-block barriers / last-block counters.
+  // Every user leaves its words at zero again when its kernel ends, so they
+  // never need clearing (and no memset is ever recorded into a graph).
+  // Word 0 is the fault flag: set by a kernel whose bounded wait expired.
+  uint32_t* sync_words = nullptr;
+};
+
+constexpr uint32_t kSyncWords = 1u << 18;  // 1 MiB
+constexpr uint32_t kFaultWord = 0;
+
+// ---- error reporting (thread-local message, status code returned) ----
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+const char* get_error();
+
+// Validation helper: returns `code` from the enclosing function with a message.
+#define DI_REQUIRE(cond, code, ...)           \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::di::set_error(__VA_ARGS__);           \
+      return (code);                          \
+    }                                         \
+  } while (0)
+
+#define DI_HIP(expr)                                                          \
+  do {                                                                        \
+    hipError_t _e = (expr);                                                   \
+    if (_e != hipSuccess) {                                                   \
+      ::di::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), \
+                      __FILE__, __LINE__);                                    \
+      return DI_EHIP;                                                         \
+    }                                                                         \
+  } while (0)
+
+// Check the launch status of the most recent kernel.
+#define DI_LAUNCH_CHECK() DI_HIP(hipGetLastError())
+
+// Entry-point prologue: non-null context, its device current on this thread.
+#define DI_CTX(ctx)                                          \
+  do {                                                       \
+    DI_REQUIRE((ctx) != nullptr, DI_EINVAL, "null context"); \
+    DI_HIP(hipSetDevice((ctx)->device));                     \
+  } while (0)
+
+#define DI_DTYPE(dt) \
+  DI_REQUIRE(::di::dtype_ok(dt), DI_EINVAL, "unsupported dtype %d", (int)(dt))
+
+// Handle lookup; fills `buf` or returns DI_EHANDLE from the enclosing function.
+int lookup(Ctx* c, di_handle h, Buffer** out);
+
+#define DI_BUF(c, h, var, need_bytes)                                            \
+  Buffer* var = nullptr;                                                         \
+  do {                                                                           \
+    int _rc = ::di::lookup((c), (h), &var);                                      \
+    if (_rc) return _rc;                                                         \
+    if ((uint64_t)(need_bytes) > var->bytes) {                                   \
+      ::di::set_error("buffer %s: handle %llu holds %llu bytes, op needs %llu", \
+                      #h, (unsigned long long)(h),                               \
+                      (unsigned long long)var->bytes,                            \
+                      (unsigned long long)(need_bytes));                         \
+      return DI_EINVAL;                                                          \
+    }                                                                            \
+  } while (0)
+
+// Workspace of at least `bytes` (grown with hipMalloc on demand).
+int workspace(Ctx* c, uint64_t bytes, void** out);
+
+// Pooled device allocation used by the C ABI and by block compositions.
+int pool_alloc(Ctx* c, uint64_t bytes, void** out, uint64_t* cap);
+void pool_release(Ctx* c, void* p, uint64_t cap);
+
+inline size_t dtype_size(int dt) { return dt == DI_F32 ? 4 : 2; }
+inline bool dtype_ok(int dt) { return dt == DI_F32 || dt == DI_F16; }
+
+}  // namespace di
+
+struct di_ctx : di::Ctx {};

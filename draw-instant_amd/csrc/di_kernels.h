@@ -1,0 +1,43 @@
+// Internal launch API of the gfx950 kernels.  Raw device pointers, explicit
+// stream; used by the C-ABI wrappers and by the block / U-Net compositions.
+// Every launcher validates nothing: callers check shapes first.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "di_internal.h"
+
+namespace di {
+
+// ---- element-wise / layout (k_eltwise.hip) ----
+void launch_convert(hipStream_t s, const void* src, int sdt, void* dst, int ddt, uint64_t n);
+// [N,C,H,W] layout/dtype change; C_dst >= C pads channels with zeros when the
+// destination is NHWC (used to give conv_in an 8-aligned channel count).
+void launch_layout(hipStream_t s, const void* src, int sdt, int slay, void* dst, int ddt,
+                   int dlay, uint32_t N, uint32_t C, uint32_t H, uint32_t W,
+                   uint32_t C_dst);
+void launch_fill_normal(hipStream_t s, void* dst, int dt, uint64_t n, uint64_t seed,
+                        float mean, float std);
+void launch_fill_const(hipStream_t s, void* dst, int dt, uint64_t n, float v);
+
+// ---- normalisation (k_norm.hip) ----
+// NCHW group norm (single pass with a cross-workgroup barrier when the group
+// slices fit in registers of co-resident workgroups, else two passes).
+int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const float* beta,
+                           void* y, uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW,
+                           float eps, bool silu, int dt);
+// NHWC fp16 group norm (two kernels: partial stats + last-block fold, apply).
+// `ws` needs gn_nhwc_ws_floats() floats; `sync` = Ctx::sync_words.
+uint32_t gn_nhwc_chunks(uint32_t HW, uint32_t C);
+uint64_t gn_nhwc_ws_floats(uint32_t N, uint32_t C, uint32_t G, uint32_t HW);
+void launch_group_norm_nhwc(hipStream_t s, const void* x, const float* gamma,
+                            const float* beta, void* y, uint32_t N, uint32_t C,
+                            uint32_t G, uint32_t HW, float eps, bool silu, float* ws,
+                            uint32_t* sync);
+void launch_layer_norm(hipStream_t s, const void* x, const float* gamma,
+                       const float* beta, void* y, uint32_t rows, uint32_t inner,
+                       float eps, int dt);
+
+}  // namespace di

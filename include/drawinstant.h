@@ -1,0 +1,214 @@
+/*
+ * drawinstant.h — C ABI of libdrawinstant_hip.so, the MI355X (gfx950) kernel
+ * library behind draw-instant's SD-Turbo U-Net op / fused-block layer.
+ *
+ * Conventions (all entry points):
+ *   - every function returns int32 status, DI_OK (0) on success; on failure a
+ *     thread-local message is available from di_last_error();
+ *   - device memory is owned by the library and named by opaque u64 handles
+ *     (replaces GPUBuffer, reference wgsl-executor.js:45-55);
+ *   - one context = one device + one in-order HIP stream; ops enqueue and
+ *     return immediately, only di_download / di_sync / di_timer_ms block;
+ *   - shapes travel as scalar arguments (the reference packs them in uniform
+ *     buffers, e.g. GnCfg wgsl-ops.js:395, ConvMmCfg wgsl-ops.js:585-598);
+ *   - all validation (shape, dtype, null/freed handle, C%G, buffer sizes) runs
+ *     before any launch, so it is testable without a GPU.
+ *
+ * Each declaration cites the reference interface it replaces (file:line in
+ * abgnydn/draw-instant).
+ */
+#ifndef DRAWINSTANT_H
+#define DRAWINSTANT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct di_ctx di_ctx;
+typedef uint64_t di_handle;
+
+/* ---- status codes ---- */
+#define DI_OK 0
+#define DI_EINVAL 1       /* bad argument / shape */
+#define DI_ENOMEM 2       /* allocation failed or DI_ALLOC_LIMIT exceeded */
+#define DI_EHIP 3         /* HIP runtime error (async faults surface here) */
+#define DI_EUNSUPPORTED 4 /* valid request this build does not implement */
+#define DI_EHANDLE 5      /* null, unknown or freed handle */
+
+/* ---- dtypes (per tensor argument unless stated) ---- */
+#define DI_F32 0
+#define DI_F16 1
+
+/* ---- activation layouts ---- */
+#define DI_NCHW 0 /* reference layout (wgsl-executor.js Tensor dims) */
+#define DI_NHWC 1 /* channels-last: the library's native U-Net layout */
+
+/* ---- unary ops: UNARY_EXPRS wgsl-ops.js:58-72 (+ tanh GELU of fused-block.js:68-75) ---- */
+#define DI_UN_SIGMOID 0
+#define DI_UN_SQRT 1
+#define DI_UN_NEG 2
+#define DI_UN_ABS 3
+#define DI_UN_SIN 4
+#define DI_UN_COS 5
+#define DI_UN_EXP 6
+#define DI_UN_LOG 7
+#define DI_UN_SILU 8
+#define DI_UN_GELU 9       /* erf GELU, erf by Abramowitz-Stegun 7.1.26 */
+#define DI_UN_ERF 10
+#define DI_UN_GELU_TANH 11 /* tanh-approximation GELU */
+
+/* ---- binary ops: BINARY_EXPRS wgsl-ops.js:130-134 ---- */
+#define DI_BIN_ADD 0
+#define DI_BIN_SUB 1
+#define DI_BIN_MUL 2
+#define DI_BIN_DIV 3
+#define DI_BIN_POW 4 /* sign-aware pow */
+#define DI_BIN_MAX 5
+#define DI_BIN_MIN 6
+
+/* ---- norm flags ---- */
+#define DI_NORM_SILU 1 /* apply x/(1+exp(-x)) after the affine (fused-resnet.js:162) */
+
+/* ======================= lifecycle ======================= */
+
+/* Replaces navigator.gpu.requestAdapter/requestDevice (unet-wgsl.js:63-72). */
+int32_t di_create(int32_t device, di_ctx** out);
+int32_t di_destroy(di_ctx* ctx);
+/* Thread-local message of the last failing call on this thread. */
+const char* di_last_error(void);
+/* Replaces device.queue.onSubmittedWorkDone (bench-timing.js:28); surfaces
+ * asynchronous kernel faults (role of getUNetGpuFault, unet-wgsl.js:172-175). */
+int32_t di_sync(di_ctx* ctx);
+/* Compute-unit count, current shader clock (kHz) and HBM bytes of the device. */
+int32_t di_device_info(di_ctx* ctx, int32_t* num_cus, int32_t* clock_khz,
+                       uint64_t* hbm_bytes);
+
+/* ======================= memory ======================= */
+
+/* BufferPool.acquire (wgsl-executor.js:71-80): 4 KiB-bucketed reuse. */
+int32_t di_alloc(di_ctx* ctx, uint64_t bytes, di_handle* out);
+/* BufferPool.release (wgsl-executor.js:84-90). Stream-ordered: safe to call
+ * right after enqueueing the last op that reads the buffer. */
+int32_t di_free(di_ctx* ctx, di_handle h);
+int32_t di_buffer_size(di_ctx* ctx, di_handle h, uint64_t* bytes);
+/* BufferPool live/peak/allocs counters (wgsl-executor.js:67-69). */
+int32_t di_pool_stats(di_ctx* ctx, uint64_t* live, uint64_t* peak,
+                      uint64_t* allocs, uint64_t* reserved_bytes);
+/* createStorage / queue.writeBuffer (wgsl-ops.js:1172-1180). */
+int32_t di_upload(di_ctx* ctx, di_handle h, uint64_t offset, const void* src,
+                  uint64_t bytes);
+/* readBack (wgsl-ops.js:1195-1210): synchronous, the only implicit sync. */
+int32_t di_download(di_ctx* ctx, di_handle h, uint64_t offset, void* dst,
+                    uint64_t bytes);
+/* encoder.copyBufferToBuffer (wgsl-executor.js:1412-1423 output snapshot). */
+int32_t di_copy(di_ctx* ctx, di_handle dst, uint64_t dst_offset, di_handle src,
+                uint64_t src_offset, uint64_t bytes);
+/* f32<->f16 element conversion, RNE (replaces f16BytesToF32 wgsl-unet.js:23-47
+ * and f32ToF16 unet.js:108-135). */
+int32_t di_convert(di_ctx* ctx, di_handle src, int32_t src_dtype, di_handle dst,
+                   int32_t dst_dtype, uint64_t n);
+/* Activation layout/dtype change for [N,C,H,W] tensors (NCHW<->NHWC, f32<->f16).
+ * No reference counterpart: the reference is NCHW f32 only. */
+int32_t di_layout_convert(di_ctx* ctx, di_handle src, int32_t src_dtype,
+                          int32_t src_layout, di_handle dst, int32_t dst_dtype,
+                          int32_t dst_layout, uint32_t N, uint32_t C, uint32_t H,
+                          uint32_t W);
+/* Seeded N(mean, std) fill on device (SplitMix64 counter hash + Box-Muller).
+ * Replaces the benches' Math.random fills (e.g. fused-resnet.js:278-283). */
+int32_t di_fill_normal(di_ctx* ctx, di_handle h, int32_t dtype, uint64_t n,
+                       uint64_t seed, float mean, float std);
+
+/* ======================= timing ======================= */
+
+/* hipEvent pair per slot on the context stream; used with the reference's
+ * slope method (measurePair bench-timing.js:49-97). */
+int32_t di_timer_begin(di_ctx* ctx, int32_t slot);
+int32_t di_timer_end(di_ctx* ctx, int32_t slot);
+int32_t di_timer_ms(di_ctx* ctx, int32_t slot, float* ms);
+
+/* ======================= executor element-wise ops ======================= */
+/* All tensors share `dtype`; n / numel count elements. */
+
+/* unary(device, op) dispatch (wgsl-ops.js:110-126) for OPS.Sigmoid/Sqrt/Erf/
+ * Abs/Neg/Silu/Sin/Cos (wgsl-executor.js:694-706, :790-794, :508-516). */
+int32_t di_unary(di_ctx* ctx, int32_t op, di_handle X, di_handle Y, uint64_t n,
+                 int32_t dtype);
+/* binary(device, op) same-shape dispatch (wgsl-ops.js:241-252). */
+int32_t di_binary(di_ctx* ctx, int32_t op, di_handle A, di_handle B, di_handle Y,
+                  uint64_t n, int32_t dtype);
+/* binaryBcast (wgsl-ops.js:156-201): rank<=4, per-operand element strides
+ * (0 on broadcast dims), as filled by wgsl-executor.js:644-667. */
+int32_t di_binary_bcast(di_ctx* ctx, int32_t op, di_handle A, di_handle B,
+                        di_handle Y, uint32_t rank, const uint32_t* out_dim,
+                        const uint32_t* a_stride, const uint32_t* b_stride,
+                        uint64_t numel, int32_t dtype);
+/* affineBcast (wgsl-ops.js:206-237): Y = A*gamma + beta, gamma/beta sharing
+ * one stride vector (OPS.AffineBcast wgsl-executor.js:753-785). */
+int32_t di_affine_bcast(di_ctx* ctx, di_handle A, di_handle gamma, di_handle beta,
+                        di_handle Y, uint32_t rank, const uint32_t* out_dim,
+                        const uint32_t* a_stride, const uint32_t* bc_stride,
+                        uint64_t numel, int32_t dtype);
+/* softmax over the last axis (wgsl-ops.js:266-295, OPS.Softmax
+ * wgsl-executor.js:1027-1037). One wavefront per row. */
+int32_t di_softmax(di_ctx* ctx, di_handle X, di_handle Y, uint32_t inner,
+                   uint32_t rows, int32_t dtype);
+/* reduceMean over the last axis (wgsl-ops.js:958-983). */
+int32_t di_reduce_mean(di_ctx* ctx, di_handle X, di_handle Y, uint32_t inner,
+                       uint32_t rows, int32_t dtype);
+/* resizeNearest (wgsl-ops.js:921-955, OPS.Resize wgsl-executor.js:1095-1114):
+ * planes = N*C, floor index mapping. */
+int32_t di_resize_nearest(di_ctx* ctx, di_handle X, di_handle Y, uint32_t planes,
+                          uint32_t Hin, uint32_t Win, uint32_t Hout, uint32_t Wout,
+                          int32_t dtype);
+/* transpose (wgsl-ops.js:993-1044, OPS.Transpose wgsl-executor.js:410-441). */
+int32_t di_transpose(di_ctx* ctx, di_handle X, di_handle Y, uint32_t rank,
+                     const uint32_t* out_dim, const uint32_t* in_stride,
+                     const uint32_t* perm, uint64_t numel, int32_t dtype);
+/* slice, step 1 (wgsl-ops.js:1092-1134, OPS.Slice wgsl-executor.js:313-368). */
+int32_t di_slice(di_ctx* ctx, di_handle X, di_handle Y, uint32_t rank,
+                 const uint32_t* out_dim, const uint32_t* in_stride,
+                 const uint32_t* start, uint64_t numel, int32_t dtype);
+/* concatCopy (wgsl-ops.js:1142-1170, OPS.Concat wgsl-executor.js:444-488). */
+int32_t di_concat_copy(di_ctx* ctx, di_handle X, di_handle Y, uint32_t stripe_in,
+                       uint32_t stripe_out, uint32_t offset_out, uint64_t numel,
+                       int32_t dtype);
+/* powScalar (wgsl-ops.js:1050-1083, OPS.Pow wgsl-executor.js:519-539). */
+int32_t di_pow_scalar(di_ctx* ctx, di_handle X, di_handle Y, uint64_t n,
+                      float exponent, int32_t dtype);
+
+/* ======================= normalisation ======================= */
+
+/* GroupNorm over each (n, g) block of cpg*HW elements, then per-channel
+ * gamma/beta (fp32, length G*cpg); optional fused SiLU.
+ * Replaces groupNorm (wgsl-ops.js:390-469) as dispatched by OPS.GroupNorm
+ * (wgsl-executor.js:715-746), and with DI_NORM_SILU the fused GN+SiLU kernel
+ * WGSL_FUSED_GN_SILU (fused-resnet.js:121-166).  Statistics follow the
+ * reference: var = E[x^2] - E[x]^2 clamped at 0, rstd = 1/sqrt(var + eps).
+ * X, Y: dtype, layout NCHW or NHWC; Y may not alias X. */
+int32_t di_group_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
+                      di_handle Y, uint32_t N, uint32_t G, uint32_t cpg,
+                      uint32_t HW, float eps, int32_t flags, int32_t dtype,
+                      int32_t layout);
+/* The fused-resnet.js GN+SiLU entry point (== di_group_norm with DI_NORM_SILU). */
+int32_t di_gn_silu(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
+                   di_handle Y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW,
+                   float eps, int32_t dtype, int32_t layout);
+/* InstanceNormalization (wgsl-ops.js:307-372, OPS.InstanceNormalization
+ * wgsl-executor.js:1011-1025): GroupNorm with G = C. The reference hard-codes
+ * eps 1e-5; here eps is an argument. NCHW. */
+int32_t di_instance_norm(di_ctx* ctx, di_handle X, di_handle gamma,
+                         di_handle beta, di_handle Y, uint32_t N, uint32_t C,
+                         uint32_t HW, float eps, int32_t dtype);
+/* Row LayerNorm over the last dim (layerNorm wgsl-ops.js:772-812, WGSL_LN
+ * fused-block-full.js:62-122); gamma/beta fp32 of length inner. */
+int32_t di_layer_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
+                      di_handle Y, uint32_t rows, uint32_t inner, float eps,
+                      int32_t dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DRAWINSTANT_H */

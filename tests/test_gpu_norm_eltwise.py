@@ -1,0 +1,294 @@
+"""GPU parity: GroupNorm(+SiLU) / InstanceNorm / LayerNorm, element-wise
+executor ops, conversions and the seeded generator of libdrawinstant_hip.so
+against the CPU oracle on identical inputs.
+
+Tolerances (written per test): fp32 norm / element-wise paths max-rel <= 1e-4
+(max |d| / max(1, |ref|)), the fp32 gate of the north star; fp16 outputs add
+at most half an fp16 ulp of the result (<= 4.9e-4 relative), so fp16 paths use
+2e-3.  Integer-like work (copies, layout changes, conversions) is bit-exact.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import max_rel
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, NCHW, NHWC = 0, 1, 0, 1
+
+
+def _up(dev, a):
+    return dev.storage(np.ascontiguousarray(a))
+
+
+def _gn_inputs(dev, N, C, HW, seed, dt=F32):
+    import drawinstant
+    n = N * C * HW
+    x = dev.create_buffer(n * (4 if dt == F32 else 2))
+    dev.fill_normal(x, n, seed, 0.0, 1.0, dt)
+    g = dev.create_buffer(C * 4)
+    dev.fill_normal(g, C, seed + 1, 1.0, 0.02)
+    b = dev.create_buffer(C * 4)
+    dev.fill_normal(b, C, seed + 2, 0.0, 0.02)
+    xh = dev.download(x, np.float32 if dt == F32 else np.float16).astype(np.float32)
+    return x, g, b, xh, dev.download(g), dev.download(b)
+
+
+@pytest.mark.parametrize("N,C,H,W,G,eps,silu", [
+    (1, 320, 64, 64, 32, 1e-5, True),     # cfg1
+    (1, 1280, 16, 16, 32, 1e-5, False),   # fused-groupnorm.js SHAPE
+    (2, 64, 8, 8, 32, 1e-6, True),
+    (1, 96, 5, 7, 4, 1e-5, True),         # HW % 4 != 0: scalar path
+    (1, 128, 128, 128, 32, 1e-5, True),   # many slices per group
+    (1, 32, 768, 768, 32, 1e-5, False),   # too large for registers: two-pass
+])
+def test_group_norm_nchw_f32(dev, N, C, H, W, G, eps, silu):
+    import drawinstant
+    HW = H * W
+    print(f"[gn nchw f32] N={N} C={C} HW={HW} G={G}", flush=True)
+    x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, HW, 101)
+    y = dev.create_buffer(N * C * HW * 4)
+    drawinstant.call("di_group_norm", dev.ctx, x.handle, g.handle, b.handle, y.handle, N, G,
+                     C // G, HW, eps, 1 if silu else 0, F32, NCHW)
+    got = dev.download(y).reshape(N, C, H, W)
+    ref = oracle.group_norm(xh.reshape(N, C, H, W), gh, bh, G, eps=eps, silu=silu)
+    assert max_rel(got, ref) <= 1e-4
+    dev.sync()  # raises if a cross-workgroup wait expired
+    for t in (x, g, b, y):
+        t.destroy()
+
+
+def test_gn_silu_entry_point_and_repeat(dev):
+    """di_gn_silu == group_norm+SiLU; repeated launches stay correct (the
+    cross-workgroup barrier words reset themselves)."""
+    import drawinstant
+    N, C, HW, G = 1, 320, 4096, 32
+    x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, HW, 111)
+    y = dev.create_buffer(N * C * HW * 4)
+    ref = oracle.group_norm(xh.reshape(N, C, HW), gh, bh, G, eps=1e-5, silu=True)
+    for _ in range(20):
+        drawinstant.call("di_gn_silu", dev.ctx, x.handle, g.handle, b.handle, y.handle, N, C, G,
+                         HW, 1e-5, F32, NCHW)
+    assert max_rel(dev.download(y).reshape(N, C, HW), ref) <= 1e-4
+    dev.sync()
+
+
+def test_group_norm_nchw_f16(dev):
+    import drawinstant
+    N, C, H, W, G = 1, 320, 32, 32, 32
+    x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, H * W, 121, dt=F16)
+    y = dev.create_buffer(N * C * H * W * 2)
+    drawinstant.call("di_group_norm", dev.ctx, x.handle, g.handle, b.handle, y.handle, N, G,
+                     C // G, H * W, 1e-5, 1, F16, NCHW)
+    got = dev.download(y, np.float16).astype(np.float32).reshape(N, C, H, W)
+    ref = oracle.group_norm(xh.reshape(N, C, H, W), gh, bh, G, eps=1e-5, silu=True)
+    assert max_rel(got, ref) <= 2e-3
+
+
+@pytest.mark.parametrize("N,C,HW,G,eps", [
+    (1, 320, 4096, 32, 1e-5), (1, 640, 1024, 32, 1e-6), (1, 960, 4096, 32, 1e-5),
+    (1, 1280, 256, 32, 1e-5), (1, 2560, 64, 32, 1e-5), (2, 1920, 256, 32, 1e-6),
+    (1, 1280, 64, 32, 1e-6),
+])
+def test_group_norm_nhwc_f16(dev, N, C, HW, G, eps):
+    import drawinstant
+    print(f"[gn nhwc f16] N={N} C={C} HW={HW}", flush=True)
+    x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, HW, 131, dt=F16)
+    y = dev.create_buffer(N * C * HW * 2)
+    for silu in (1, 0):
+        drawinstant.call("di_group_norm", dev.ctx, x.handle, g.handle, b.handle, y.handle, N, G,
+                         C // G, HW, eps, silu, F16, NHWC)
+        got = dev.download(y, np.float16).astype(np.float32).reshape(N, HW, C)
+        ref = oracle.group_norm(xh.reshape(N, HW, C).transpose(0, 2, 1).copy(), gh, bh, G,
+                                eps=eps, silu=bool(silu))
+        assert max_rel(got.transpose(0, 2, 1), ref) <= 2e-3
+
+
+def test_instance_norm_kat(dev):
+    import drawinstant
+    n, c, h, w = 2, 4, 8, 8  # wgsl-ops-test.js:132-133
+    x = np.array([math.sin(i * 0.07) * 3 + 1 for i in range(n * c * h * w)], np.float32)
+    g = np.full(c, 1.2, np.float32)
+    b = np.full(c, -0.3, np.float32)
+    bx, bg, bb = _up(dev, x), _up(dev, g), _up(dev, b)
+    y = dev.create_buffer(x.nbytes)
+    drawinstant.call("di_instance_norm", dev.ctx, bx.handle, bg.handle, bb.handle, y.handle, n, c,
+                     h * w, 1e-5, F32)
+    ref = oracle.instance_norm(x.reshape(n, c, h, w), g, b, eps=1e-5)
+    assert max_rel(dev.download(y).reshape(n, c, h, w), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("rows,inner,dt", [(8, 128, F32), (4096, 320, F16), (1024, 640, F16),
+                                           (256, 1280, F16), (77, 1024, F32), (5, 33, F32)])
+def test_layer_norm(dev, rows, inner, dt, rng):
+    import drawinstant
+    if rows == 8:  # wgsl-ops-test.js:308-312
+        x = np.array([math.sin(i * 0.05) * 2 + 1 for i in range(rows * inner)], np.float32)
+        g = np.array([0.9 + i * 0.01 for i in range(inner)], np.float32)
+        b = np.array([-0.1 + i * 0.005 for i in range(inner)], np.float32)
+    else:
+        x = rng.standard_normal(rows * inner).astype(np.float32)
+        g = (1 + 0.02 * rng.standard_normal(inner)).astype(np.float32)
+        b = (0.02 * rng.standard_normal(inner)).astype(np.float32)
+    npdt = np.float32 if dt == F32 else np.float16
+    x = x.astype(npdt)
+    bx, bg, bb = _up(dev, x), _up(dev, g), _up(dev, b)
+    y = dev.create_buffer(x.nbytes)
+    drawinstant.call("di_layer_norm", dev.ctx, bx.handle, bg.handle, bb.handle, y.handle, rows,
+                     inner, 1e-5, dt)
+    got = dev.download(y, npdt).astype(np.float32).reshape(rows, inner)
+    ref = oracle.layer_norm(x.astype(np.float32).reshape(rows, inner), g, b, eps=1e-5)
+    assert max_rel(got, ref) <= (1e-4 if dt == F32 else 2e-3)
+
+
+UN = {"Sigmoid": 0, "Sqrt": 1, "Neg": 2, "Abs": 3, "Sin": 4, "Cos": 5, "Exp": 6, "Log": 7,
+      "SiLU": 8, "GELU": 9, "Erf": 10, "GELU_TANH": 11}
+
+
+@pytest.mark.parametrize("op", list(UN))
+def test_unary_kat(dev, op):
+    import drawinstant
+    n = 1024
+    x = np.array([(i - n / 2) / (n / 4) for i in range(n)], np.float32)  # wgsl-ops-test.js:40
+    bx, y = _up(dev, x), dev.create_buffer(x.nbytes)
+    drawinstant.call("di_unary", dev.ctx, UN[op], bx.handle, y.handle, n, F32)
+    assert max_rel(dev.download(y), oracle.unary(op, x)) <= 1e-4  # reference gate :29-34
+
+
+BIN = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Pow": 4, "Max": 5, "Min": 6}
+
+
+@pytest.mark.parametrize("op", list(BIN))
+def test_binary_kat(dev, op):
+    import drawinstant
+    n = 512
+    a = np.array([(i + 1) * 0.1 for i in range(n)], np.float32)            # :80
+    b = np.array([math.sin(i * 0.1) + 1.5 for i in range(n)], np.float32)
+    if op == "Pow":
+        a = (a - 20).astype(np.float32)
+        b = np.round(b * 2).astype(np.float32)
+    ba, bb, y = _up(dev, a), _up(dev, b), dev.create_buffer(a.nbytes)
+    drawinstant.call("di_binary", dev.ctx, BIN[op], ba.handle, bb.handle, y.handle, n, F32)
+    ref = oracle.binary(op, a, b)
+    assert max_rel(dev.download(y), ref) <= 1e-4 * (np.abs(ref).max() if op == "Pow" else 1)
+
+
+def test_binary_bcast_temb_add(dev, rng):
+    """The ResNet temb add h[1,C,H,W] + t[1,C,1,1] through the broadcast kernel."""
+    import drawinstant
+    C, H, W = 640, 32, 32
+    h = rng.standard_normal((1, C, H, W)).astype(np.float32)
+    t = rng.standard_normal((1, C, 1, 1)).astype(np.float32)
+    dims = np.array([1, C, H, W], np.uint32)
+    as_ = np.array([C * H * W, H * W, W, 1], np.uint32)
+    bs = np.array([0, 1, 0, 0], np.uint32)
+    bh, bt, y = _up(dev, h), _up(dev, t), dev.create_buffer(h.nbytes)
+    p = lambda a: a.ctypes.data_as(__import__("ctypes").POINTER(__import__("ctypes").c_uint32))
+    drawinstant.call("di_binary_bcast", dev.ctx, 0, bh.handle, bt.handle, y.handle, 4, p(dims),
+                     p(as_), p(bs), h.size, F32)
+    assert max_rel(dev.download(y).reshape(h.shape), h + t) <= 1e-6
+
+
+def test_softmax_reduce_resize_pow(dev, rng):
+    import ctypes
+    import drawinstant
+    x = np.array([math.sin(i * 0.1) * 2 for i in range(4 * 64)], np.float32)  # :105
+    bx, y = _up(dev, x), dev.create_buffer(x.nbytes)
+    drawinstant.call("di_softmax", dev.ctx, bx.handle, y.handle, 64, 4, F32)
+    assert max_rel(dev.download(y).reshape(4, 64), oracle.softmax(x.reshape(4, 64))) <= 1e-4
+    s = rng.standard_normal((4096, 77)).astype(np.float32) * 4
+    bs, ys = _up(dev, s), dev.create_buffer(s.nbytes)
+    drawinstant.call("di_softmax", dev.ctx, bs.handle, ys.handle, 77, 4096, F32)
+    assert max_rel(dev.download(ys).reshape(s.shape), oracle.softmax(s)) <= 1e-4
+    r = dev.create_buffer(4096 * 4)
+    drawinstant.call("di_reduce_mean", dev.ctx, bs.handle, r.handle, 77, 4096, F32)
+    assert max_rel(dev.download(r), oracle.reduce_mean(s)[:, 0]) <= 1e-4
+    img = np.array([math.sin(i * 0.3) for i in range(3 * 16)], np.float32)  # :394
+    bi, yi = _up(dev, img), dev.create_buffer(3 * 64 * 4)
+    drawinstant.call("di_resize_nearest", dev.ctx, bi.handle, yi.handle, 3, 4, 4, 8, 8, F32)
+    np.testing.assert_array_equal(dev.download(yi).reshape(3, 8, 8),
+                                  oracle.resize_nearest(img.reshape(3, 4, 4), 8, 8))
+    for e in (2.0, 3.0, 0.5):
+        v = np.array([(i - 128) / 32 for i in range(256)], np.float32)       # :418
+        bv, yv = _up(dev, v), dev.create_buffer(v.nbytes)
+        drawinstant.call("di_pow_scalar", dev.ctx, bv.handle, yv.handle, 256, e, F32)
+        assert max_rel(dev.download(yv), oracle.pow_scalar(v, e)) <= 1e-4
+
+
+def test_transpose_slice_concat_exact(dev, rng):
+    import ctypes
+    import drawinstant
+    p = lambda a: np.ascontiguousarray(a, np.uint32).ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+    x = rng.standard_normal((2, 5, 6, 7)).astype(np.float32)
+    bx = _up(dev, x)
+    perm = (0, 2, 3, 1)
+    out = x.transpose(perm)
+    y = dev.create_buffer(x.nbytes)
+    drawinstant.call("di_transpose", dev.ctx, bx.handle, y.handle, 4, p(out.shape),
+                     p([210, 42, 7, 1]), p(perm), x.size, F32)
+    np.testing.assert_array_equal(dev.download(y).reshape(out.shape), out)
+    sl = x[:, 1:4, 2:6, 3:5]
+    ys = dev.create_buffer(sl.nbytes)
+    drawinstant.call("di_slice", dev.ctx, bx.handle, ys.handle, 4, p(sl.shape), p([210, 42, 7, 1]),
+                     p([0, 1, 2, 3]), sl.size, F32)
+    np.testing.assert_array_equal(dev.download(ys).reshape(sl.shape), sl)
+    a = rng.standard_normal((3, 4)).astype(np.float32)
+    b = rng.standard_normal((3, 2)).astype(np.float32)
+    yc = dev.create_buffer(3 * 6 * 4)
+    drawinstant.call("di_concat_copy", dev.ctx, _up(dev, a).handle, yc.handle, 4, 6, 0, 12, F32)
+    drawinstant.call("di_concat_copy", dev.ctx, _up(dev, b).handle, yc.handle, 2, 6, 4, 6, F32)
+    np.testing.assert_array_equal(dev.download(yc).reshape(3, 6), np.concatenate([a, b], 1))
+
+
+def test_convert_and_layout_exact(dev, rng):
+    import drawinstant
+    x = (rng.standard_normal((2, 37, 9, 11)) * 100).astype(np.float32)
+    bx = _up(dev, x)
+    h = dev.create_buffer(x.size * 2)
+    drawinstant.call("di_convert", dev.ctx, bx.handle, F32, h.handle, F16, x.size)
+    np.testing.assert_array_equal(dev.download(h, np.float16).reshape(x.shape),
+                                  x.astype(np.float16))  # RNE
+    t = dev.create_buffer(x.size * 2)
+    drawinstant.call("di_layout_convert", dev.ctx, bx.handle, F32, NCHW, t.handle, F16, NHWC,
+                     2, 37, 9, 11)
+    np.testing.assert_array_equal(dev.download(t, np.float16).reshape(2, 9, 11, 37),
+                                  x.astype(np.float16).transpose(0, 2, 3, 1))
+    back = dev.create_buffer(x.nbytes)
+    drawinstant.call("di_layout_convert", dev.ctx, t.handle, F16, NHWC, back.handle, F32, NCHW,
+                     2, 37, 9, 11)
+    np.testing.assert_array_equal(dev.download(back).reshape(x.shape),
+                                  x.astype(np.float16).astype(np.float32))
+
+
+def test_fill_normal_matches_oracle_generator(dev):
+    n = 1 << 20
+    b = dev.create_buffer(n * 4)
+    dev.fill_normal(b, n, 2024, 0.0, 1.0)
+    got = dev.download(b)
+    ref = oracle.fill_normal(n, 2024)
+    # fp64 log/cos on the GPU and in libm may differ in the last bit; after
+    # rounding to fp32 the streams agree to 1 ulp.
+    np.testing.assert_allclose(got, ref, rtol=2.5e-7, atol=1e-7)
+
+
+def test_validation_errors(dev):
+    import drawinstant
+    from drawinstant import DiError
+    x = dev.create_buffer(64 * 4)
+    with pytest.raises(DiError) as e:  # C % G (wgsl-executor.js:732)
+        drawinstant.call("di_gn_silu", dev.ctx, x.handle, x.handle, x.handle, x.handle, 1, 10, 3,
+                         1, 1e-5, F32, NCHW)
+    assert "not divisible" in str(e.value)
+    with pytest.raises(DiError) as e:  # buffer too small
+        drawinstant.call("di_layer_norm", dev.ctx, x.handle, x.handle, x.handle, x.handle, 8, 16,
+                         1e-5, F32)
+    assert e.value.code == 1
+    x.destroy()
+    with pytest.raises(DiError) as e:  # freed handle
+        drawinstant.call("di_unary", dev.ctx, 0, x.handle, x.handle, 4, F32)
+    assert e.value.code == 5
+    st = dev.pool_stats()
+    assert st["peak"] >= st["live"] and st["allocs"] >= 1
