@@ -1,0 +1,58 @@
+// Argument block and launch API of the MFMA GEMM / implicit-GEMM conv kernel
+// (k_gemm.hip).  Raw device pointers; callers validate shapes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace di {
+
+enum AMode { A_DENSE = 0, A_CONV_NHWC = 1, A_CONV_NCHW = 2 };
+enum BMode { B_NK = 0, B_KN = 1 };
+enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_GEGLU = 2, ACT_SILU = 3 };
+enum TileCfg { TILE_64x64 = 0, TILE_128x64 = 1, TILE_64x128 = 2, TILE_128x128 = 3 };
+
+struct GemmArgs {
+  // ---- A operand ----
+  const void* a = nullptr;
+  const void* a2 = nullptr;  // second source: k (dense) or channel (conv) >= c1
+  uint64_t lda = 0, lda2 = 0;  // row / pixel stride in elements
+  uint64_t sa = 0, sa2 = 0;    // batch stride in elements
+  uint32_t c1 = 0;             // split point (0 with a2 == nullptr: single source)
+  // conv geometry (A_CONV_*): source H x W, input upsampled by `up` (1 or 2)
+  uint32_t Cin = 0, H = 0, W = 0, Ho = 0, Wo = 0, ks = 1, stride = 1, pad = 0, up = 1;
+  // ---- B operand: B_NK = [N][K] (torch Linear / OHWI conv), B_KN = [K][N] ----
+  const void* b = nullptr;
+  uint64_t ldb = 0, sb = 0;
+  // ---- problem ----
+  uint32_t M = 0, N = 0, K = 0, batch = 1;
+  uint32_t splits = 1, k_split = 0;
+  uint32_t a_vec_ok = 1, b_vec_ok = 1;  // 16-byte vector loads legal
+  // ---- epilogue ----
+  float alpha = 1.0f;
+  const float* bias = nullptr;   // [N]
+  const float* bias2 = nullptr;  // [(m / rows_b2)][ld_b2]
+  uint32_t rows_b2 = 0, ld_b2 = 0;
+  const void* res = nullptr;  // residual, same layout as C (NHWC rows)
+  uint64_t ldr = 0, sr = 0;
+  int res_f32 = 0;
+  int act = ACT_NONE;
+  void* c = nullptr;
+  uint64_t ldc = 0, sc = 0;
+  int c_f32 = 0;
+  int c_nchw = 0;     // store C[(img*N + n)*c_hw + p] with m = img*c_hw + p
+  uint32_t c_hw = 1;
+  float* part = nullptr;  // split-K partials [splits][batch][M][N]
+};
+
+int gemm_pick_tile(const GemmArgs& g, int num_cus);
+uint32_t gemm_pick_splits(const GemmArgs& g, int tile_cfg, int num_cus);
+uint64_t gemm_ws_bytes(const GemmArgs& g);
+// elem: DI_F16 or DI_F32 operand element type.
+void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s);
+// OIHW (any dtype) -> OHWI fp16 with optional zero channel padding Cin -> Cin_pad.
+void launch_repack_oihw_ohwi(hipStream_t s, const void* w, int wdt, void* out, uint32_t Cout,
+                             uint32_t Cin, uint32_t ks, uint32_t Cin_pad);
+
+}  // namespace di

@@ -68,6 +68,16 @@ typedef uint64_t di_handle;
 #define DI_BIN_MAX 5
 #define DI_BIN_MIN 6
 
+/* ---- epilogue activations of the contraction ops ---- */
+#define DI_ACT_NONE 0
+#define DI_ACT_GELU 1  /* erf GELU */
+#define DI_ACT_GEGLU 2 /* h * GELU(gate); weight rows interleaved in 16-row groups */
+#define DI_ACT_SILU 3
+
+/* ---- conv flags ---- */
+#define DI_CONV_F16_COMPUTE 1 /* NCHW fp32 tensors through the fp16 MFMA path */
+#define DI_CONV_UPSAMPLE2X 2  /* convolve the 2x nearest-upsampled input */
+
 /* ---- norm flags ---- */
 #define DI_NORM_SILU 1 /* apply x/(1+exp(-x)) after the affine (fused-resnet.js:162) */
 
@@ -206,6 +216,39 @@ int32_t di_instance_norm(di_ctx* ctx, di_handle X, di_handle gamma,
 int32_t di_layer_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
                       di_handle Y, uint32_t rows, uint32_t inner, float eps,
                       int32_t dtype);
+
+/* ======================= contractions (MFMA) ======================= */
+/* Per-channel parameters (bias) are fp32 buffers; 0 = absent. */
+
+/* matmul (wgsl-ops.js:477-569, OPS.MatMul wgsl-executor.js:1040-1054):
+ * Y[b] = A[b] (M x K) . B (K x N), B batched (offset b*K*N) iff b_batched.
+ * fp32 uses fp32 MFMA (exact fp32 products), fp16 the fp16 MFMA. */
+int32_t di_matmul(di_ctx* ctx, di_handle A, di_handle B, di_handle Y, uint32_t M,
+                  uint32_t N, uint32_t K, uint32_t batch, int32_t b_batched,
+                  int32_t dtype);
+/* gemm (wgsl-ops.js:821-910, OPS.Gemm wgsl-executor.js:1057-1065):
+ * Y = A . B (+transB) + C[col]; C fp32 (0 = none). */
+int32_t di_gemm(di_ctx* ctx, di_handle A, di_handle B, di_handle C, di_handle Y,
+                uint32_t M, uint32_t N, uint32_t K, int32_t trans_b, int32_t dtype);
+/* Linear in torch layout with the fused epilogue of fused-block.js WGSL_MATMUL
+ * (:54-115: GELU / residual hooks): Y = act(X[M,K] . W[N,K]^T + bias) + R.
+ * DI_ACT_GEGLU writes N/2 columns: out[:, 16t+j] = h * GELU(g) with h, g the
+ * results of weight rows 32t+j and 32t+16+j. */
+int32_t di_linear(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_handle R,
+                  di_handle Y, uint32_t M, uint32_t N, uint32_t K, int32_t act,
+                  int32_t dtype);
+/* Conv2d, square kernel K, stride S, symmetric pad (convMM wgsl-ops.js:584-711,
+ * OPS.Conv wgsl-executor.js:1068-1092; batch N >= 1, the reference computes
+ * batch 0 only).  Optional residual R (same shape as Y) added after the bias
+ * (fused-resnet.js WGSL_CONV :173-208 residual epilogue).
+ *   layout DI_NCHW: X NCHW, W OIHW, dtype fp32 (exact fp32 MFMA), or with
+ *                   DI_CONV_F16_COMPUTE fp16-in / fp32-acc MFMA;
+ *   layout DI_NHWC: X NHWC fp16, W OHWI fp16 ([Cout][K][K][Cin]), Cin % 8 == 0.
+ * DI_CONV_UPSAMPLE2X convolves the 2x nearest upsample of X (H, W are X's). */
+int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_handle R,
+                  di_handle Y, uint32_t N, uint32_t Cin, uint32_t Cout, uint32_t H,
+                  uint32_t Wd, uint32_t K, uint32_t S, uint32_t pad, int32_t flags,
+                  int32_t dtype, int32_t layout);
 
 #ifdef __cplusplus
 }

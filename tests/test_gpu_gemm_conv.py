@@ -1,0 +1,220 @@
+"""GPU parity of the MFMA contraction kernels (di_matmul / di_gemm /
+di_linear / di_conv2d) against the CPU oracle on identical inputs.
+
+Tolerances: fp32 paths (exact fp32 MFMA products, fp32 accumulation) use the
+reference KAT gate max-rel <= 1e-4.  fp16 paths are compared with the oracle
+run on the same fp16-rounded inputs, so only fp32 summation order and the
+fp16 rounding of the output differ: rel-L2 <= 2e-3 asserted (the north-star
+bar for MFMA contractions is rel-L2 <= 1e-2); max-abs is printed.
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import max_rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, NCHW, NHWC = 0, 1, 0, 1
+ACT = {"none": 0, "gelu": 1, "geglu": 2, "silu": 3}
+
+
+def _call(dev, fn, *a):
+    import drawinstant
+    drawinstant.call(fn, dev.ctx, *a)
+
+
+def _h(b):
+    return 0 if b is None else b.handle
+
+
+# ---------------- fp32 executor ops: reference KATs ----------------
+
+def test_matmul_kat(dev):
+    M, N, K = 32, 48, 24  # wgsl-ops-test.js:165-167
+    a = np.array([math.sin(i * 0.3) for i in range(M * K)], np.float32).reshape(M, K)
+    b = np.array([math.cos(i * 0.17) for i in range(K * N)], np.float32).reshape(K, N)
+    ba, bb, y = dev.storage(a), dev.storage(b), dev.create_buffer(M * N * 4)
+    _call(dev, "di_matmul", ba.handle, bb.handle, y.handle, M, N, K, 1, 0, F32)
+    assert max_rel(dev.download(y).reshape(M, N), oracle.matmul(a, b)) <= 1e-4
+
+
+@pytest.mark.parametrize("batched", [0, 1])
+def test_matmul_batched_kat(dev, batched):
+    Bt, M, N, K = 2, 20, 24, 12  # wgsl-ops-test.js:189-191, :213-215
+    a = np.array([math.sin(i * 0.21) for i in range(Bt * M * K)], np.float32).reshape(Bt, M, K)
+    nb = Bt * K * N if batched else K * N
+    b = np.array([math.cos(i * 0.13) for i in range(nb)], np.float32)
+    b = b.reshape((Bt, K, N) if batched else (K, N))
+    y = dev.create_buffer(Bt * M * N * 4)
+    _call(dev, "di_matmul", dev.storage(a).handle, dev.storage(b).handle, y.handle, M, N, K, Bt,
+          batched, F32)
+    assert max_rel(dev.download(y).reshape(Bt, M, N), oracle.matmul(a, b, bool(batched))) <= 1e-4
+
+
+@pytest.mark.parametrize("trans_b", [0, 1])
+def test_gemm_kat(dev, trans_b):
+    M, N, K = 16, 24, 12  # wgsl-ops-test.js:341-343, :367-369
+    a = np.array([math.sin(i * 0.1) for i in range(M * K)], np.float32).reshape(M, K)
+    b = np.array([math.cos(i * 0.15) for i in range(K * N)], np.float32)
+    b = b.reshape((N, K) if trans_b else (K, N))
+    c = np.array([0.01 * i for i in range(N)], np.float32)
+    y = dev.create_buffer(M * N * 4)
+    _call(dev, "di_gemm", dev.storage(a).handle, dev.storage(b).handle, dev.storage(c).handle,
+          y.handle, M, N, K, trans_b, F32)
+    assert max_rel(dev.download(y).reshape(M, N), oracle.gemm(a, b, c, bool(trans_b))) <= 1e-4
+
+
+def test_gemm_fp32_large_ragged(dev, rng):
+    M, N, K = 333, 1281, 77
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K)).astype(np.float32)
+    c = rng.standard_normal(N).astype(np.float32)
+    y = dev.create_buffer(M * N * 4)
+    _call(dev, "di_gemm", dev.storage(a).handle, dev.storage(b).handle, dev.storage(c).handle,
+          y.handle, M, N, K, 1, F32)
+    assert max_rel(dev.download(y).reshape(M, N), oracle.gemm(a, b, c, True)) <= 1e-4
+
+
+def test_conv3x3_kat(dev):
+    cin, cout, h, w = 3, 4, 8, 8  # wgsl-ops-test.js:239-243
+    x = np.array([math.sin(i * 0.2) for i in range(cin * h * w)], np.float32).reshape(1, cin, h, w)
+    wt = np.array([math.cos(i * 0.13) * 0.5 for i in range(cout * cin * 9)],
+                  np.float32).reshape(cout, cin, 3, 3)
+    bias = np.array([0.1 * i for i in range(cout)], np.float32)
+    y = dev.create_buffer(cout * h * w * 4)
+    _call(dev, "di_conv2d", dev.storage(x).handle, dev.storage(wt).handle, dev.storage(bias).handle,
+          0, y.handle, 1, cin, cout, h, w, 3, 1, 1, 0, F32, NCHW)
+    assert max_rel(dev.download(y).reshape(1, cout, h, w), oracle.conv2d(x, wt, bias)) <= 1e-4
+
+
+def test_conv1x1_kat(dev):
+    cin, cout, h, w = 8, 6, 4, 4  # wgsl-ops-test.js:275-279
+    x = np.array([math.sin(i * 0.1) for i in range(cin * h * w)], np.float32).reshape(1, cin, h, w)
+    wt = np.array([math.cos(i * 0.2) * 0.3 for i in range(cout * cin)],
+                  np.float32).reshape(cout, cin, 1, 1)
+    bias = np.array([0.05 * i for i in range(cout)], np.float32)
+    y = dev.create_buffer(cout * h * w * 4)
+    _call(dev, "di_conv2d", dev.storage(x).handle, dev.storage(wt).handle, dev.storage(bias).handle,
+          0, y.handle, 1, cin, cout, h, w, 1, 1, 0, 0, F32, NCHW)
+    assert max_rel(dev.download(y).reshape(1, cout, h, w), oracle.conv2d(x, wt, bias)) <= 1e-4
+
+
+def test_conv_fp32_stride2_batched_residual(dev, rng):
+    x = rng.standard_normal((2, 5, 9, 10)).astype(np.float32)
+    wt = rng.standard_normal((7, 5, 3, 3)).astype(np.float32)
+    bias = rng.standard_normal(7).astype(np.float32)
+    ref = oracle.conv2d(x, wt, bias, stride=2)
+    r = rng.standard_normal(ref.shape).astype(np.float32)
+    y = dev.create_buffer(ref.nbytes)
+    _call(dev, "di_conv2d", dev.storage(x).handle, dev.storage(wt).handle, dev.storage(bias).handle,
+          dev.storage(r).handle, y.handle, 2, 5, 7, 9, 10, 3, 2, 1, 0, F32, NCHW)
+    assert max_rel(dev.download(y).reshape(ref.shape), ref + r) <= 1e-4
+
+
+# ---------------- fp16 MFMA paths ----------------
+
+def _f16(a):
+    return np.asarray(a, np.float32).astype(np.float16)
+
+
+@pytest.mark.parametrize("M,N,K,act,res", [
+    (4096, 320, 320, "none", True),     # proj_in / to_out + residual
+    (4096, 960, 320, "none", False),    # fused QKV
+    (4096, 2560, 320, "geglu", False),  # GEGLU proj (64x64 level)
+    (4096, 320, 1280, "none", True),    # FF out + residual
+    (77, 640, 1024, "none", False),     # cross-attn K/V from context
+    (64, 1280, 5120, "none", True),     # 8x8 level FF out (split-K)
+    (256, 10240, 1280, "geglu", False), # 16x16 level GEGLU
+    (100, 96, 40, "gelu", False),       # ragged M, N, K % 8 == 0
+    (1, 1280, 1280, "silu", False),     # GEMV-shaped
+])
+def test_linear_fp16(dev, rng, M, N, K, act, res):
+    print(f"[linear f16] M={M} N={N} K={K} act={act}", flush=True)
+    x = _f16(rng.standard_normal((M, K)))
+    w = _f16(rng.standard_normal((N, K)) * math.sqrt(1.0 / K))
+    b = (0.01 * rng.standard_normal(N)).astype(np.float32)
+    nout = N // 2 if act == "geglu" else N
+    r = _f16(rng.standard_normal((M, nout))) if res else None
+    y = dev.create_buffer(M * nout * 2)
+    br = dev.storage(r) if res else None
+    _call(dev, "di_linear", dev.storage(x).handle, dev.storage(w).handle, dev.storage(b).handle,
+          _h(br), y.handle, M, N, K, ACT[act], F16)
+    got = dev.download(y, np.float16).astype(np.float32).reshape(M, nout)
+    full = oracle.linear(x.astype(np.float32), w.astype(np.float32), b)
+    if act == "geglu":
+        grp = full.reshape(M, N // 32, 2, 16)
+        ref = grp[:, :, 0, :].reshape(M, nout) * oracle.unary("GELU", grp[:, :, 1, :].reshape(M, nout))
+    elif act == "gelu":
+        ref = oracle.unary("GELU", full)
+    elif act == "silu":
+        ref = oracle.unary("SiLU", full)
+    else:
+        ref = full
+    if res:
+        ref = ref + r.astype(np.float32)
+    err = rel_l2(got, ref)
+    print(f"   rel-L2 {err:.2e} max-abs {np.max(np.abs(got - ref)):.2e}", flush=True)
+    assert err <= 2e-3
+
+
+def _conv_case(dev, rng, n, cin, cout, h, w, k, s, pad, up=1, res=False, cin_pad=None):
+    """NHWC fp16 conv vs the oracle's NCHW conv on the same fp16 values."""
+    x = _f16(rng.standard_normal((n, h, w, cin)))
+    wt = _f16(rng.standard_normal((cout, k, k, cin)) * math.sqrt(2.0 / (cin * k * k)))
+    bias = (0.01 * rng.standard_normal(cout)).astype(np.float32)
+    hi, wi = h * up, w * up
+    ho, wo = (hi + 2 * pad - k) // s + 1, (wi + 2 * pad - k) // s + 1
+    r = _f16(rng.standard_normal((n, ho, wo, cout))) if res else None
+    y = dev.create_buffer(n * ho * wo * cout * 2)
+    flags = 2 if up == 2 else 0
+    _call(dev, "di_conv2d", dev.storage(x).handle, dev.storage(wt).handle, dev.storage(bias).handle,
+          _h(dev.storage(r) if res else None), y.handle, n, cin, cout, h, w, k, s, pad, flags, F16,
+          NHWC)
+    got = dev.download(y, np.float16).astype(np.float32).reshape(n, ho, wo, cout)
+    xin = x.astype(np.float32).transpose(0, 3, 1, 2)
+    if up == 2:
+        xin = xin.repeat(2, axis=2).repeat(2, axis=3)
+    ref = oracle.conv2d(xin, wt.astype(np.float32).transpose(0, 3, 1, 2), bias, stride=s, pad=pad)
+    ref = ref.transpose(0, 2, 3, 1)
+    if res:
+        ref = ref + r.astype(np.float32)
+    err = rel_l2(got, ref)
+    print(f"   rel-L2 {err:.2e} max-abs {np.max(np.abs(got - ref)):.2e}", flush=True)
+    return err
+
+
+@pytest.mark.parametrize("n,cin,cout,h,w,k,s,pad,up,res", [
+    (1, 320, 320, 64, 64, 3, 1, 1, 1, False),   # cfg2 shape
+    (1, 320, 640, 32, 32, 3, 1, 1, 1, False),   # cfg3 conv1
+    (1, 640, 640, 32, 32, 3, 1, 1, 1, True),    # cfg3 conv2 + skip residual
+    (1, 320, 640, 32, 32, 1, 1, 0, 1, False),   # cfg3 1x1 skip
+    (1, 320, 320, 64, 64, 3, 2, 1, 1, False),   # Downsample2D
+    (1, 1280, 1280, 8, 8, 3, 1, 1, 2, False),   # Upsample2D conv (fused 2x nearest)
+    (1, 2560, 1280, 8, 8, 3, 1, 1, 1, False),   # up0 resnet conv1 (8x8, split-K)
+    (2, 64, 48, 7, 9, 3, 1, 1, 1, True),        # batch 2, ragged
+    (1, 8, 320, 64, 64, 3, 1, 1, 1, False),     # conv_in (channels padded to 8)
+    (1, 320, 8, 64, 64, 3, 1, 1, 1, False),     # conv_out (padded to 8)
+])
+def test_conv_nhwc_fp16(dev, rng, n, cin, cout, h, w, k, s, pad, up, res):
+    print(f"[conv f16] n={n} cin={cin} cout={cout} {h}x{w} k={k} s={s} up={up}", flush=True)
+    assert _conv_case(dev, rng, n, cin, cout, h, w, k, s, pad, up, res) <= 2e-3
+
+
+def test_conv_nchw_f32_via_f16_compute_cfg2(dev, rng):
+    """cfg2: fp32 NCHW tensors, fp16-in / fp32-acc MFMA (DI_CONV_F16_COMPUTE);
+    compared with the fp32 oracle on the unrounded fp32 inputs: rel-L2 <= 1e-2."""
+    x = rng.standard_normal((1, 320, 64, 64)).astype(np.float32)
+    wt = (rng.standard_normal((320, 320, 3, 3)) * math.sqrt(2.0 / 2880)).astype(np.float32)
+    bias = (0.01 * rng.standard_normal(320)).astype(np.float32)
+    y = dev.create_buffer(x.nbytes)
+    _call(dev, "di_conv2d", dev.storage(x).handle, dev.storage(wt).handle, dev.storage(bias).handle,
+          0, y.handle, 1, 320, 320, 64, 64, 3, 1, 1, 1, F32, NCHW)
+    got = dev.download(y).reshape(x.shape)
+    ref = oracle.conv2d(x, wt, bias)
+    err = rel_l2(got, ref)
+    print(f"   cfg2 rel-L2 {err:.2e} max-abs {np.max(np.abs(got - ref)):.2e}", flush=True)
+    assert err <= 1e-2
