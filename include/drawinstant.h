@@ -78,6 +78,10 @@ typedef uint64_t di_handle;
 #define DI_CONV_F16_COMPUTE 1 /* NCHW fp32 tensors through the fp16 MFMA path */
 #define DI_CONV_UPSAMPLE2X 2  /* convolve the 2x nearest-upsampled input */
 
+/* ---- attention tensor layouts ---- */
+#define DI_ATTN_BSHD 0 /* [B, S, H, d]: fused-attn.js:69-70 */
+#define DI_ATTN_BHSD 1 /* [B, H, S, d]: fused-cross-attn.js:51-52 */
+
 /* ---- norm flags ---- */
 #define DI_NORM_SILU 1 /* apply x/(1+exp(-x)) after the affine (fused-resnet.js:162) */
 
@@ -249,6 +253,32 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_hand
                   di_handle Y, uint32_t N, uint32_t Cin, uint32_t Cout, uint32_t H,
                   uint32_t Wd, uint32_t K, uint32_t S, uint32_t pad, int32_t flags,
                   int32_t dtype, int32_t layout);
+
+/* ======================= attention ======================= */
+/* Flash attention, head dim d = 64, online softmax (no score matrix).  scale
+ * <= 0 selects 1/sqrt(d).  fp16 tensors run directly; fp32 tensors are staged
+ * through fp16 MFMA operands (fp32 accumulation and output). */
+
+/* softmax(Q K^T * scale) V over S keys: WGSL_FUSED_ATTN (fused-attn.js:199-307,
+ * runAttnBench :364-476) and the executor's MatMul -> Softmax -> MatMul chain. */
+int32_t di_attn_self(di_ctx* ctx, di_handle Q, di_handle K, di_handle V, di_handle O,
+                     uint32_t B, uint32_t H, uint32_t S, uint32_t d, int32_t layout,
+                     float scale, int32_t dtype);
+/* Cross attention over Skv keys (e.g. 77 text tokens): WGSL_FUSED
+ * (fused-cross-attn.js:112-173, runCrossAttnBench :220-318). */
+int32_t di_attn_cross(di_ctx* ctx, di_handle Q, di_handle K, di_handle V, di_handle O,
+                      uint32_t B, uint32_t H, uint32_t Sq, uint32_t Skv, uint32_t d,
+                      int32_t layout, float scale, int32_t dtype);
+
+/* ======================= timestep embedding ======================= */
+
+/* fused-tembed.js (WGSL_SINEMB :28-44, WGSL_FUSED :73-130, runTEmbedBench
+ * :175-267): emb = [cos(t f) || sin(t f)], f_i = exp(-ln(1e4) i / (emb_dim/2)),
+ * Y = W2 SiLU(W1 emb + b1) + b2.  T: fp32 [B] timesteps; W1 [hid][emb_dim],
+ * W2 [hid][hid] of dtype wdtype; biases and Y fp32.  B <= 8, dims <= 1280. */
+int32_t di_tembed(di_ctx* ctx, di_handle T, di_handle W1, di_handle b1, di_handle W2,
+                  di_handle b2, di_handle Y, uint32_t B, uint32_t emb_dim, uint32_t hid,
+                  int32_t wdtype);
 
 #ifdef __cplusplus
 }
