@@ -1,0 +1,122 @@
+// Block compositions of the SD2.1 U-Net on the gfx950 kernels (blocks.cpp):
+// ResnetBlock2D and Transformer2DModel (linear projection, one
+// BasicTransformerBlock), on NHWC fp16 activations.
+#pragma once
+
+#include <cstdint>
+
+#include "di_device.h"
+#include "di_internal.h"
+#include "di_kernels.h"
+
+namespace di {
+
+// Stream-ordered scratch allocation from the context pool; released (to the
+// pool, not the driver) when the owner goes out of scope.  Safe because all
+// work is on the context's single in-order stream.
+struct Scratch {
+  Ctx* c = nullptr;
+  void* p = nullptr;
+  uint64_t cap = 0;
+  Scratch() = default;
+  Scratch(const Scratch&) = delete;
+  Scratch& operator=(const Scratch&) = delete;
+  Scratch(Scratch&& o) noexcept : c(o.c), p(o.p), cap(o.cap) { o.p = nullptr; }
+  Scratch& operator=(Scratch&& o) noexcept {
+    if (this != &o) {
+      release();
+      c = o.c;
+      p = o.p;
+      cap = o.cap;
+      o.p = nullptr;
+    }
+    return *this;
+  }
+  int alloc(Ctx* ctx, uint64_t bytes) {
+    c = ctx;
+    return pool_alloc(ctx, bytes, &p, &cap);
+  }
+  void release() {
+    if (p) pool_release(c, p, cap);
+    p = nullptr;
+  }
+  ~Scratch() { release(); }
+  f16* h() const { return (f16*)p; }
+  float* f() const { return (float*)p; }
+};
+
+struct ResnetW {
+  const float *n1_g = nullptr, *n1_b = nullptr;
+  const f16* c1_w = nullptr;  // OHWI [Cout][3][3][Cin]
+  const float* c1_b = nullptr;
+  const float *n2_g = nullptr, *n2_b = nullptr;
+  const f16* c2_w = nullptr;  // OHWI [Cout][3][3][Cout]
+  const float* c2_b = nullptr;
+  const f16* sk_w = nullptr;  // 1x1 [Cout][Cin], null when Cin == Cout
+  const float* sk_b = nullptr;
+};
+
+struct ResnetShape {
+  uint32_t B, H, W, Cin, Cout, groups;
+  float eps;
+};
+
+// out[B][HW][Cout] = conv2(SiLU(GN2(conv1(SiLU(GN1(x))) + temb))) + skip(x).
+// x is a channel concat of one or two NHWC sources.  temb: fp32 rows per
+// image, temb[b * ld_temb + c] (already offset to this block), may be null.
+int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x,
+                   const float* temb, uint32_t ld_temb, f16* out);
+
+struct TransformerW {
+  const float *n_g = nullptr, *n_b = nullptr;       // GroupNorm
+  const f16* pin_w = nullptr;                        // proj_in [C][C]
+  const float* pin_b = nullptr;
+  const float *ln1_g = nullptr, *ln1_b = nullptr;
+  const f16* qkv_w = nullptr;  // [3C][C] = to_q ; to_k ; to_v (no bias)
+  const f16* o1_w = nullptr;   // attn1.to_out.0 [C][C]
+  const float* o1_b = nullptr;
+  const float *ln2_g = nullptr, *ln2_b = nullptr;
+  const f16* q2_w = nullptr;   // attn2.to_q [C][C]
+  const f16* kv2_w = nullptr;  // [2C][cross] = to_k ; to_v
+  const f16* o2_w = nullptr;
+  const float* o2_b = nullptr;
+  const float *ln3_g = nullptr, *ln3_b = nullptr;
+  const f16* ff1_w = nullptr;  // GEGLU proj [8C][C], rows in 32-groups [16 h | 16 gate]
+  const float* ff1_b = nullptr;
+  const f16* ff2_w = nullptr;  // [C][4C]
+  const float* ff2_b = nullptr;
+  const f16* pout_w = nullptr;  // proj_out [C][C]
+  const float* pout_b = nullptr;
+};
+
+struct TransformerShape {
+  uint32_t B, H, W, C, Sctx, cross, groups;
+  float gn_eps, ln_eps;
+};
+
+// out = proj_out(block(proj_in(GN(x)))) + x; context fp16 [B][Sctx][cross].
+int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s, const f16* x,
+                        const f16* context, f16* out);
+
+// NHWC conv through the implicit-GEMM kernel (fp16 in, fp16 or NCHW fp32 out).
+struct ConvCall {
+  NhwcSrc x;
+  uint32_t B, H, W, Cin, Cout, ks = 3, stride = 1, pad = 1, up = 1;
+  const f16* w = nullptr;
+  const float* bias = nullptr;
+  const float* bias2 = nullptr;
+  uint32_t rows_b2 = 0, ld_b2 = 0;
+  const f16* res = nullptr;
+  uint64_t ldr = 0;
+  void* y = nullptr;
+  uint64_t ldc = 0;
+  int y_nchw_f32 = 0;
+};
+int conv_nhwc(Ctx* c, const ConvCall& cc);
+
+// Linear on token rows: y = act(x w^T + b) (+ res); fp16.
+int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const f16* w,
+               uint32_t N, const float* b, int act, const f16* res, uint64_t ldr, f16* y,
+               uint64_t ldy);
+
+}  // namespace di

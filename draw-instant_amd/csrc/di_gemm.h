@@ -10,7 +10,7 @@ namespace di {
 
 enum AMode { A_DENSE = 0, A_CONV_NHWC = 1, A_CONV_NCHW = 2 };
 enum BMode { B_NK = 0, B_KN = 1 };
-enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_GEGLU = 2, ACT_SILU = 3 };
+enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_GEGLU = 2, ACT_SILU = 3, ACT_GELU_TANH = 4 };
 enum TileCfg { TILE_64x64 = 0, TILE_128x64 = 1, TILE_64x128 = 2, TILE_128x128 = 3 };
 
 struct GemmArgs {

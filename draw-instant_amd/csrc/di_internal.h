@@ -52,6 +52,10 @@ struct Ctx {
   // never need clearing (and no memset is ever recorded into a graph).
   // Word 0 is the fault flag: set by a kernel whose bounded wait expired.
   uint32_t* sync_words = nullptr;
+  // While set (graph capture), pool_release parks buffers in `held` instead
+  // of the free list; the capturing owner takes them over.
+  bool hold_releases = false;
+  std::vector<std::pair<void*, uint64_t>> held;
 };
 
 constexpr uint32_t kSyncWords = 1u << 18;  // 1 MiB

@@ -7,6 +7,7 @@
 
 #include <cstdint>
 
+#include "di_device.h"
 #include "di_internal.h"
 
 namespace di {
@@ -32,10 +33,21 @@ int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const floa
 // `ws` needs gn_nhwc_ws_floats() floats; `sync` = Ctx::sync_words.
 uint32_t gn_nhwc_chunks(uint32_t HW, uint32_t C);
 uint64_t gn_nhwc_ws_floats(uint32_t N, uint32_t C, uint32_t G, uint32_t HW);
-void launch_group_norm_nhwc(hipStream_t s, const void* x, const float* gamma,
-                            const float* beta, void* y, uint32_t N, uint32_t C,
-                            uint32_t G, uint32_t HW, float eps, bool silu, float* ws,
-                            uint32_t* sync);
+// Channel concat of two NHWC fp16 sources: channel c < c1 from p1 (pixel
+// stride ld1), else channel c - c1 from p2 (pixel stride ld2); c1 % 8 == 0.
+struct NhwcSrc {
+  const f16* p1;
+  const f16* p2;
+  uint32_t c1;
+  uint64_t ld1, ld2;
+  __device__ __forceinline__ f16x8 load8(uint64_t pix, uint32_t c) const {
+    return c < c1 ? *(const f16x8*)(p1 + pix * ld1 + c)
+                  : *(const f16x8*)(p2 + pix * ld2 + (c - c1));
+  }
+};
+void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const float* beta,
+                            void* y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW,
+                            float eps, bool silu, float* ws, uint32_t* sync);
 void launch_layer_norm(hipStream_t s, const void* x, const float* gamma,
                        const float* beta, void* y, uint32_t rows, uint32_t inner,
                        float eps, int dt);

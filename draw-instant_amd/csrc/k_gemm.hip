@@ -84,6 +84,7 @@ __device__ __forceinline__ float epi_value(const GemmArgs& g, uint32_t bz, uint3
 __device__ __forceinline__ float apply_act(int act, float v) {
   if (act == ACT_GELU) return gelu_erf_f(v);
   if (act == ACT_SILU) return silu_f(v);
+  if (act == ACT_GELU_TANH) return gelu_tanh_f(v);
   return v;
 }
 

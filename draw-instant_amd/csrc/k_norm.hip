@@ -267,15 +267,13 @@ constexpr int kMaxKV = 2;  // C <= 4096
 // grid (chunks, N). Per-channel partial sums of pixel chunk -> per-group
 // partials; the last workgroup of image n folds all chunks into mean/rstd.
 __global__ __launch_bounds__(256) void k_gn_nhwc_stats(
-    const f16* __restrict__ x, uint32_t C, uint32_t G, uint32_t HW, uint32_t ppc, float eps,
+    NhwcSrc x, uint32_t C, uint32_t G, uint32_t HW, uint32_t ppc, float eps,
     float* __restrict__ part /*[N][chunks][G][2]*/, float* __restrict__ stats /*[N][G][2]*/,
     uint32_t* __restrict__ sync) {
-  extern __shared__ float csh[];  // [2*C] per-channel sum / sumsq
+  extern __shared__ float csh[];  // [R][2][C] per pixel-lane, per-channel sum / sumsq
   __shared__ bool last;
   const uint32_t chunk = blockIdx.x, n = blockIdx.y, chunks = gridDim.x;
   const NhwcMap m = nhwc_map(C);
-  for (uint32_t i = threadIdx.x; i < 2 * C; i += 256) csh[i] = 0.0f;
-  __syncthreads();
   const uint32_t p0 = chunk * ppc, p1 = min(p0 + ppc, HW);
   const uint32_t lane_cv = threadIdx.x % m.cvb, pl = threadIdx.x / m.cvb;
   if (pl < m.R) {
@@ -284,13 +282,13 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_stats(
     for (int k = 0; k < kMaxKV; k++)
 #pragma unroll
       for (int j = 0; j < 8; j++) s[k][j] = q[k][j] = 0.0f;
-    const f16* xn = x + (uint64_t)n * HW * C;
     for (uint32_t p = p0 + pl; p < p1; p += m.R) {
+      const uint64_t pix = (uint64_t)n * HW + p;
 #pragma unroll
       for (int k = 0; k < kMaxKV; k++) {
         uint32_t cv = lane_cv + k * m.cvb;
         if (k < (int)m.kv && cv < m.CV) {
-          f16x8 v = *(const f16x8*)(xn + (uint64_t)p * C + cv * 8);
+          f16x8 v = x.load8(pix, cv * 8);
 #pragma unroll
           for (int j = 0; j < 8; j++) {
             float f = (float)v[j];
@@ -300,14 +298,15 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_stats(
         }
       }
     }
+    // every (pixel-lane, channel) slot is written by exactly one thread
 #pragma unroll
     for (int k = 0; k < kMaxKV; k++) {
       uint32_t cv = lane_cv + k * m.cvb;
       if (k < (int)m.kv && cv < m.CV) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          atomicAdd(&csh[cv * 8 + j], s[k][j]);
-          atomicAdd(&csh[C + cv * 8 + j], q[k][j]);
+          csh[(pl * 2) * C + cv * 8 + j] = s[k][j];
+          csh[(pl * 2 + 1) * C + cv * 8 + j] = q[k][j];
         }
       }
     }
@@ -317,10 +316,11 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_stats(
   if (threadIdx.x < G) {
     uint32_t g = threadIdx.x;
     float a = 0.0f, b = 0.0f;
-    for (uint32_t c = g * cpg; c < (g + 1) * cpg; c++) {
-      a += csh[c];
-      b += csh[C + c];
-    }
+    for (uint32_t r = 0; r < m.R; r++)  // fixed order: deterministic
+      for (uint32_t c = g * cpg; c < (g + 1) * cpg; c++) {
+        a += csh[(r * 2) * C + c];
+        b += csh[(r * 2 + 1) * C + c];
+      }
     float* pp = part + (((uint64_t)n * chunks + chunk) * G + g) * 2;
     st_relaxed_f(pp, a);
     st_relaxed_f(pp + 1, b);
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_stats(
 // grid (chunks, N): y = x * a[c] + b[c] (+SiLU) with a = rstd*gamma,
 // b = beta - mean*rstd*gamma folded per channel in LDS.
 __global__ __launch_bounds__(256) void k_gn_nhwc_apply(
-    const f16* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    NhwcSrc x, const float* __restrict__ gamma, const float* __restrict__ beta,
     f16* __restrict__ y, uint32_t C, uint32_t G, uint32_t HW, uint32_t ppc, int silu,
     const float* __restrict__ stats) {
   extern __shared__ float ab[];  // [2*C]
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply(
   for (uint32_t i = threadIdx.x; i < nv; i += 256) {
     uint32_t cv = i % CV;
     uint64_t off = base + (uint64_t)i * 8;
-    f16x8 v = *(const f16x8*)(x + off);
+    f16x8 v = x.load8((uint64_t)n * HW + p0 + i / CV, cv * 8);
     f16x8 o;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -524,18 +524,18 @@ uint64_t gn_nhwc_ws_floats(uint32_t N, uint32_t C, uint32_t G, uint32_t HW) {
   return (uint64_t)N * gn_nhwc_chunks(HW, C) * G * 2 + (uint64_t)N * G * 2;
 }
 
-void launch_group_norm_nhwc(hipStream_t s, const void* x, const float* gamma,
-                            const float* beta, void* y, uint32_t N, uint32_t C, uint32_t G,
-                            uint32_t HW, float eps, bool silu, float* ws, uint32_t* sync) {
+void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const float* beta,
+                            void* y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW, float eps,
+                            bool silu, float* ws, uint32_t* sync) {
   uint32_t chunks = gn_nhwc_chunks(HW, C);
   uint32_t ppc = (HW + chunks - 1) / chunks;
   float* part = ws;
   float* stats = ws + (uint64_t)N * chunks * G * 2;
+  const NhwcMap m = nhwc_map(C);
   size_t lds = 2 * C * sizeof(float);
-  k_gn_nhwc_stats<<<dim3(chunks, N), 256, lds, s>>>((const f16*)x, C, G, HW, ppc, eps, part,
-                                                    stats, sync);
-  k_gn_nhwc_apply<<<dim3(chunks, N), 256, lds, s>>>((const f16*)x, gamma, beta, (f16*)y, C, G,
-                                                    HW, ppc, silu ? 1 : 0, stats);
+  k_gn_nhwc_stats<<<dim3(chunks, N), 256, lds * m.R, s>>>(x, C, G, HW, ppc, eps, part, stats, sync);
+  k_gn_nhwc_apply<<<dim3(chunks, N), 256, lds, s>>>(x, gamma, beta, (f16*)y, C, G, HW, ppc,
+                                                    silu ? 1 : 0, stats);
 }
 
 void launch_layer_norm(hipStream_t s, const void* x, const float* gamma, const float* beta,
@@ -584,8 +584,9 @@ int32_t di_group_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
     void* ws = nullptr;
     int rc = workspace(ctx, gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float), &ws);
     if (rc) return rc;
-    launch_group_norm_nhwc(ctx->stream, x->ptr, (const float*)g->ptr, (const float*)b->ptr,
-                           y->ptr, N, C, G, HW, eps, silu, (float*)ws, ctx->sync_words);
+    NhwcSrc src{(const f16*)x->ptr, (const f16*)x->ptr, C, C, C};
+    launch_group_norm_nhwc(ctx->stream, src, (const float*)g->ptr, (const float*)b->ptr, y->ptr,
+                           N, C, G, HW, eps, silu, (float*)ws, ctx->sync_words);
   }
   DI_LAUNCH_CHECK();
   return DI_OK;

@@ -117,7 +117,7 @@ int32_t di_linear(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_hand
   DI_CTX(ctx);
   DI_DTYPE(dt);
   DI_REQUIRE(M && N && K, DI_EINVAL, "di_linear: zero dimension (M=%u N=%u K=%u)", M, N, K);
-  DI_REQUIRE(act >= ACT_NONE && act <= ACT_SILU, DI_EINVAL, "di_linear: unknown act %d", act);
+  DI_REQUIRE(act >= ACT_NONE && act <= ACT_GELU_TANH, DI_EINVAL, "di_linear: unknown act %d", act);
   DI_REQUIRE(act != ACT_GEGLU || N % 32 == 0, DI_EINVAL,
              "di_linear: GEGLU needs N %% 32 == 0 (got %u)", N);
   const size_t es = dtype_size(dt);

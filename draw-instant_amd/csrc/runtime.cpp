@@ -88,6 +88,10 @@ int pool_alloc(Ctx* c, uint64_t bytes, void** out, uint64_t* cap_out) {
 }
 
 void pool_release(Ctx* c, void* p, uint64_t cap) {
+  if (c->hold_releases) {
+    c->held.emplace_back(p, cap);  // stays live: owned by the captured graph
+    return;
+  }
   c->free_list[cap].push_back(p);
   c->live--;
 }

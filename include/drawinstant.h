@@ -73,6 +73,7 @@ typedef uint64_t di_handle;
 #define DI_ACT_GELU 1  /* erf GELU */
 #define DI_ACT_GEGLU 2 /* h * GELU(gate); weight rows interleaved in 16-row groups */
 #define DI_ACT_SILU 3
+#define DI_ACT_GELU_TANH 4 /* tanh GELU of the FFN bench, fused-block.js:68-75 */
 
 /* ---- conv flags ---- */
 #define DI_CONV_F16_COMPUTE 1 /* NCHW fp32 tensors through the fp16 MFMA path */
@@ -279,6 +280,109 @@ int32_t di_attn_cross(di_ctx* ctx, di_handle Q, di_handle K, di_handle V, di_han
 int32_t di_tembed(di_ctx* ctx, di_handle T, di_handle W1, di_handle b1, di_handle W2,
                   di_handle b2, di_handle Y, uint32_t B, uint32_t emb_dim, uint32_t hid,
                   int32_t wdtype);
+
+/* ======================= fused blocks ======================= */
+/* NHWC fp16 activations; conv weights OHWI fp16; linear weights [out][in]
+ * fp16; biases, norm affines and temb fp32.  0 = absent optional weight. */
+
+typedef struct {
+  di_handle norm1_gamma, norm1_beta; /* [Cin] */
+  di_handle conv1_w, conv1_b;        /* [Cout][3][3][Cin], [Cout] */
+  di_handle temb_w, temb_b;          /* [Cout][temb_dim], [Cout] (temb given) */
+  di_handle norm2_gamma, norm2_beta; /* [Cout] */
+  di_handle conv2_w, conv2_b;        /* [Cout][3][3][Cout], [Cout] */
+  di_handle skip_w, skip_b;          /* [Cout][Cin] 1x1, [Cout] (Cin != Cout) */
+} di_resnet_weights;
+
+/* ResnetBlock2D: y = conv2(SiLU(GN2(conv1(SiLU(GN1(x))) + temb_proj(SiLU(temb)))))
+ * + skip(x).  runResNetBench (fused-resnet.js:267-420: GN+SiLU -> conv -> GN+SiLU
+ * -> conv + residual) extended with the temb add and 1x1 skip its header says it
+ * omits (fused-resnet.js:9-12).  temb: fp32 [B][temb_dim] or 0. */
+int32_t di_resnet_block(di_ctx* ctx, const di_resnet_weights* w, di_handle X,
+                        di_handle temb, di_handle Y, uint32_t B, uint32_t Cin,
+                        uint32_t Cout, uint32_t H, uint32_t Wd, uint32_t temb_dim,
+                        uint32_t groups, float eps);
+
+typedef struct {
+  di_handle norm_gamma, norm_beta;     /* GroupNorm [C] */
+  di_handle proj_in_w, proj_in_b;      /* [C][C], [C] */
+  di_handle ln1_gamma, ln1_beta;       /* [C] */
+  di_handle attn1_qkv_w;               /* [3C][C] = to_q ; to_k ; to_v */
+  di_handle attn1_out_w, attn1_out_b;  /* [C][C], [C] */
+  di_handle ln2_gamma, ln2_beta;
+  di_handle attn2_q_w;                 /* [C][C] */
+  di_handle attn2_kv_w;                /* [2C][cross_dim] = to_k ; to_v */
+  di_handle attn2_out_w, attn2_out_b;
+  di_handle ln3_gamma, ln3_beta;
+  di_handle ff_in_w, ff_in_b;          /* GEGLU [8C][C] rows as [16 h | 16 gate] groups, [8C] */
+  di_handle ff_out_w, ff_out_b;        /* [C][4C], [C] */
+  di_handle proj_out_w, proj_out_b;    /* [C][C], [C] */
+} di_transformer_weights;
+
+/* Transformer2DModel with linear projection and one BasicTransformerBlock
+ * (GN -> proj_in -> LN+self-attn -> LN+cross-attn -> LN+GEGLU FFN -> proj_out
+ * + residual), heads = C/64.  The SD block that runBlockBench
+ * (fused-block-full.js:456-686) approximates with LN/attn/GELU-FFN only.
+ * X, Y: [B][H*W][C] fp16; context: [B][Sctx][cross_dim] fp16. */
+int32_t di_transformer_block(di_ctx* ctx, const di_transformer_weights* w, di_handle X,
+                             di_handle context, di_handle Y, uint32_t B, uint32_t C,
+                             uint32_t H, uint32_t Wd, uint32_t Sctx, uint32_t cross_dim,
+                             uint32_t groups, float gn_eps, float ln_eps);
+
+/* FFN of runFFNBench (fused-block.js:219-342): Y = act(X W1^T + b1) W2^T + b2 + X
+ * with act DI_ACT_GELU_TANH (the bench's GELU), DI_ACT_GELU or DI_ACT_GEGLU
+ * (W1 then [2F][D]).  W1 [F][D], W2 [D][F] torch layout. */
+int32_t di_ffn(di_ctx* ctx, di_handle X, di_handle W1, di_handle b1, di_handle W2,
+               di_handle b2, di_handle Y, uint32_t rows, uint32_t D, uint32_t F,
+               int32_t act, int32_t dtype);
+
+/* ======================= SD2.1 / SD-Turbo U-Net ======================= */
+
+typedef struct {
+  uint32_t in_channels, out_channels; /* 4, 4 */
+  uint32_t block_channels[4];         /* 320, 640, 1280, 1280 (multiples of 64) */
+  uint32_t cross_attn[4];             /* 1, 1, 1, 0: CrossAttn{Down,Up}Block2D levels */
+  uint32_t layers_per_block;          /* 2 */
+  uint32_t cross_dim;                 /* 1024 */
+  uint32_t time_dim;                  /* 1280 */
+  uint32_t groups;                    /* 32 */
+  float resnet_eps;                   /* 1e-5 */
+  float transformer_gn_eps;           /* 1e-6 */
+  float ln_eps;                       /* 1e-5 */
+} di_unet_config;
+
+typedef struct di_unet di_unet;
+
+/* physical layout tags of di_unet_param_info */
+#define DI_PARAM_VECTOR 0         /* [n] */
+#define DI_PARAM_LINEAR 1         /* [out][in] */
+#define DI_PARAM_CONV_OHWI 2      /* [Cout][K][K][Cin] */
+#define DI_PARAM_LINEAR_STACKED 3 /* [k*out][in]: k linears stacked by rows */
+#define DI_PARAM_GEGLU_ROWS 4     /* rows (or entries) in 32-groups [16 hidden | 16 gate] */
+
+#define DI_UNET_GRAPH 1 /* capture the step in a HIP graph once, replay after */
+
+int32_t di_unet_default_config(di_unet_config* cfg);
+/* Build the model with seeded random weights (no checkpoint is available
+ * offline); cfg = NULL selects SD2.1.  Replaces loadUNetWGSL (unet-wgsl.js:40-114). */
+int32_t di_unet_create(di_ctx* ctx, const di_unet_config* cfg, uint64_t seed, di_unet** out);
+int32_t di_unet_destroy(di_ctx* ctx, di_unet* unet);
+int32_t di_unet_num_params(di_ctx* ctx, di_unet* unet, uint32_t* n_tensors,
+                           uint64_t* n_elements);
+int32_t di_unet_param_info(di_ctx* ctx, di_unet* unet, uint32_t index, char* name,
+                           uint32_t name_cap, uint32_t* dims, uint32_t* ndims,
+                           int32_t* dtype, int32_t* layout);
+int32_t di_unet_param_download(di_ctx* ctx, di_unet* unet, uint32_t index, void* dst,
+                               uint64_t bytes);
+/* Load one tensor (WeightCache upload role, wgsl-unet.js:55-97). */
+int32_t di_unet_param_upload(di_ctx* ctx, di_unet* unet, uint32_t index, const void* src,
+                             uint64_t bytes);
+/* One denoise step: unetForwardWGSL (unet-wgsl.js:145-195).  sample, out: fp32
+ * [B][4][H][W] (NCHW); timesteps: fp32 [B]; context: fp32 [B][Sctx][cross_dim].
+ * Enqueues only; flags DI_UNET_GRAPH replays a captured graph. */
+int32_t di_unet_forward(di_ctx* ctx, di_unet* unet, di_handle sample, di_handle timesteps,
+                        di_handle context, di_handle out, uint32_t B, uint32_t H,
+                        uint32_t W, uint32_t Sctx, int32_t flags);
 
 #ifdef __cplusplus
 }

@@ -318,11 +318,13 @@ void or_attention(const float* q, const float* k, const float* v, float* o, int6
         z += sc[j];
       }
       float* oi = o + b * o_bs + h * o_hs + i * o_rs;
-      for (int64_t t = 0; t < d; t++) {
-        double acc = 0.0;
-        for (int64_t j = 0; j < Skv; j++) acc += sc[j] * v[b * v_bs + h * v_hs + j * v_rs + t];
-        oi[t] = (float)(acc / z);
+      double* acc = (double*)calloc(d, sizeof(double));
+      for (int64_t j = 0; j < Skv; j++) {
+        const float* vj = v + b * v_bs + h * v_hs + j * v_rs;
+        for (int64_t t = 0; t < d; t++) acc[t] += sc[j] * vj[t];
       }
+      for (int64_t t = 0; t < d; t++) oi[t] = (float)(acc[t] / z);
+      free(acc);
       free(sc);
     }
   }
