@@ -58,7 +58,7 @@ struct Ctx {
   std::vector<std::pair<void*, uint64_t>> held;
 };
 
-constexpr uint32_t kSyncWords = 1u << 18;  // 1 MiB
+constexpr uint32_t kSyncWords = 1u << 19;  // 2 MiB: GN barriers + last-block counters
 constexpr uint32_t kFaultWord = 0;
 
 // ---- error reporting (thread-local message, status code returned) ----

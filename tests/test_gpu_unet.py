@@ -83,7 +83,11 @@ def test_sd21_step_b4_batch_independent(sd21, rng):
     got = sd21(x, ts, ctx)
     for b in (0, 3):
         one = sd21(x[b:b + 1], ts[b], ctx[b:b + 1])
-        assert rel_l2(got[b:b + 1], one) <= 1e-3
+        # B=4 and B=1 tile the GEMMs differently (M = 4*HW vs HW), so fp32
+        # summation order and the fp16 roundings of ~50 layers differ: ~2e-3
+        # measured.  Mixing samples (GN stats, attention, temb across the
+        # batch) would be an O(1) error.
+        assert rel_l2(got[b:b + 1], one) <= 5e-3
     err = rel_l2(got, _torch_ref(sd21, x, ts, ctx))
     print(f"[sd21 B=4] rel-L2 {err:.2e}", flush=True)
     assert err <= 1e-2
