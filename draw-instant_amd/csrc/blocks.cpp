@@ -24,8 +24,9 @@ namespace di {
 namespace {
 
 int run(Ctx* c, GemmArgs& g, int a_mode) {
-  const int tile = gemm_pick_tile(g, c->num_cus);
-  g.splits = gemm_pick_splits(g, tile, c->num_cus);
+  const GemmPlan plan = gemm_plan(g, DI_F16, c->num_cus);
+  const int tile = plan.tile;
+  g.splits = plan.splits;
   if (g.splits > 1) {
     void* ws = nullptr;
     int rc = workspace(c, gemm_ws_bytes(g), &ws);
@@ -72,6 +73,10 @@ int conv_nhwc(Ctx* c, const ConvCall& cc) {
   g.K = cc.ks * cc.ks * cc.Cin;
   g.b = cc.w;
   g.ldb = g.K;
+  const uint64_t pixels = (uint64_t)cc.B * cc.H * cc.W;
+  g.a_bytes = gemm_extent(pixels * cc.x.ld1 * 2);
+  g.a2_bytes = gemm_extent(pixels * cc.x.ld2 * 2);
+  g.b_bytes = gemm_extent((uint64_t)g.N * g.K * 2);
   g.bias = cc.bias;
   g.bias2 = cc.bias2;
   g.rows_b2 = cc.rows_b2;
@@ -108,6 +113,8 @@ int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const
   g.ldc = ldy;
   g.a_vec_ok = (K % 8 == 0) && (ldx % 8 == 0);
   g.b_vec_ok = K % 8 == 0;
+  g.a_bytes = gemm_extent((uint64_t)M * ldx * 2);
+  g.b_bytes = gemm_extent((uint64_t)N * K * 2);
   return run(c, g, A_DENSE);
 }
 

@@ -11,7 +11,20 @@ namespace di {
 enum AMode { A_DENSE = 0, A_CONV_NHWC = 1, A_CONV_NCHW = 2 };
 enum BMode { B_NK = 0, B_KN = 1 };
 enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_GEGLU = 2, ACT_SILU = 3, ACT_GELU_TANH = 4 };
-enum TileCfg { TILE_64x64 = 0, TILE_128x64 = 1, TILE_64x128 = 2, TILE_128x128 = 3 };
+enum TileCfg {
+  TILE_64x64 = 0,
+  TILE_128x64 = 1,
+  TILE_64x128 = 2,
+  TILE_128x128 = 3,
+  TILE_128x160 = 4,
+  TILE_64x160 = 5,
+  TILE_COUNT = 6
+};
+
+struct GemmPlan {
+  int tile;
+  uint32_t splits;
+};
 
 struct GemmArgs {
   // ---- A operand ----
@@ -29,6 +42,9 @@ struct GemmArgs {
   uint32_t M = 0, N = 0, K = 0, batch = 1;
   uint32_t splits = 1, k_split = 0;
   uint32_t a_vec_ok = 1, b_vec_ok = 1;  // 16-byte vector loads legal
+  // Byte extents of A, A2 (per batch entry) and B for buffer-load range
+  // checks; 0 = unknown (generic path).  Must stay below 2 GiB.
+  uint32_t a_bytes = 0, a2_bytes = 0, b_bytes = 0;
   // ---- epilogue ----
   float alpha = 1.0f;
   const float* bias = nullptr;   // [N]
@@ -46,9 +62,14 @@ struct GemmArgs {
   float* part = nullptr;  // split-K partials [splits][batch][M][N]
 };
 
-int gemm_pick_tile(const GemmArgs& g, int num_cus);
-uint32_t gemm_pick_splits(const GemmArgs& g, int tile_cfg, int num_cus);
+// Tile shape and split-K factor from a cost model (env DI_GEMM_TILE /
+// DI_GEMM_SPLITS override, for tuning sweeps).
+GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus);
 uint64_t gemm_ws_bytes(const GemmArgs& g);
+// Whether the buffer-load (FAST) kernel variant applies.
+bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode);
+// Byte extent clamped to the buffer-load limit (0 = too large for it).
+inline uint32_t gemm_extent(uint64_t bytes) { return bytes < 0x7fff0000ull ? (uint32_t)bytes : 0; }
 // elem: DI_F16 or DI_F32 operand element type.
 void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s);
 // OIHW (any dtype) -> OHWI fp16 with optional zero channel padding Cin -> Cin_pad.

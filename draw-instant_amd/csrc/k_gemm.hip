@@ -23,6 +23,9 @@
 // holds row l%16, k (l/16)*8..+7; C rows (l/16)*4..+3, col l%16), fp32 uses
 // v_mfma_f32_16x16x4_f32 (k = l/16).  Split-K writes fp32 partials that a
 // second kernel reduces and passes through the same epilogue.
+#include <cmath>
+#include <cstdlib>
+
 #include "di_device.h"
 #include "di_gemm.h"
 #include "di_kernels.h"
@@ -71,6 +74,16 @@ __device__ __forceinline__ typename Mfma<T>::vec zero_vec() {
   return v;
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  // raw buffer, stride 0; dword3 0x00020000 is the gfx9-family data format
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+template <typename V>
+__device__ __forceinline__ V buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // ---- epilogue (shared by the GEMM kernel and the split-K reducer) ----
 template <typename T>
 __device__ __forceinline__ float epi_value(const GemmArgs& g, uint32_t bz, uint32_t m, uint32_t n,
@@ -108,7 +121,7 @@ __device__ __forceinline__ void store_out(const GemmArgs& g, uint32_t bz, uint32
 }
 
 // ---- the GEMM kernel ----
-template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD>
+template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   using MT = Mfma<T>;
   constexpr int KV = MT::KV;
@@ -128,9 +141,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
 
-  // tile coordinates: N fastest so neighbouring workgroups share A rows
+  // Tile order: N fastest, so consecutive tiles share A rows.  Workgroups are
+  // dealt round-robin to the 8 XCDs (each with its own L2); remap so that
+  // each XCD gets a contiguous run of tiles and shares their A / B reads.
   const uint32_t n_tiles = (g.N + BN - 1) / BN;
-  const uint32_t tile = blockIdx.x;
+  const uint32_t n_wg = gridDim.x;
+  uint32_t tile = blockIdx.x;
+  {
+    const uint32_t per = n_wg / 8, rem = n_wg % 8, xcd = tile % 8, slot = tile / 8;
+    tile = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  }
   const uint32_t m0 = (tile / n_tiles) * BM, n0 = (tile % n_tiles) * BN;
   const uint32_t splits = g.splits;
   const uint32_t bz = blockIdx.z / splits, split = blockIdx.z % splits;
@@ -178,9 +198,44 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   const bool a_fast = g.a_vec_ok;
   const bool b_fast = g.b_vec_ok;
 
-  typename MT::vec ra[NVA], rb[NVB];
+  // ---- FAST path (fp16, B_NK, dense or NHWC conv with Cin % 64 == 0):
+  // every load is an unconditional raw buffer load; invalid elements get an
+  // offset past the buffer's range and read as zero, so the loads carry no
+  // branches and the compiler can keep exact vmcnt waits for the pipeline.
+  constexpr uint32_t kInv = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(A, g.a_bytes), rA2 = make_rsrc(A2, g.a2_bytes),
+                               rB = make_rsrc(B, g.b_bytes);
+  uint32_t fa1[NVA], fa2[NVA], fb[NVB];
+  uint32_t fimg[NVA];
+  uint32_t f_ci0 = 0, f_ky = 0, f_kx = 0;  // conv: per-stage tap and channel base (uniform)
+  const uint32_t upsh = g.up == 2 ? 1 : 0;
+  if constexpr (FAST) {
+#pragma unroll
+    for (int i = 0; i < NVA; i++) {
+      const uint32_t m = m0 + (tid + i * 256) / VPR;
+      fa1[i] = m < g.M ? m * (uint32_t)g.lda * 2u : kInv;
+      fa2[i] = m < g.M ? m * (uint32_t)g.lda2 * 2u : kInv;
+      fimg[i] = (uint32_t)a_row_off[i] * g.H;
+    }
+#pragma unroll
+    for (int i = 0; i < NVB; i++) {
+      const uint32_t n = n0 + (tid + i * 256) / VPR;
+      fb[i] = n < g.N ? n * (uint32_t)g.ldb * 2u : kInv;
+    }
+    if constexpr (AM == A_CONV_NHWC) {
+      const uint32_t tap0 = k_begin / g.Cin;
+      f_ci0 = k_begin % g.Cin;
+      f_ky = tap0 / g.ks;
+      f_kx = tap0 % g.ks;
+    }
+  }
 
-  auto load_a = [&](int stage) {
+  struct Stage {
+    typename MT::vec a[NVA];
+    typename MT::vec b[NVB];
+  };
+
+  auto load_a = [&](int stage, Stage& st) {
     const uint32_t kbase = k_begin + stage * BK;
 #pragma unroll
     for (int i = 0; i < NVA; i++) {
@@ -226,7 +281,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
           }
         }
       }
-      ra[i] = v;
+      st.a[i] = v;
     }
     if constexpr (AM == A_CONV_NHWC) {
       ci += BK;
@@ -240,7 +295,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
   };
 
-  auto load_b = [&](int stage) {
+  auto load_b = [&](int stage, Stage& st) {
     const uint32_t kbase = k_begin + stage * BK;
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
@@ -271,26 +326,26 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
           }
         }
       }
-      rb[i] = v;
+      st.b[i] = v;
     }
   };
 
-  auto store_stage = [&](int buf) {
+  auto store_stage = [&](int buf, const Stage& st) {
 #pragma unroll
     for (int i = 0; i < NVA; i++) {
       uint32_t r = (tid + i * 256) / VPR;
-      *(typename MT::vec*)&sA[buf][r * LDK + kc * KV] = ra[i];
+      *(typename MT::vec*)&sA[buf][r * LDK + kc * KV] = st.a[i];
     }
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
       if constexpr (BMD == B_NK) {
         uint32_t r = (tid + i * 256) / VPR;
-        *(typename MT::vec*)&sB[buf][r * LDK + kc * KV] = rb[i];
+        *(typename MT::vec*)&sB[buf][r * LDK + kc * KV] = st.b[i];
       } else {
         constexpr int VPK = BN / KV;
         uint32_t kr = (tid + i * 256) / VPK, nc = (tid + i * 256) % VPK;
 #pragma unroll
-        for (int j = 0; j < KV; j++) sB[buf][(nc * KV + j) * LDK + kr] = rb[i][j];
+        for (int j = 0; j < KV; j++) sB[buf][(nc * KV + j) * LDK + kr] = st.b[i][j];
       }
     }
   };
@@ -301,34 +356,112 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
     for (int b = 0; b < TN; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (n_stages > 0) {
-    load_a(0);
-    load_b(0);
-    store_stage(0);
-  }
-  __syncthreads();
-
   const int fr = lane & 15, fk = (lane >> 4) * MT::FK;
-  for (int s = 0; s < n_stages; s++) {
-    const int cur = s & 1;
-    if (s + 1 < n_stages) {
-      load_a(s + 1);
-      load_b(s + 1);
-    }
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < BK; kk += MT::KM) {
       typename MT::frag af[TM], bf[TN];
 #pragma unroll
-      for (int a = 0; a < TM; a++) af[a] = ld_frag<T>(&sA[cur][(wm0 + a * 16 + fr) * LDK + kk + fk]);
+      for (int a = 0; a < TM; a++) af[a] = ld_frag<T>(&sA[buf][(wm0 + a * 16 + fr) * LDK + kk + fk]);
 #pragma unroll
-      for (int b = 0; b < TN; b++) bf[b] = ld_frag<T>(&sB[cur][(wn0 + b * 16 + fr) * LDK + kk + fk]);
+      for (int b = 0; b < TN; b++) bf[b] = ld_frag<T>(&sB[buf][(wn0 + b * 16 + fr) * LDK + kk + fk]);
 #pragma unroll
       for (int a = 0; a < TM; a++)
 #pragma unroll
         for (int b = 0; b < TN; b++) acc[a][b] = MT::mma(af[a], bf[b], acc[a][b]);
     }
-    if (s + 1 < n_stages) store_stage(cur ^ 1);
+  };
+  auto load_fast = [&](int stage, Stage& st) {
+    const uint32_t kbase = k_begin + stage * BK;
+    const uint32_t k = kbase + kc * KV;
+    const bool kval = k < k_end;
+    if constexpr (AM == A_DENSE) {
+      const bool s2 = kbase >= g.c1;  // uniform: which concat source
+      const uint32_t kb = (s2 ? k - g.c1 : k) * 2u;
+#pragma unroll
+      for (int i = 0; i < NVA; i++) {
+        const uint32_t off = kval ? (s2 ? fa2[i] : fa1[i]) + kb : kInv;
+        st.a[i] = buf_load16<typename MT::vec>(s2 ? rA2 : rA, off);
+      }
+    } else {
+      const bool s2 = f_ci0 >= g.c1;
+      const uint32_t cb = ((s2 ? f_ci0 - g.c1 : f_ci0) + kc * KV) * 2u;
+      const uint32_t ld2 = (uint32_t)(s2 ? g.lda2 : g.lda) * 2u;
+      const int Hi_ = (int)(g.H << upsh), Wi_ = (int)(g.W << upsh);
+#pragma unroll
+      for (int i = 0; i < NVA; i++) {
+        const int iy = a_iy0[i] + (int)f_ky, ix = a_ix0[i] + (int)f_kx;
+        const bool ok = a_row_ok[i] && kval && iy >= 0 && iy < Hi_ && ix >= 0 && ix < Wi_;
+        const uint32_t pix = (fimg[i] + ((uint32_t)iy >> upsh)) * g.W + ((uint32_t)ix >> upsh);
+        st.a[i] = buf_load16<typename MT::vec>(s2 ? rA2 : rA, ok ? pix * ld2 + cb : kInv);
+      }
+      f_ci0 += BK;
+      if (f_ci0 >= g.Cin) {
+        f_ci0 = 0;
+        if (++f_kx == g.ks) {
+          f_kx = 0;
+          ++f_ky;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NVB; i++) st.b[i] = buf_load16<typename MT::vec>(rB, kval ? fb[i] + k * 2u : kInv);
+  };
+  auto load = [&](int stage, Stage& st) {
+    if constexpr (FAST) {
+      load_fast(stage, st);
+    } else {
+      load_a(stage, st);
+      load_b(stage, st);
+    }
+  };
+
+  // Software pipeline, prefetch distance 2: stage s is loaded into registers
+  // at iteration s-3, stored to LDS buffer s%2 at iteration s-1 and consumed
+  // at iteration s, so each global load has two iterations of MFMA work to
+  // arrive.  Unrolled by two so both register sets stay in registers.
+  Stage r0, r1;
+  if constexpr (FAST) {
+    // Loads past the last stage read zeros (offsets out of range), so the
+    // steady state runs without conditions and the waitcnt pass can keep
+    // one stage of loads in flight across each LDS store.
+    if (n_stages > 0) {
+      load(0, r0);
+      store_stage(0, r0);
+      load(1, r1);
+      load(2, r0);
+      __syncthreads();
+      // one exit, at the bottom: an odd trailing stage multiplies zeros
+      for (int s = 0; s < n_stages; s += 2) {
+        compute(0);
+        store_stage(1, r1);
+        __syncthreads();
+        load(s + 3, r1);
+        compute(1);
+        store_stage(0, r0);
+        __syncthreads();
+        load(s + 4, r0);
+      }
+    }
+  } else {
+  if (n_stages > 0) {
+    load(0, r0);
+    store_stage(0, r0);
+  }
+  if (n_stages > 1) load(1, r1);
+  if (n_stages > 2) load(2, r0);
+  __syncthreads();
+  for (int s = 0; s < n_stages; s += 2) {
+    compute(0);
+    if (s + 1 < n_stages) store_stage(1, r1);
     __syncthreads();
+    if (s + 3 < n_stages) load(s + 3, r1);
+    if (s + 1 >= n_stages) break;
+    compute(1);
+    if (s + 2 < n_stages) store_stage(0, r0);
+    __syncthreads();
+    if (s + 4 < n_stages) load(s + 4, r0);
+  }
   }
 
   // ---- epilogue ----
@@ -410,27 +543,81 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
   }
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD>
+template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST>
 void launch_cfg(const GemmArgs& g, hipStream_t s) {
   uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  k_gemm<T, BM, BN, WGM, WGN, AM, BMD><<<dim3(tiles, 1, g.batch * g.splits), 256, 0, s>>>(g);
+  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST><<<dim3(tiles, 1, g.batch * g.splits), 256, 0, s>>>(g);
 }
 
+// Generic (bounds-checked) variants: two tile shapes.
 template <typename T, int AM, int BMD>
-void launch_tile(const GemmArgs& g, int tile_cfg, hipStream_t s) {
+void launch_slow(const GemmArgs& g, int tile_cfg, hipStream_t s) {
+  if (tile_cfg == TILE_64x64 || tile_cfg == TILE_128x64 || tile_cfg == TILE_64x128 ||
+      tile_cfg == TILE_64x160)
+    launch_cfg<T, 64, 64, 2, 2, AM, BMD, false>(g, s);
+  else
+    launch_cfg<T, 128, 128, 2, 2, AM, BMD, false>(g, s);
+}
+
+// Buffer-load variants: every tile shape.
+template <int AM>
+void launch_fast(const GemmArgs& g, int tile_cfg, hipStream_t s) {
   switch (tile_cfg) {
-    case TILE_128x128: launch_cfg<T, 128, 128, 2, 2, AM, BMD>(g, s); break;
-    case TILE_128x64: launch_cfg<T, 128, 64, 2, 2, AM, BMD>(g, s); break;
-    case TILE_64x128: launch_cfg<T, 64, 128, 2, 2, AM, BMD>(g, s); break;
-    default: launch_cfg<T, 64, 64, 2, 2, AM, BMD>(g, s); break;
+    case TILE_128x160: launch_cfg<f16, 128, 160, 2, 2, AM, B_NK, true>(g, s); break;
+    case TILE_128x128: launch_cfg<f16, 128, 128, 2, 2, AM, B_NK, true>(g, s); break;
+    case TILE_128x64: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true>(g, s); break;
+    case TILE_64x160: launch_cfg<f16, 64, 160, 2, 2, AM, B_NK, true>(g, s); break;
+    case TILE_64x128: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true>(g, s); break;
+    default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true>(g, s); break;
   }
 }
 
-uint64_t tiles_of(const GemmArgs& g, int cfg) {
-  uint32_t bm = (cfg == TILE_128x128 || cfg == TILE_128x64) ? 128 : 64;
-  uint32_t bn = (cfg == TILE_128x128 || cfg == TILE_64x128) ? 128 : 64;
-  return (uint64_t)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch;
+const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64};
+const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160};
+// Relative per-CU MFMA efficiency of each tile shape (the 2x2 wavefront tile
+// sets LDS bytes per MFMA cycle); tuned by measurement.
+const double kTileEff[TILE_COUNT] = {0.35, 0.5, 0.5, 0.8, 0.85, 0.55};
+
+}  // namespace
+
+GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
+  const char* env_tile = getenv("DI_GEMM_TILE");
+  const char* env_split = getenv("DI_GEMM_SPLITS");
+  GemmPlan best{TILE_64x64, 1};
+  if (elem == DI_F32) {
+    uint64_t t = (uint64_t)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
+    best.tile = t >= (uint64_t)num_cus / 2 ? TILE_128x128 : TILE_64x64;
+    return best;
+  }
+  const double cus = num_cus;
+  double best_t = 1e300;
+  for (int tc = 0; tc < TILE_COUNT; tc++) {
+    if (g.act == ACT_GEGLU && kTileN[tc] == 160) continue;  // GEGLU pairs need even TN
+    const uint64_t mt = (g.M + kTileM[tc] - 1) / kTileM[tc], nt = (g.N + kTileN[tc] - 1) / kTileN[tc];
+    const uint64_t T = mt * nt * g.batch;
+    for (uint32_t s = 1; s <= 32; s++) {
+      const uint32_t kper = ((g.K + s - 1) / s + 63) / 64 * 64;
+      if (s > 1 && kper < 256) break;
+      const double rounds = ceil((double)T * s / cus);
+      // cycles per work unit at the tile's efficiency (4096 fp16 FLOP/clk/CU)
+      // plus a fixed prologue / epilogue cost
+      const double cyc = 2.0 * kTileM[tc] * kTileN[tc] * kper / (4096.0 * kTileEff[tc]) + 3000.0;
+      double t = rounds * cyc;
+      if (s > 1)  // fp32 partials written and read back (~4 TB/s) plus a launch
+        t += (double)g.batch * g.M * g.N * 4.0 * (s + 1) / (4.0e12 / 2.4e9) + 5000.0;
+      if (t < best_t * 0.97) {
+        best_t = t;
+        best = GemmPlan{tc, s};
+      }
+    }
+  }
+  if (env_tile) best.tile = atoi(env_tile);
+  if (env_split) best.splits = (uint32_t)atoi(env_split);
+  if (best.splits < 1) best.splits = 1;
+  return best;
 }
+
+namespace {
 
 template <typename S>
 __global__ void k_repack(const S* __restrict__ w, f16* __restrict__ out, uint32_t Cout,
@@ -460,24 +647,17 @@ void launch_repack_oihw_ohwi(hipStream_t s, const void* w, int wdt, void* out, u
     k_repack<f16><<<(unsigned)blocks, 256, 0, s>>>((const f16*)w, (f16*)out, Cout, Cin, ks, Cin_pad);
 }
 
-int gemm_pick_tile(const GemmArgs& g, int num_cus) {
-  // Largest tile that still gives every CU a workgroup; else 64x64.
-  if (tiles_of(g, TILE_128x128) >= (uint64_t)num_cus) return TILE_128x128;
-  if (tiles_of(g, TILE_128x64) >= (uint64_t)num_cus) return TILE_128x64;
-  if (tiles_of(g, TILE_64x128) >= (uint64_t)num_cus) return TILE_64x128;
-  return TILE_64x64;
-}
-
-uint32_t gemm_pick_splits(const GemmArgs& g, int tile_cfg, int num_cus) {
-  uint64_t t = tiles_of(g, tile_cfg);
-  uint32_t k_stages = (g.K + 63) / 64;
-  uint32_t s = 1;
-  while (t * s * 2 <= (uint64_t)num_cus && k_stages / (s * 2) >= 8 && s < 16) s *= 2;
-  return s;
-}
-
 uint64_t gemm_ws_bytes(const GemmArgs& g) {
   return g.splits > 1 ? (uint64_t)g.splits * g.batch * g.M * g.N * sizeof(float) : 0;
+}
+
+bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode) {
+  if (elem != DI_F16 || b_mode != B_NK || !g.b_vec_ok) return false;
+  if (g.a_bytes == 0 || g.a2_bytes == 0 || g.b_bytes == 0) return false;  // extents unknown
+  const bool single = g.c1 == 0xffffffffu || g.a2 == g.a;
+  if (a_mode == A_DENSE) return g.a_vec_ok && (single || g.c1 % 64 == 0);
+  if (a_mode == A_CONV_NHWC) return g.Cin % 64 == 0 && (single || g.c1 % 64 == 0) && (g.up == 1 || g.up == 2);
+  return false;
 }
 
 void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s) {
@@ -491,13 +671,18 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
     g.a2 = g.a;
     g.lda2 = g.lda;
     g.sa2 = g.sa;
+    g.a2_bytes = g.a_bytes;
     if (g.c1 == 0) g.c1 = 0xffffffffu;
   }
 #define DI_GEMM_CASE(T, AMv, BMv)                        \
   if (a_mode == AMv && b_mode == BMv) {                  \
-    launch_tile<T, AMv, BMv>(g, tile_cfg, s);            \
+    launch_slow<T, AMv, BMv>(g, tile_cfg, s);            \
   }
-  if (elem == DI_F16) {
+  const bool fast = gemm_fast_ok(g, elem, a_mode, b_mode);
+  if (fast) {
+    if (a_mode == A_DENSE) launch_fast<A_DENSE>(g, tile_cfg, s);
+    else launch_fast<A_CONV_NHWC>(g, tile_cfg, s);
+  } else if (elem == DI_F16) {
     DI_GEMM_CASE(f16, A_DENSE, B_NK)
     else DI_GEMM_CASE(f16, A_DENSE, B_KN)
     else DI_GEMM_CASE(f16, A_CONV_NHWC, B_NK)

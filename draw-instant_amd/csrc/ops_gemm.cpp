@@ -10,8 +10,9 @@ namespace {
 
 int run_gemm(di_ctx* ctx, GemmArgs& g, int elem, int a_mode, int b_mode, int tile = -1,
              int splits = -1) {
-  if (tile < 0) tile = gemm_pick_tile(g, ctx->num_cus);
-  g.splits = splits > 0 ? (uint32_t)splits : gemm_pick_splits(g, tile, ctx->num_cus);
+  const GemmPlan plan = gemm_plan(g, elem, ctx->num_cus);
+  if (tile < 0) tile = plan.tile;
+  g.splits = splits > 0 ? (uint32_t)splits : plan.splits;
   if (g.splits > 1) {
     void* ws = nullptr;
     int rc = workspace(ctx, gemm_ws_bytes(g), &ws);
@@ -109,6 +110,8 @@ int32_t di_gemm(di_ctx* ctx, di_handle A, di_handle B, di_handle C, di_handle Y,
   const uint32_t kv = dt == DI_F32 ? 4 : 8;
   g.a_vec_ok = K % kv == 0;
   g.b_vec_ok = (trans_b ? K : N) % kv == 0;
+  g.a_bytes = gemm_extent((uint64_t)M * K * es);
+  g.b_bytes = gemm_extent((uint64_t)K * N * es);
   return run_gemm(ctx, g, dt, A_DENSE, trans_b ? B_NK : B_KN);
 }
 
@@ -149,6 +152,8 @@ int32_t di_linear(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_hand
   g.c_f32 = dt == DI_F32;
   const uint32_t kv = dt == DI_F32 ? 4 : 8;
   g.a_vec_ok = g.b_vec_ok = K % kv == 0;
+  g.a_bytes = gemm_extent((uint64_t)M * K * es);
+  g.b_bytes = gemm_extent((uint64_t)N * K * es);
   return run_gemm(ctx, g, dt, A_DENSE, B_NK);
 }
 
@@ -206,6 +211,8 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_han
     g.c = y->ptr;
     g.ldc = Cout;
     g.ldr = Cout;
+    g.a_bytes = gemm_extent(nx * 2);
+    g.b_bytes = gemm_extent((uint64_t)Cout * g.K * 2);
     return run_gemm(ctx, g, DI_F16, A_CONV_NHWC, B_NK);
   }
   DI_REQUIRE(layout == DI_NCHW, DI_EINVAL, "di_conv2d: bad layout %d", layout);
@@ -243,6 +250,8 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_han
   g.K = Cp * K * K;
   g.b = tw.p;
   g.ldb = g.K;
+  g.a_bytes = gemm_extent((uint64_t)N * Cp * H * W * 2);
+  g.b_bytes = gemm_extent((uint64_t)Cout * g.K * 2);
   return run_gemm(ctx, g, DI_F16, A_CONV_NHWC, B_NK);
 }
 
