@@ -42,8 +42,7 @@ int gn_nhwc(Ctx* c, NhwcSrc x, const float* g, const float* b, f16* y, uint32_t 
   void* ws = nullptr;
   int rc = workspace(c, gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float), &ws);
   if (rc) return rc;
-  launch_group_norm_nhwc(c->stream, x, g, b, y, N, C, G, HW, eps, silu, (float*)ws,
-                         c->sync_words);
+  launch_group_norm_nhwc(c->stream, x, g, b, y, N, C, G, HW, eps, silu, (float*)ws);
   return DI_OK;
 }
 

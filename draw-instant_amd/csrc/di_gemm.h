@@ -60,6 +60,10 @@ struct GemmArgs {
   int c_nchw = 0;     // store C[(img*N + n)*c_hw + p] with m = img*c_hw + p
   uint32_t c_hw = 1;
   float* part = nullptr;  // split-K partials [splits][batch][M][N]
+  // Set by launch_gemm: fp16 NHWC output whose rows, bias, temb bias and
+  // residual allow 16-byte vectors (the C tile is then staged through LDS
+  // and written 8 columns per thread).
+  int vec_epi = 0;
 };
 
 // Tile shape and split-K factor from a cost model (env DI_GEMM_TILE /

@@ -47,19 +47,11 @@ struct Ctx {
   // kernel workspace (partials); grown on demand, never during graph capture
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
-  // Zero-initialised words for cross-block barriers / last-block counters.
-  // Every user leaves its words at zero again when its kernel ends, so they
-  // never need clearing (and no memset is ever recorded into a graph).
-  // Word 0 is the fault flag: set by a kernel whose bounded wait expired.
-  uint32_t* sync_words = nullptr;
   // While set (graph capture), pool_release parks buffers in `held` instead
   // of the free list; the capturing owner takes them over.
   bool hold_releases = false;
   std::vector<std::pair<void*, uint64_t>> held;
 };
-
-constexpr uint32_t kSyncWords = 1u << 19;  // 2 MiB: GN barriers + last-block counters
-constexpr uint32_t kFaultWord = 0;
 
 // ---- error reporting (thread-local message, status code returned) ----
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));

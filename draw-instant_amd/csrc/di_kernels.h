@@ -29,9 +29,9 @@ void launch_fill_const(hipStream_t s, void* dst, int dt, uint64_t n, float v);
 int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const float* beta,
                            void* y, uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW,
                            float eps, bool silu, int dt);
-// NHWC fp16 group norm (two kernels: partial stats + last-block fold, apply).
-// `ws` needs gn_nhwc_ws_floats() floats; `sync` = Ctx::sync_words.
-uint32_t gn_nhwc_chunks(uint32_t HW, uint32_t C);
+// NHWC fp16 group norm (two kernels: per-chunk partial stats; fold + apply).
+// `ws` needs gn_nhwc_ws_floats() floats.
+uint32_t gn_nhwc_chunks(uint32_t N, uint32_t HW);
 uint64_t gn_nhwc_ws_floats(uint32_t N, uint32_t C, uint32_t G, uint32_t HW);
 // Channel concat of two NHWC fp16 sources: channel c < c1 from p1 (pixel
 // stride ld1), else channel c - c1 from p2 (pixel stride ld2); c1 % 8 == 0.
@@ -47,7 +47,7 @@ struct NhwcSrc {
 };
 void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const float* beta,
                             void* y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW,
-                            float eps, bool silu, float* ws, uint32_t* sync);
+                            float eps, bool silu, float* ws);
 void launch_layer_norm(hipStream_t s, const void* x, const float* gamma,
                        const float* beta, void* y, uint32_t rows, uint32_t inner,
                        float eps, int dt);

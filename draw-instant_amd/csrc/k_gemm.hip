@@ -24,6 +24,7 @@
 // v_mfma_f32_16x16x4_f32 (k = l/16).  Split-K writes fp32 partials that a
 // second kernel reduces and passes through the same epilogue.
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 
 #include "di_device.h"
@@ -120,8 +121,177 @@ __device__ __forceinline__ void store_out(const GemmArgs& g, uint32_t bz, uint32
   else ((f16*)g.c)[off] = (f16)v;
 }
 
+// ---- vector epilogue (8 consecutive columns per thread) ----
+__device__ __forceinline__ void act8(int act, float* v) {
+  switch (act) {
+    case ACT_GELU:
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = gelu_erf_f(v[j]);
+      break;
+    case ACT_SILU:
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = silu_f(v[j]);
+      break;
+    case ACT_GELU_TANH:
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = gelu_tanh_f(v[j]);
+      break;
+    default:
+      break;
+  }
+}
+
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; }
+
+// x = act(x*alpha + bias[n..n+8) + bias2[(m/rows_b2)*ld_b2 + n..]) for one
+// vector whose operand loads (bb = bias, tb = bias2) were issued earlier.
+__device__ __forceinline__ void epi_math8(const GemmArgs& g, float* x, const f32x4* bb,
+                                          const f32x4* tb) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    float v = x[j] * g.alpha;
+    if (g.bias) v += bb[j >> 2][j & 3];
+    if (g.bias2) v += tb[j >> 2][j & 3];
+    x[j] = v;
+  }
+  act8(g.act, x);
+}
+
+// Writes (GEGLU-combined when act == GEGLU) results for the rows/columns of
+// one C tile staged in LDS as fp32 sC[BM][LDC].  Split-K partials are
+// stored as fp32 vectors instead.  All operand loads of a batch of vectors
+// are issued before any is consumed.
+template <int BM, int BN, int LDC>
+__device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float* sC, uint32_t m0,
+                                                  uint32_t n0, uint32_t bz, uint32_t split) {
+  const int tid = threadIdx.x;
+  if (g.splits > 1) {
+    constexpr int VPR4 = BN / 4;
+    constexpr int NV = (BM * VPR4 + 255) / 256;
+    float* P = g.part + ((uint64_t)split * g.batch + bz) * (uint64_t)g.M * g.N;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const int idx = tid + v * 256;
+      if (idx < BM * VPR4) {
+        const int r = idx / VPR4, c4 = (idx % VPR4) * 4;
+        const uint32_t m = m0 + r, n = n0 + c4;
+        if (m < g.M && n < g.N) *(f32x4*)&P[(uint64_t)m * g.N + n] = ld4(&sC[r * LDC + c4]);
+      }
+    }
+    return;
+  }
+  f16* C = (f16*)g.c + (uint64_t)bz * g.sc;
+  const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr;
+  if (g.act == ACT_GEGLU) {
+    // 32-column groups [16 hidden | 16 gate]; a vector is 8 outputs from
+    // hidden columns cl..cl+7 and gate columns cl+16..cl+23.
+    constexpr int VPRG = BN / 16;
+    constexpr int NV = (BM * VPRG + 255) / 256;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const int idx = tid + v * 256;
+      if (idx >= BM * VPRG) break;
+      const int r = idx / VPRG, q = idx % VPRG, cl = (q >> 1) * 32 + (q & 1) * 8;
+      const uint32_t m = m0 + r, nh = n0 + cl;
+      const bool ok = m < g.M && nh < g.N;
+      const uint32_t nhc = ok ? nh : n0;
+      f32x4 bh[2] = {}, bg[2] = {};
+      if (g.bias) {
+        bh[0] = ld4(g.bias + nhc);
+        bh[1] = ld4(g.bias + nhc + 4);
+        bg[0] = ld4(g.bias + nhc + 16);
+        bg[1] = ld4(g.bias + nhc + 20);
+      }
+      const uint32_t f = (nh / 32) * 16 + (nh % 32);
+      f16x8 rv = {};
+      if (g.res) rv = *(const f16x8*)(R + (uint64_t)(ok ? m : m0) * g.ldr + (ok ? f : 0));
+      float h[8], gt[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        h[j] = sC[r * LDC + cl + j];
+        gt[j] = sC[r * LDC + cl + 16 + j];
+      }
+      // bias only (no bias2 / activation on GEGLU projections)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float hv = h[j] * g.alpha + (g.bias ? bh[j >> 2][j & 3] : 0.0f);
+        const float gv = gt[j] * g.alpha + (g.bias ? bg[j >> 2][j & 3] : 0.0f);
+        h[j] = hv * gelu_erf_f(gv);
+        if (g.res) h[j] += (float)rv[j];
+      }
+      if (ok) {
+        f16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = (f16)h[j];
+        *(f16x8*)(C + (uint64_t)m * g.ldc + f) = o;
+      }
+    }
+    return;
+  }
+  constexpr int VPR8 = BN / 8;
+  constexpr int NV = (BM * VPR8 + 255) / 256;
+  constexpr int CH = NV < 4 ? NV : 4;  // vectors per load batch
+#pragma unroll
+  for (int v0 = 0; v0 < NV; v0 += CH) {
+    f32x4 bb[CH][2], tb[CH][2];
+    f16x8 rr[CH];
+    uint32_t mm[CH], nn[CH];
+    bool okv[CH];
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      const int idx = tid + (v0 + u) * 256;
+      const int r = idx / VPR8, c8 = (idx % VPR8) * 8;
+      mm[u] = m0 + r;
+      nn[u] = n0 + c8;
+      okv[u] = v0 + u < NV && idx < BM * VPR8 && mm[u] < g.M && nn[u] < g.N;
+    }
+    if (g.bias) {
+#pragma unroll
+      for (int u = 0; u < CH; u++) {
+        const uint32_t nc = okv[u] ? nn[u] : n0;
+        bb[u][0] = ld4(g.bias + nc);
+        bb[u][1] = ld4(g.bias + nc + 4);
+      }
+    }
+    if (g.bias2) {
+#pragma unroll
+      for (int u = 0; u < CH; u++) {
+        const uint32_t mc = okv[u] ? mm[u] : m0, nc = okv[u] ? nn[u] : n0;
+        const float* t = g.bias2 + (uint64_t)(mc / g.rows_b2) * g.ld_b2 + nc;
+        tb[u][0] = ld4(t);
+        tb[u][1] = ld4(t + 4);
+      }
+    }
+    if (g.res) {
+#pragma unroll
+      for (int u = 0; u < CH; u++) {
+        const uint32_t mc = okv[u] ? mm[u] : m0, nc = okv[u] ? nn[u] : n0;
+        rr[u] = *(const f16x8*)(R + (uint64_t)mc * g.ldr + nc);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      if (!okv[u]) continue;
+      const int idx = tid + (v0 + u) * 256;
+      const int r = idx / VPR8, c8 = (idx % VPR8) * 8;
+      float x[8];
+      const f32x4 a0 = ld4(&sC[r * LDC + c8]), a1 = ld4(&sC[r * LDC + c8 + 4]);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        x[j] = a0[j];
+        x[j + 4] = a1[j];
+      }
+      epi_math8(g, x, bb[u], tb[u]);
+      f16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rr[u][j] : x[j]);
+      *(f16x8*)(C + (uint64_t)mm[u] * g.ldc + nn[u]) = o;
+    }
+  }
+}
+
 // ---- the GEMM kernel ----
-template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST>
+template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   using MT = Mfma<T>;
   constexpr int KV = MT::KV;
@@ -135,8 +305,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   static_assert(WGM * WGN == 4, "4 wavefronts");
   static_assert(NVA >= 1 && NVB >= 1 && TM >= 1 && TN >= 1, "tile too small");
 
-  __shared__ __attribute__((aligned(16))) T sA[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) T sB[2][BN * LDK];
+  // Pipeline buffers sA[2][BM*LDK], sB[2][BN*LDK]; reused by the fp32 C tile
+  // of the vector epilogue.
+  __shared__ __attribute__((aligned(16))) T smem[2 * (BM + BN) * LDK];
+  T (*sA)[BM * LDK] = reinterpret_cast<T (*)[BM * LDK]>(smem);
+  T (*sB)[BN * LDK] = reinterpret_cast<T (*)[BN * LDK]>(smem + 2 * BM * LDK);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
@@ -416,31 +589,32 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
   };
 
-  // Software pipeline, prefetch distance 2: stage s is loaded into registers
-  // at iteration s-3, stored to LDS buffer s%2 at iteration s-1 and consumed
-  // at iteration s, so each global load has two iterations of MFMA work to
-  // arrive.  Unrolled by two so both register sets stay in registers.
+  // FAST path: a ring of D register stages.  Sub-step s issues the loads of
+  // stage s+D into the slot stage s just left, computes stage s from LDS
+  // buffer s%2, then stores stage s+1 (loaded D-1 sub-steps earlier) into the
+  // other buffer; one barrier per stage.  D stages are in flight, so each
+  // global load has D-1 stages of work to arrive.  Loads past the last stage
+  // read zeros (offsets out of range) and stages past the end skip their MFMA
+  // work, so the loop body has no branches around loads and the waitcnt pass
+  // keeps exact vmcnt counts.
   Stage r0, r1;
   if constexpr (FAST) {
-    // Loads past the last stage read zeros (offsets out of range), so the
-    // steady state runs without conditions and the waitcnt pass can keep
-    // one stage of loads in flight across each LDS store.
+    static_assert(D % 2 == 0, "even ring depth: LDS buffer = stage parity");
+    Stage r[D];
     if (n_stages > 0) {
-      load(0, r0);
-      store_stage(0, r0);
-      load(1, r1);
-      load(2, r0);
+#pragma unroll
+      for (int j = 0; j < D; j++) load(j, r[j]);
+      store_stage(0, r[0]);
       __syncthreads();
-      // one exit, at the bottom: an odd trailing stage multiplies zeros
-      for (int s = 0; s < n_stages; s += 2) {
-        compute(0);
-        store_stage(1, r1);
-        __syncthreads();
-        load(s + 3, r1);
-        compute(1);
-        store_stage(0, r0);
-        __syncthreads();
-        load(s + 4, r0);
+      for (int s0 = 0; s0 < n_stages; s0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+          const int s = s0 + j;
+          load(s + D, r[j]);
+          if (s < n_stages) compute(j & 1);
+          store_stage((j + 1) & 1, r[(j + 1) % D]);
+          __syncthreads();
+        }
       }
     }
   } else {
@@ -466,6 +640,24 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
   // ---- epilogue ----
   const uint32_t rq = (lane >> 4) * 4;
+  if constexpr (sizeof(T) == 2) {
+    if (g.vec_epi) {
+      constexpr int LDC = BN + 4;
+      static_assert(BM * LDC * 4 <= (int)sizeof(smem), "C tile fits the pipeline LDS");
+      float* sC = reinterpret_cast<float*>(smem);
+      __syncthreads();  // every wave is done reading the last stage
+#pragma unroll
+      for (int a = 0; a < TM; a++)
+#pragma unroll
+        for (int b = 0; b < TN; b++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            sC[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr] = acc[a][b][i];
+      __syncthreads();
+      gemm_epilogue_vec<BM, BN, LDC>(g, sC, m0, n0, bz, split);
+      return;
+    }
+  }
   if (splits > 1) {
     float* P = g.part + ((uint64_t)split * g.batch + bz) * (uint64_t)g.M * g.N;
 #pragma unroll
@@ -543,10 +735,87 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
   }
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST>
+// Vector split-K reduction + epilogue (vec_epi): one thread per 8 output
+// columns; the partials of all splits are summed in split order.
+__device__ __forceinline__ void sum_splits8(const GemmArgs& g, uint32_t bz, uint32_t m, uint32_t n,
+                                            float* out) {
+  const uint64_t mn = (uint64_t)g.M * g.N;
+  const float* p = g.part + (uint64_t)bz * mn + (uint64_t)m * g.N + n;
+  const uint64_t step = (uint64_t)g.batch * mn;
+#pragma unroll
+  for (int j = 0; j < 8; j++) out[j] = 0.0f;
+  for (uint32_t s0 = 0; s0 < g.splits; s0 += 8) {
+    f32x4 t[8][2];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint32_t sp = s0 + u < g.splits ? s0 + u : s0;
+      t[u][0] = ld4(p + sp * step);
+      t[u][1] = ld4(p + sp * step + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      if (s0 + u < g.splits) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          out[j] += t[u][0][j];
+          out[j + 4] += t[u][1][j];
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
+  const bool geglu = g.act == ACT_GEGLU;
+  const uint32_t ncols = geglu ? g.N / 2 : g.N;
+  const uint32_t vpr = ncols / 8;
+  const uint64_t total = (uint64_t)g.batch * g.M * vpr;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const uint32_t c8 = (uint32_t)(i % vpr) * 8;
+    const uint64_t t = i / vpr;
+    const uint32_t m = (uint32_t)(t % g.M), bz = (uint32_t)(t / g.M);
+    f16* C = (f16*)g.c + (uint64_t)bz * g.sc + (uint64_t)m * g.ldc + c8;
+    const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr + (uint64_t)m * g.ldr + c8;
+    float x[8];
+    if (geglu) {
+      const uint32_t nh = (c8 / 16) * 32 + c8 % 16;
+      float gt[8];
+      sum_splits8(g, bz, m, nh, x);
+      sum_splits8(g, bz, m, nh + 16, gt);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float hv = x[j] * g.alpha + (g.bias ? g.bias[nh + j] : 0.0f);
+        const float gv = gt[j] * g.alpha + (g.bias ? g.bias[nh + 16 + j] : 0.0f);
+        x[j] = hv * gelu_erf_f(gv);
+      }
+    } else {
+      f32x4 bb[2] = {}, tb[2] = {};
+      if (g.bias) {
+        bb[0] = ld4(g.bias + c8);
+        bb[1] = ld4(g.bias + c8 + 4);
+      }
+      if (g.bias2) {
+        const float* tp = g.bias2 + (uint64_t)(m / g.rows_b2) * g.ld_b2 + c8;
+        tb[0] = ld4(tp);
+        tb[1] = ld4(tp + 4);
+      }
+      sum_splits8(g, bz, m, c8, x);
+      epi_math8(g, x, bb, tb);
+    }
+    f16x8 rv = {};
+    if (g.res) rv = *(const f16x8*)R;
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rv[j] : x[j]);
+    *(f16x8*)C = o;
+  }
+}
+
+template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D = 2>
 void launch_cfg(const GemmArgs& g, hipStream_t s) {
   uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST><<<dim3(tiles, 1, g.batch * g.splits), 256, 0, s>>>(g);
+  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D><<<dim3(tiles, 1, g.batch * g.splits), 256, 0, s>>>(g);
 }
 
 // Generic (bounds-checked) variants: two tile shapes.
@@ -559,17 +828,21 @@ void launch_slow(const GemmArgs& g, int tile_cfg, hipStream_t s) {
     launch_cfg<T, 128, 128, 2, 2, AM, BMD, false>(g, s);
 }
 
-// Buffer-load variants: every tile shape.
-template <int AM>
-void launch_fast(const GemmArgs& g, int tile_cfg, hipStream_t s) {
+// Buffer-load variants: every tile shape, ring depth D.
+template <int AM, int D>
+void launch_fast_d(const GemmArgs& g, int tile_cfg, hipStream_t s) {
   switch (tile_cfg) {
-    case TILE_128x160: launch_cfg<f16, 128, 160, 2, 2, AM, B_NK, true>(g, s); break;
-    case TILE_128x128: launch_cfg<f16, 128, 128, 2, 2, AM, B_NK, true>(g, s); break;
-    case TILE_128x64: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true>(g, s); break;
-    case TILE_64x160: launch_cfg<f16, 64, 160, 2, 2, AM, B_NK, true>(g, s); break;
-    case TILE_64x128: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true>(g, s); break;
-    default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true>(g, s); break;
+    case TILE_128x128: launch_cfg<f16, 128, 128, 2, 2, AM, B_NK, true, D>(g, s); break;
+    case TILE_128x64: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D>(g, s); break;
+    case TILE_64x160: launch_cfg<f16, 64, 160, 2, 2, AM, B_NK, true, D>(g, s); break;
+    case TILE_64x128: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D>(g, s); break;
+    default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D>(g, s); break;
   }
+}
+template <int AM>
+void launch_fast(const GemmArgs& g, int tile_cfg, int depth, hipStream_t s) {
+  if (depth >= 4) launch_fast_d<AM, 4>(g, tile_cfg, s);
+  else launch_fast_d<AM, 2>(g, tile_cfg, s);
 }
 
 const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64};
@@ -592,6 +865,7 @@ GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
   const double cus = num_cus;
   double best_t = 1e300;
   for (int tc = 0; tc < TILE_COUNT; tc++) {
+    if (tc == TILE_128x160) continue;  // spills registers: not built
     if (g.act == ACT_GEGLU && kTileN[tc] == 160) continue;  // GEGLU pairs need even TN
     const uint64_t mt = (g.M + kTileM[tc] - 1) / kTileM[tc], nt = (g.N + kTileN[tc] - 1) / kTileN[tc];
     const uint64_t T = mt * nt * g.batch;
@@ -674,14 +948,31 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
     g.a2_bytes = g.a_bytes;
     if (g.c1 == 0) g.c1 = 0xffffffffu;
   }
+  static const bool trace = getenv("DI_TRACE_GEMM") != nullptr;
+  if (trace)
+    fprintf(stderr,
+            "[di_gemm] M=%u N=%u K=%u batch=%u amode=%d bmode=%d elem=%d cin=%u hw=%ux%u ks=%u "
+            "stride=%u up=%u tile=%d splits=%u act=%d fast=%d\n",
+            g.M, g.N, g.K, g.batch, a_mode, b_mode, elem, g.Cin, g.H, g.W, g.ks, g.stride, g.up,
+            tile_cfg, g.splits, g.act, (int)gemm_fast_ok(g, elem, a_mode, b_mode));
 #define DI_GEMM_CASE(T, AMv, BMv)                        \
   if (a_mode == AMv && b_mode == BMv) {                  \
     launch_slow<T, AMv, BMv>(g, tile_cfg, s);            \
   }
+  {
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    g.vec_epi = elem == DI_F16 && !g.c_nchw && !g.c_f32 && g.N % 8 == 0 && g.ldc % 8 == 0 &&
+                g.sc % 8 == 0 && al16(g.c) && (!g.bias || al16(g.bias)) &&
+                (!g.bias2 || (al16(g.bias2) && g.ld_b2 % 4 == 0)) &&
+                (!g.res || (!g.res_f32 && g.ldr % 8 == 0 && g.sr % 8 == 0 && al16(g.res))) &&
+                (g.act != ACT_GEGLU || g.N % 32 == 0) && tile_cfg != TILE_128x160;
+  }
   const bool fast = gemm_fast_ok(g, elem, a_mode, b_mode);
   if (fast) {
-    if (a_mode == A_DENSE) launch_fast<A_DENSE>(g, tile_cfg, s);
-    else launch_fast<A_CONV_NHWC>(g, tile_cfg, s);
+    static const char* env_depth = getenv("DI_GEMM_DEPTH");
+    const int depth = env_depth ? atoi(env_depth) : 4;
+    if (a_mode == A_DENSE) launch_fast<A_DENSE>(g, tile_cfg, depth, s);
+    else launch_fast<A_CONV_NHWC>(g, tile_cfg, depth, s);
   } else if (elem == DI_F16) {
     DI_GEMM_CASE(f16, A_DENSE, B_NK)
     else DI_GEMM_CASE(f16, A_DENSE, B_KN)
@@ -697,7 +988,13 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
     uint64_t total = (uint64_t)g.batch * g.M * ncols;
     uint64_t blocks = (total + 255) / 256;
     if (blocks > 65535ull * 8) blocks = 65535ull * 8;
-    k_splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(g);
+    if (g.vec_epi) {
+      uint64_t vblocks = (total / 8 + 255) / 256;
+      if (vblocks > 65535ull * 8) vblocks = 65535ull * 8;
+      k_splitk_reduce_vec<<<(unsigned)vblocks, 256, 0, s>>>(g);
+    } else {
+      k_splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(g);
+    }
   }
 }
 

@@ -7,19 +7,19 @@
 // beta[c], optionally followed by SiLU y/(1+e^-y).  Partial sums are fp32.
 //
 // Work decomposition is MI355X-first instead of the reference's one
-// workgroup per group (32 workgroups for 256 CUs, X read twice):
-//  * NCHW: each group is split over S workgroups; every workgroup keeps its
-//    slice in registers, publishes (sum, sumsq), meets the group's other
-//    workgroups at a bounded cross-block barrier and normalises from
-//    registers, so X is read from HBM once.  Launched cooperatively so all
-//    workgroups are co-resident; the wait is bounded and raises the context
-//    fault word instead of hanging.
-//  * NHWC fp16 (U-Net activations): one kernel reduces per-channel partials
-//    of a pixel chunk (fully coalesced rows of C), the last workgroup to finish
-//    folds them into per-group mean/rstd; a second kernel applies the affine
-//    (+SiLU) as per-channel scale/shift.  No waiting, safe under graph replay.
-#include <cstdlib>
-
+// workgroup per group (32 workgroups for 256 CUs, serial reductions): every
+// group norm is two kernels with no inter-workgroup communication,
+//  1. partial sums: ~1024 workgroups each reduce a slice of the input to
+//     (sum, sumsq) per group and write them to a workspace, no atomics;
+//  2. fold + apply: every workgroup folds the partials it needs in one fixed
+//     order (so all workgroups agree bit-for-bit), then normalises its slice.
+// Deterministic and safe under graph replay.  X is read twice; the second
+// read is usually served by the 256 MB Infinity Cache.
+//
+// Latency, not bandwidth, bounds these kernels at U-Net sizes (2.5-10 MB per
+// call), so each issues all of a round's loads (x, partials, gamma/beta)
+// before consuming any: `sched_barrier` stops the scheduler from sinking the
+// loads next to their uses, which would serialise them.
 #include "di_device.h"
 #include "di_kernels.h"
 
@@ -27,22 +27,10 @@ namespace di {
 
 namespace {
 
-constexpr uint32_t kGnBarBase = 1;              // sync words [1, 1 + 2*kGnMaxGroups)
-constexpr uint32_t kGnMaxGroups = 65536;
-constexpr uint32_t kLastBlockBase = 1 + 2 * kGnMaxGroups;  // last-block counters
-constexpr uint32_t kSpinLimit = 1u << 22;
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-__device__ __forceinline__ uint32_t ld_acquire(uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_relaxed_f(float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_relaxed_f(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Block-wide sum of two values (256 threads = 4 waves). Result valid in thread 0.
+// Block-wide sum of two values (256 threads = 4 waves), in a fixed order.
+// Result valid in thread 0.
 __device__ __forceinline__ void block_sum2(float& a, float& b, float* sh /*[2*8]*/) {
   a = wave_sum(a);
   b = wave_sum(b);
@@ -70,8 +58,8 @@ struct Vec<float, 4> {
   typedef f32x4 type;
 };
 template <>
-struct Vec<f16, 4> {
-  typedef f16x4 type;
+struct Vec<f16, 8> {
+  typedef f16x8 type;
 };
 template <typename T>
 struct Vec<T, 1> {
@@ -101,157 +89,119 @@ __device__ __forceinline__ void store_vec(T* p, const float* in) {
   }
 }
 
-// ---------------- NCHW single pass (register-resident slice) ----------------
-// grid (S, N*G), 256 threads. Slice s of group ng covers elements
-// [s*chunk, min((s+1)*chunk, L)) of the group's contiguous L = cpg*HW block.
-template <typename T, int VEC, int MAXI>
-__global__ __launch_bounds__(256) void k_gn_nchw_1pass(
-    const T* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
-    T* __restrict__ y, uint32_t G, uint32_t cpg, uint32_t HW, uint32_t S, uint32_t chunk,
-    float eps, int silu, float* __restrict__ part, uint32_t* __restrict__ sync) {
-  __shared__ float sh[16];
-  __shared__ float s_mean, s_rstd;
-  const uint32_t s = blockIdx.x, ng = blockIdx.y;
-  const uint32_t L = cpg * HW;
-  const uint64_t gbase = (uint64_t)ng * L;  // NCHW: group ng = n*G+g is contiguous
-  const uint32_t lo = s * chunk, hi = min(lo + chunk, L);
-  const uint32_t g = ng % G;
+// ---------------- NCHW (each group is one contiguous block) ----------------
+// grid (S, N*G): slice s of group ng covers elements [s*chunk, min((s+1)*chunk,
+// L)) of the group's L = cpg*HW elements; every slice is non-empty and VEC
+// divides HW (so a vector never straddles a channel) and chunk.
+constexpr int kNchwU = 4;  // vectors per thread per round
 
-  float v[MAXI][VEC];
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void k_gn_nchw_partial(const T* __restrict__ x, uint32_t L,
+                                                          uint32_t chunk,
+                                                          float* __restrict__ part) {
+  __shared__ float sh[16];
+  const uint32_t s = blockIdx.x, ng = blockIdx.y, S = gridDim.x;
+  const T* xg = x + (uint64_t)ng * L;
+  const uint32_t lo = s * chunk, hi = min(lo + chunk, L);
   float ts = 0.0f, tq = 0.0f;
+  for (uint32_t b = lo; b < hi; b += 256 * VEC * kNchwU) {
+    float v[kNchwU][VEC];
 #pragma unroll
-  for (int k = 0; k < MAXI; k++) {
-    uint32_t e = lo + (k * 256 + threadIdx.x) * VEC;
-    if (e < hi) {
-      load_vec<T, VEC>(x + gbase + e, v[k]);
+    for (int u = 0; u < kNchwU; u++) {
+      const uint32_t e = b + (u * 256 + threadIdx.x) * VEC;
+      load_vec<T, VEC>(xg + (e < hi ? e : lo), v[u]);
+    }
+    sched_fence();
+#pragma unroll
+    for (int u = 0; u < kNchwU; u++) {
+      const bool ok = b + (u * 256 + threadIdx.x) * VEC < hi;
 #pragma unroll
       for (int j = 0; j < VEC; j++) {
-        ts += v[k][j];
-        tq += v[k][j] * v[k][j];
+        const float f = ok ? v[u][j] : 0.0f;
+        ts += f;
+        tq += f * f;
       }
     }
   }
   block_sum2(ts, tq, sh);
   if (threadIdx.x == 0) {
-    float* pp = part + ((uint64_t)ng * S + s) * 2;
-    st_relaxed_f(pp, ts);
-    st_relaxed_f(pp + 1, tq);
-    uint32_t* cnt = sync + kGnBarBase + 2 * ng;
-    uint32_t* gen = cnt + 1;
-    uint32_t g0 = ld_acquire(gen);
-    __threadfence();
-    uint32_t arrived = atomicAdd(cnt, 1u);
-    if (arrived == S - 1) {
-      atomicExch(cnt, 0u);
-      __threadfence();
-      atomicAdd(gen, 1u);
-    } else {
-      uint32_t spins = 0;
-      while (ld_acquire(gen) == g0) {
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > kSpinLimit) {
-          atomicOr(sync + kFaultWord, 1u);
-          break;
-        }
-      }
+    part[((uint64_t)ng * S + s) * 2] = ts;
+    part[((uint64_t)ng * S + s) * 2 + 1] = tq;
+  }
+}
+
+// Same grid.  Folds the group's S <= 256 partials (one load per thread, fixed
+// order), then y = x * a[c] + b[c] (+SiLU) over the slice.  The first round of
+// x and its gamma/beta are loaded before the fold.
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void k_gn_nchw_apply(const T* __restrict__ x,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta,
+                                                        T* __restrict__ y, uint32_t G,
+                                                        uint32_t cpg, uint32_t HW, uint32_t chunk,
+                                                        float eps, int silu,
+                                                        const float* __restrict__ part) {
+  __shared__ float sh[16];
+  __shared__ float s_mean, s_rstd;
+  const uint32_t s = blockIdx.x, ng = blockIdx.y, S = gridDim.x;
+  const uint32_t L = cpg * HW;
+  const uint64_t gbase = (uint64_t)ng * L;
+  const uint32_t c0 = (ng % G) * cpg;
+  const uint32_t lo = s * chunk, hi = min(lo + chunk, L);
+  float v[kNchwU][VEC], gm[kNchwU], bt[kNchwU];
+  auto load_round = [&](uint32_t b) {
+#pragma unroll
+    for (int u = 0; u < kNchwU; u++) {
+      uint32_t e = b + (u * 256 + threadIdx.x) * VEC;
+      e = e < hi ? e : lo;
+      load_vec<T, VEC>(x + gbase + e, v[u]);
+      gm[u] = gamma[c0 + e / HW];
+      bt[u] = beta[c0 + e / HW];
     }
-    __threadfence();
-    float sum = 0.0f, sq = 0.0f;
-    const float* pg = part + (uint64_t)ng * S * 2;
-    for (uint32_t j = 0; j < S; j++) {
-      sum += ld_relaxed_f((float*)pg + 2 * j);
-      sq += ld_relaxed_f((float*)pg + 2 * j + 1);
-    }
-    float mean = sum / (float)L;
-    float var = fmaxf(sq / (float)L - mean * mean, 0.0f);
+  };
+  load_round(lo);
+  float ps = 0.0f, pq = 0.0f;
+  if (threadIdx.x < S) {
+    ps = part[((uint64_t)ng * S + threadIdx.x) * 2];
+    pq = part[((uint64_t)ng * S + threadIdx.x) * 2 + 1];
+  }
+  sched_fence();
+  block_sum2(ps, pq, sh);
+  if (threadIdx.x == 0) {
+    const float mean = ps / (float)L;
+    const float var = fmaxf(pq / (float)L - mean * mean, 0.0f);
     s_mean = mean;
     s_rstd = 1.0f / sqrtf(var + eps);
   }
   __syncthreads();
   const float mean = s_mean, rstd = s_rstd;
-#pragma unroll
-  for (int k = 0; k < MAXI; k++) {
-    uint32_t e = lo + (k * 256 + threadIdx.x) * VEC;
-    if (e < hi) {
-      // VEC divides HW, so the VEC elements of a vector share one channel.
-      const uint32_t c = g * cpg + e / HW;
-      const float a = rstd * gamma[c], b = beta[c] - mean * a;
-      float o[VEC];
-#pragma unroll
-      for (int j = 0; j < VEC; j++) {
-        float t = v[k][j] * a + b;
-        o[j] = silu ? silu_f(t) : t;
-      }
-      store_vec<T, VEC>(y + gbase + e, o);
+  for (uint32_t b = lo; b < hi; b += 256 * VEC * kNchwU) {
+    if (b != lo) {
+      load_round(b);
+      sched_fence();
     }
-  }
-}
-
-// ---------------- NCHW two-pass fallback (any size) ----------------
-// Pass 1: grid (S, N*G) partial sums; the last workgroup of each group folds
-// them into (mean, rstd).  Pass 2: grid-stride normalise.
-template <typename T>
-__global__ __launch_bounds__(256) void k_gn_nchw_stats(const T* __restrict__ x, uint32_t L,
-                                                       uint32_t S, uint32_t chunk, float eps,
-                                                       float* __restrict__ part,
-                                                       float* __restrict__ stats,
-                                                       uint32_t* __restrict__ sync) {
-  __shared__ float sh[16];
-  __shared__ bool last;
-  const uint32_t s = blockIdx.x, ng = blockIdx.y;
-  const uint64_t gbase = (uint64_t)ng * L;
-  const uint32_t lo = s * chunk, hi = min(lo + chunk, L);
-  float ts = 0.0f, tq = 0.0f;
-  for (uint32_t e = lo + threadIdx.x; e < hi; e += 256) {
-    float v = (float)x[gbase + e];
-    ts += v;
-    tq += v * v;
-  }
-  block_sum2(ts, tq, sh);
-  if (threadIdx.x == 0) {
-    float* pp = part + ((uint64_t)ng * S + s) * 2;
-    st_relaxed_f(pp, ts);
-    st_relaxed_f(pp + 1, tq);
-    __threadfence();
-    uint32_t* cnt = sync + kLastBlockBase + ng;
-    last = atomicAdd(cnt, 1u) == S - 1;
-    if (last) {
-      __threadfence();
-      float sum = 0.0f, sq = 0.0f;
-      for (uint32_t j = 0; j < S; j++) {
-        sum += ld_relaxed_f(part + ((uint64_t)ng * S + j) * 2);
-        sq += ld_relaxed_f(part + ((uint64_t)ng * S + j) * 2 + 1);
+#pragma unroll
+    for (int u = 0; u < kNchwU; u++) {
+      const uint32_t e = b + (u * 256 + threadIdx.x) * VEC;
+      if (e < hi) {
+        const float a = rstd * gm[u], sb = bt[u] - mean * a;
+        float o[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+          const float t = v[u][j] * a + sb;
+          o[j] = silu ? silu_f(t) : t;
+        }
+        store_vec<T, VEC>(y + gbase + e, o);
       }
-      float mean = sum / (float)L;
-      float var = fmaxf(sq / (float)L - mean * mean, 0.0f);
-      stats[2 * ng] = mean;
-      stats[2 * ng + 1] = 1.0f / sqrtf(var + eps);
-      atomicExch(cnt, 0u);
     }
-  }
-}
-
-template <typename T>
-__global__ __launch_bounds__(256) void k_gn_nchw_apply(const T* __restrict__ x,
-                                                       const float* __restrict__ gamma,
-                                                       const float* __restrict__ beta,
-                                                       T* __restrict__ y, uint32_t G,
-                                                       uint32_t cpg, uint32_t HW, uint64_t n,
-                                                       int silu,
-                                                       const float* __restrict__ stats) {
-  const uint64_t L = (uint64_t)cpg * HW;
-  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    uint64_t ng = i / L;
-    uint32_t c = (uint32_t)(ng % G) * cpg + (uint32_t)((i % L) / HW);
-    float t = ((float)x[i] - stats[2 * ng]) * stats[2 * ng + 1] * gamma[c] + beta[c];
-    y[i] = (T)(silu ? silu_f(t) : t);
   }
 }
 
 // ---------------- NHWC fp16 (U-Net path) ----------------
 // Thread layout for a row of C channels: CV = C/8 vectors of 8 halfs;
-// cvb = min(CV, 256) threads across the row, R = 256/cvb pixel lanes.
+// cvb = min(CV, 256) threads across the row, R = 256/cvb pixel lanes, and
+// KV = ceil(CV/cvb) <= 2 vectors per thread.  Every thread keeps the same
+// channels for all its pixels.
 struct NhwcMap {
   uint32_t CV, cvb, R, kv;
 };
@@ -264,130 +214,313 @@ __host__ __device__ inline NhwcMap nhwc_map(uint32_t C) {
   return m;
 }
 
-constexpr int kMaxKV = 2;  // C <= 4096
+// Per-thread view of its (up to KV) channel vectors in the two-source input.
+template <int KV>
+struct NhwcLane {
+  const f16* base[KV];
+  uint64_t ld[KV];
+  bool ok[KV];
+  uint32_t cv[KV];
+  __device__ NhwcLane(const NhwcSrc& x, const NhwcMap& m, uint32_t lane_cv) {
+#pragma unroll
+    for (int k = 0; k < KV; k++) {
+      cv[k] = lane_cv + k * m.cvb;
+      ok[k] = cv[k] < m.CV;
+      const uint32_t c = ok[k] ? cv[k] * 8 : 0;  // clamped: loads stay in bounds
+      const bool first = c < x.c1;
+      base[k] = first ? x.p1 + c : x.p2 + (c - x.c1);
+      ld[k] = first ? x.ld1 : x.ld2;
+    }
+  }
+  __device__ __forceinline__ f16x8 load(int k, uint64_t pix) const {
+    return *(const f16x8*)(base[k] + pix * ld[k]);
+  }
+};
 
-// grid (chunks, N). Per-channel partial sums of pixel chunk -> per-group
-// partials; the last workgroup of image n folds all chunks into mean/rstd.
-__global__ __launch_bounds__(256) void k_gn_nhwc_stats(
-    NhwcSrc x, uint32_t C, uint32_t G, uint32_t HW, uint32_t ppc, float eps,
-    float* __restrict__ part /*[N][chunks][G][2]*/, float* __restrict__ stats /*[N][G][2]*/,
-    uint32_t* __restrict__ sync) {
-  extern __shared__ float csh[];  // [R][2][C] per pixel-lane, per-channel sum / sumsq
-  __shared__ bool last;
+// pixel loads in flight per thread: 8 vectors of 16 bytes
+template <int KV>
+constexpr int gn_unroll() {
+  return 8 / KV;
+}
+
+// Pass 1, grid (chunks, N): per-(chunk, group) partial sum / sum of squares
+// part[n][chunk][g][2], written without atomics.  A round's loads use pixel
+// indices clamped into the chunk and are masked afterwards.
+template <int KV>
+__global__ __launch_bounds__(256) void k_gn_nhwc_partial(NhwcSrc x, uint32_t C, uint32_t G,
+                                                          uint32_t HW, uint32_t ppc,
+                                                          float* __restrict__ part) {
+  extern __shared__ float csh[];  // [R][2][C]: per pixel lane, per-channel sum / sumsq
   const uint32_t chunk = blockIdx.x, n = blockIdx.y, chunks = gridDim.x;
   const NhwcMap m = nhwc_map(C);
   const uint32_t p0 = chunk * ppc, p1 = min(p0 + ppc, HW);
   const uint32_t lane_cv = threadIdx.x % m.cvb, pl = threadIdx.x / m.cvb;
   if (pl < m.R) {
-    float s[kMaxKV][8], q[kMaxKV][8];
+    const NhwcLane<KV> ln(x, m, lane_cv);
+    float s[KV][8], q[KV][8];
 #pragma unroll
-    for (int k = 0; k < kMaxKV; k++)
+    for (int k = 0; k < KV; k++)
 #pragma unroll
       for (int j = 0; j < 8; j++) s[k][j] = q[k][j] = 0.0f;
-    for (uint32_t p = p0 + pl; p < p1; p += m.R) {
-      const uint64_t pix = (uint64_t)n * HW + p;
+    const uint32_t cnt = p0 + pl < p1 ? (p1 - p0 - pl + m.R - 1) / m.R : 0;
+    const uint64_t pix0 = (uint64_t)n * HW + p0 + pl;
+    constexpr int U = gn_unroll<KV>();
+    for (uint32_t i = 0; i < cnt; i += U) {
+      f16x8 v[U][KV];
 #pragma unroll
-      for (int k = 0; k < kMaxKV; k++) {
-        uint32_t cv = lane_cv + k * m.cvb;
-        if (k < (int)m.kv && cv < m.CV) {
-          f16x8 v = x.load8(pix, cv * 8);
+      for (int u = 0; u < U; u++) {
+        const uint32_t ii = min(i + u, cnt - 1);
+#pragma unroll
+        for (int k = 0; k < KV; k++) v[u][k] = ln.load(k, pix0 + (uint64_t)ii * m.R);
+      }
+      sched_fence();
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+#pragma unroll
+        for (int k = 0; k < KV; k++) {
+          const bool valid = (i + u < cnt) && ln.ok[k];
 #pragma unroll
           for (int j = 0; j < 8; j++) {
-            float f = (float)v[j];
+            const float f = valid ? (float)v[u][k][j] : 0.0f;
             s[k][j] += f;
             q[k][j] += f * f;
           }
         }
       }
     }
-    // every (pixel-lane, channel) slot is written by exactly one thread
 #pragma unroll
-    for (int k = 0; k < kMaxKV; k++) {
-      uint32_t cv = lane_cv + k * m.cvb;
-      if (k < (int)m.kv && cv < m.CV) {
+    for (int k = 0; k < KV; k++) {
+      if (ln.ok[k]) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          csh[(pl * 2) * C + cv * 8 + j] = s[k][j];
-          csh[(pl * 2 + 1) * C + cv * 8 + j] = q[k][j];
+          csh[pl * 2 * C + ln.cv[k] * 8 + j] = s[k][j];
+          csh[pl * 2 * C + C + ln.cv[k] * 8 + j] = q[k][j];
         }
       }
     }
   }
   __syncthreads();
+  // per channel and statistic: sum over pixel lanes in fixed order (in place
+  // into row 0; entry i is touched by one thread only)
+  for (uint32_t i = threadIdx.x; i < 2 * C; i += 256) {
+    float a = csh[i];
+    for (uint32_t r = 1; r < m.R; r++) a += csh[r * 2 * C + i];
+    csh[i] = a;
+  }
+  __syncthreads();
   const uint32_t cpg = C / G;
-  if (threadIdx.x < G) {
-    uint32_t g = threadIdx.x;
-    float a = 0.0f, b = 0.0f;
-    for (uint32_t r = 0; r < m.R; r++)  // fixed order: deterministic
-      for (uint32_t c = g * cpg; c < (g + 1) * cpg; c++) {
-        a += csh[(r * 2) * C + c];
-        b += csh[(r * 2 + 1) * C + c];
-      }
-    float* pp = part + (((uint64_t)n * chunks + chunk) * G + g) * 2;
-    st_relaxed_f(pp, a);
-    st_relaxed_f(pp + 1, b);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    uint32_t* cnt = sync + kLastBlockBase + kGnMaxGroups + n;
-    last = atomicAdd(cnt, 1u) == chunks - 1;
-    if (last) atomicExch(cnt, 0u);
-  }
-  __syncthreads();
-  if (last && threadIdx.x < G) {
-    __threadfence();
-    uint32_t g = threadIdx.x;
-    float a = 0.0f, b = 0.0f;
-    for (uint32_t k = 0; k < chunks; k++) {
-      float* pp = part + (((uint64_t)n * chunks + k) * G + g) * 2;
-      a += ld_relaxed_f(pp);
-      b += ld_relaxed_f(pp + 1);
-    }
-    float L = (float)cpg * (float)HW;
-    float mean = a / L;
-    float var = fmaxf(b / L - mean * mean, 0.0f);
-    stats[((uint64_t)n * G + g) * 2] = mean;
-    stats[((uint64_t)n * G + g) * 2 + 1] = 1.0f / sqrtf(var + eps);
+  for (uint32_t t = threadIdx.x; t < 2 * G; t += 256) {
+    const uint32_t g = t >> 1, st = t & 1;
+    float a = 0.0f;
+    for (uint32_t c = g * cpg; c < (g + 1) * cpg; c++) a += csh[st * C + c];
+    part[(((uint64_t)n * chunks + chunk) * G) * 2 + t] = a;
   }
 }
 
-// grid (chunks, N): y = x * a[c] + b[c] (+SiLU) with a = rstd*gamma,
-// b = beta - mean*rstd*gamma folded per channel in LDS.
+// Sum of partials pn[k*P + pair] for k = sl, sl+step, ... < nk, in that order,
+// with 16 loads in flight at a time.
+__device__ __forceinline__ float gn_fold(const float* __restrict__ pn, uint32_t P, uint32_t pair,
+                                         uint32_t sl, uint32_t step, uint32_t nk) {
+  float a = 0.0f;
+  for (uint32_t k0 = sl; k0 < nk; k0 += 16 * step) {
+    float t[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const uint32_t k = k0 + u * step;
+      t[u] = pn[(uint64_t)(k < nk ? k : sl) * P + pair];
+    }
+    sched_fence();
+#pragma unroll
+    for (int u = 0; u < 16; u++) a += (k0 + u * step < nk) ? t[u] : 0.0f;
+  }
+  return a;
+}
+
+// Pass 2, grid (achunks, N): every workgroup folds the image's partials in
+// the same fixed order into mean/rstd per group (so all workgroups agree
+// bit-for-bit) and applies y = x*a[c] + b[c] (+SiLU), a = rstd*gamma[c],
+// b = beta[c] - mean*a, to its pixel range.  The first round of pixels and
+// the thread's gamma/beta are loaded before the fold.
+template <int KV>
 __global__ __launch_bounds__(256) void k_gn_nhwc_apply(
     NhwcSrc x, const float* __restrict__ gamma, const float* __restrict__ beta,
-    f16* __restrict__ y, uint32_t C, uint32_t G, uint32_t HW, uint32_t ppc, int silu,
-    const float* __restrict__ stats) {
-  extern __shared__ float ab[];  // [2*C]
+    f16* __restrict__ y, uint32_t C, uint32_t G, uint32_t HW, uint32_t ppc, uint32_t schunks,
+    float eps, int silu, const float* __restrict__ part) {
+  __shared__ float red[256];
+  __shared__ float gstat[2 * 256];  // per group: sums, then (mean, rstd)
   const uint32_t chunk = blockIdx.x, n = blockIdx.y;
-  const uint32_t cpg = C / G;
-  for (uint32_t c = threadIdx.x; c < C; c += 256) {
-    uint32_t g = c / cpg;
-    float mean = stats[((uint64_t)n * G + g) * 2], rstd = stats[((uint64_t)n * G + g) * 2 + 1];
-    float a = rstd * gamma[c];
-    ab[c] = a;
-    ab[C + c] = beta[c] - mean * a;
+  const NhwcMap m = nhwc_map(C);
+  const uint32_t lane_cv = threadIdx.x % m.cvb, pl = threadIdx.x / m.cvb;
+  const bool active = pl < m.R;
+  const NhwcLane<KV> ln(x, m, active ? lane_cv : 0);
+  const uint32_t p0 = chunk * ppc, p1 = min(p0 + ppc, HW);
+  const uint32_t cnt = active && p0 + pl < p1 ? (p1 - p0 - pl + m.R - 1) / m.R : 0;
+  constexpr int U = gn_unroll<KV>();
+  // Unconditional loads at pixel indices clamped into [p0, p1) (every chunk is
+  // non-empty), so no lane branches around them.
+  const uint64_t img = (uint64_t)n * HW;
+  const uint32_t pfirst = min(p0 + (active ? pl : 0), p1 - 1);
+  f16x8 v[U][KV];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint64_t pix = img + min(pfirst + u * m.R, p1 - 1);
+#pragma unroll
+    for (int k = 0; k < KV; k++) v[u][k] = ln.load(k, pix);
+  }
+  f32x4 gam[KV][2], bet[KV][2];
+#pragma unroll
+  for (int k = 0; k < KV; k++) {
+    const uint32_t c = (ln.ok[k] ? ln.cv[k] : 0) * 8;
+    gam[k][0] = *(const f32x4*)(gamma + c);
+    gam[k][1] = *(const f32x4*)(gamma + c + 4);
+    bet[k][0] = *(const f32x4*)(beta + c);
+    bet[k][1] = *(const f32x4*)(beta + c + 4);
+  }
+  sched_fence();
+  const uint32_t P = 2 * G;  // (group, statistic) pairs
+  const float* pn = part + (uint64_t)n * schunks * P;
+  const uint32_t slices = P <= 256 ? 256 / P : 1;
+  if (P <= 256) {
+    if (threadIdx.x < P * slices)
+      red[threadIdx.x] = gn_fold(pn, P, threadIdx.x % P, threadIdx.x / P, slices, schunks);
+  } else {
+    for (uint32_t pair = threadIdx.x; pair < P; pair += 256)
+      gstat[pair] = gn_fold(pn, P, pair, 0, 1, schunks);
   }
   __syncthreads();
-  const uint32_t CV = C / 8;
-  const uint32_t p0 = chunk * ppc, p1 = min(p0 + ppc, HW);
-  const uint64_t base = ((uint64_t)n * HW + p0) * C;
-  const uint32_t nv = (p1 - p0) * CV;
-  for (uint32_t i = threadIdx.x; i < nv; i += 256) {
-    uint32_t cv = i % CV;
-    uint64_t off = base + (uint64_t)i * 8;
-    f16x8 v = x.load8((uint64_t)n * HW + p0 + i / CV, cv * 8);
-    f16x8 o;
+  if (P <= 256 && threadIdx.x < P) {
+    float a = 0.0f;
+    for (uint32_t sl = 0; sl < slices; sl++) a += red[sl * P + threadIdx.x];
+    gstat[threadIdx.x] = a;
+  }
+  __syncthreads();
+  const uint32_t cpg = C / G;
+  const float L = (float)cpg * (float)HW;
+  if (G <= 128 && threadIdx.x < G) {
+    const float mean = gstat[2 * threadIdx.x] / L;
+    const float var = fmaxf(gstat[2 * threadIdx.x + 1] / L - mean * mean, 0.0f);
+    red[threadIdx.x] = mean;
+    red[128 + threadIdx.x] = 1.0f / sqrtf(var + eps);
+  }
+  // G <= 128 keeps mean/rstd in `red`; larger G reuses gstat in place.
+  __syncthreads();
+  if (G > 128) {
+    for (uint32_t g = threadIdx.x; g < G; g += 256) {
+      const float mean = gstat[2 * g] / L;
+      const float var = fmaxf(gstat[2 * g + 1] / L - mean * mean, 0.0f);
+      gstat[2 * g] = mean;
+      gstat[2 * g + 1] = 1.0f / sqrtf(var + eps);
+    }
+    __syncthreads();
+  }
+  if (!active) return;
+  float sa[KV][8], sb[KV][8];
+#pragma unroll
+  for (int k = 0; k < KV; k++) {
+    const uint32_t cb = (ln.ok[k] ? ln.cv[k] : 0) * 8;
+    uint32_t g = cb / cpg;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      float t = (float)v[j] * ab[cv * 8 + j] + ab[C + cv * 8 + j];
-      o[j] = (f16)(silu ? silu_f(t) : t);
+      while (cb + j >= (g + 1) * cpg) g++;
+      const float mean = G > 128 ? gstat[2 * g] : red[g];
+      const float rstd = G > 128 ? gstat[2 * g + 1] : red[128 + g];
+      const float gj = j < 4 ? gam[k][0][j] : gam[k][1][j - 4];
+      const float bj = j < 4 ? bet[k][0][j] : bet[k][1][j - 4];
+      sa[k][j] = rstd * gj;
+      sb[k][j] = bj - mean * sa[k][j];
     }
-    *(f16x8*)(y + off) = o;
+  }
+  for (uint32_t i = 0; i < cnt; i += U) {
+    if (i > 0) {
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const uint64_t pix = img + min(pfirst + (i + u) * m.R, p1 - 1);
+#pragma unroll
+        for (int k = 0; k < KV; k++) v[u][k] = ln.load(k, pix);
+      }
+      sched_fence();
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (i + u >= cnt) break;
+      const uint64_t pix = img + pfirst + (i + u) * m.R;
+#pragma unroll
+      for (int k = 0; k < KV; k++) {
+        if (!ln.ok[k]) continue;
+        f16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float t = (float)v[u][k][j] * sa[k][j] + sb[k][j];
+          o[j] = (f16)(silu ? silu_f(t) : t);
+        }
+        *(f16x8*)(y + pix * C + ln.cv[k] * 8) = o;
+      }
+    }
   }
 }
 
 // ---------------- LayerNorm: one wavefront per row ----------------
+// fp16 rows with inner % 8 == 0 and inner <= 64*8*kLnMaxV stay in registers
+// (one read, vector stores); other shapes take the generic two-read loop.
+constexpr int kLnMaxV = 4;
+
+template <int NV>
+__global__ __launch_bounds__(256) void k_layer_norm_f16_reg(const f16* __restrict__ x,
+                                                            const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta,
+                                                            f16* __restrict__ y, uint32_t rows,
+                                                            uint32_t inner, float eps) {
+  const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  const f16* xr = x + (uint64_t)row * inner;
+  f16* yr = y + (uint64_t)row * inner;
+  f16x8 v[NV];
+  f32x4 gm[NV][2], bt[NV][2];
+  float s = 0.0f, q = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    uint32_t j = (lane + k * kWave) * 8;
+    j = j < inner ? j : 0;  // clamped: every lane loads in bounds
+    v[k] = *(const f16x8*)(xr + j);
+    gm[k][0] = *(const f32x4*)(gamma + j);
+    gm[k][1] = *(const f32x4*)(gamma + j + 4);
+    bt[k][0] = *(const f32x4*)(beta + j);
+    bt[k][1] = *(const f32x4*)(beta + j + 4);
+  }
+  sched_fence();
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    if ((lane + k * kWave) * 8 < inner) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float f = (float)v[k][e];
+        s += f;
+        q += f * f;
+      }
+    }
+  }
+  s = wave_sum(s);
+  q = wave_sum(q);
+  const float mean = s / (float)inner;
+  const float var = fmaxf(q / (float)inner - mean * mean, 0.0f);
+  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    const uint32_t j = (lane + k * kWave) * 8;
+    if (j < inner) {
+      const f32x4 g0 = gm[k][0], g1 = gm[k][1], b0 = bt[k][0], b1 = bt[k][1];
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        o[e] = (f16)(((float)v[k][e] - mean) * rstd * g0[e] + b0[e]);
+        o[e + 4] = (f16)(((float)v[k][e + 4] - mean) * rstd * g1[e] + b1[e]);
+      }
+      *(f16x8*)(yr + j) = o;
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_layer_norm(const T* __restrict__ x,
                                                     const float* __restrict__ gamma,
@@ -435,83 +568,46 @@ __global__ __launch_bounds__(256) void k_layer_norm(const T* __restrict__ x,
     yr[j] = (T)(((float)xr[j] - mean) * rstd * gamma[j] + beta[j]);
 }
 
-template <typename T, int VEC, int MAXI>
-int try_1pass(Ctx* c, const void* x, const float* gamma, const float* beta, void* y,
-              uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu,
-              bool* launched) {
-  *launched = false;
-  const uint32_t L = cpg * HW;
-  const uint32_t NG = N * G;
-  if (NG > kGnMaxGroups || (VEC > 1 && HW % VEC != 0)) return DI_OK;
-  auto kern = k_gn_nchw_1pass<T, VEC, MAXI>;
-  int per_cu = 0;
-  DI_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0));
-  const uint64_t resident = (uint64_t)per_cu * c->num_cus;
-  // Aim for ~2 workgroups per CU over all groups, within register capacity.
-  uint32_t S = (uint32_t)((2ull * c->num_cus + NG - 1) / NG);
-  const uint32_t per_block_max = 256 * VEC * MAXI;
-  uint32_t S_min = (L + per_block_max - 1) / per_block_max;
-  if (S < S_min) S = S_min;
+// Slice count per group for the NCHW kernels: ~1024 workgroups in total, at
+// least one vector per thread, at most 256 (one partial per thread in the fold).
+void nchw_slices(uint32_t L, uint32_t NG, uint32_t vec, uint32_t* S_out, uint32_t* chunk_out) {
+  uint32_t S = (1024 + NG - 1) / NG;
+  const uint32_t smax = (L + 256 * vec - 1) / (256 * vec);
+  if (S > smax) S = smax;
+  if (S > 256) S = 256;
   if (S < 1) S = 1;
   uint32_t chunk = (L + S - 1) / S;
-  chunk = (chunk + VEC - 1) / VEC * VEC;
-  S = (L + chunk - 1) / chunk;
-  if ((uint64_t)S * NG > resident || chunk > per_block_max) return DI_OK;
+  chunk = (chunk + vec - 1) / vec * vec;
+  *S_out = (L + chunk - 1) / chunk;
+  *chunk_out = chunk;
+}
+
+template <typename T, int VEC>
+int gn_nchw_launch(Ctx* c, const void* x, const float* gamma, const float* beta, void* y,
+                   uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu) {
+  const uint32_t L = cpg * HW, NG = N * G;
+  uint32_t S, chunk;
+  nchw_slices(L, NG, VEC, &S, &chunk);
   void* ws = nullptr;
   int rc = workspace(c, (uint64_t)NG * S * 2 * sizeof(float), &ws);
   if (rc) return rc;
-  const T* xp = (const T*)x;
-  T* yp = (T*)y;
   float* part = (float*)ws;
-  uint32_t* sync = c->sync_words;
-  int silu_i = silu ? 1 : 0;
-  void* args[] = {(void*)&xp, (void*)&gamma, (void*)&beta, (void*)&yp, (void*)&G, (void*)&cpg,
-                  (void*)&HW, (void*)&S, (void*)&chunk, (void*)&eps, (void*)&silu_i,
-                  (void*)&part, (void*)&sync};
-  // All S*NG workgroups fit on the device at once (checked above against the
-  // occupancy calculator), so a regular launch keeps them co-resident; the
-  // barrier's wait is bounded in any case.
-  if (getenv("DI_GN_COOP"))
-    DI_HIP(hipLaunchCooperativeKernel((const void*)kern, dim3(S, NG), dim3(256), args, 0,
-                                      c->stream));
-  else
-    kern<<<dim3(S, NG), 256, 0, c->stream>>>(xp, gamma, beta, yp, G, cpg, HW, S, chunk, eps,
-                                             silu_i, part, sync);
-  *launched = true;
+  k_gn_nchw_partial<T, VEC><<<dim3(S, NG), 256, 0, c->stream>>>((const T*)x, L, chunk, part);
+  k_gn_nchw_apply<T, VEC><<<dim3(S, NG), 256, 0, c->stream>>>(
+      (const T*)x, gamma, beta, (T*)y, G, cpg, HW, chunk, eps, silu ? 1 : 0, part);
   return DI_OK;
 }
 
 template <typename T>
 int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* y, uint32_t N,
             uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu) {
-  bool done = false;
-  int rc = try_1pass<T, 4, 8>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, &done);
-  if (rc || done) return rc;
-  rc = try_1pass<T, 1, 16>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, &done);
-  if (rc || done) return rc;
-  // Two-pass fallback.
-  const uint32_t L = cpg * HW, NG = N * G;
-  DI_REQUIRE(NG <= kGnMaxGroups, DI_EUNSUPPORTED, "group norm: %u groups exceed %u", NG,
-             kGnMaxGroups);
-  uint32_t S = (uint32_t)((2ull * c->num_cus + NG - 1) / NG);
-  uint32_t chunk = (L + S - 1) / S;
-  if (chunk < 1024) chunk = 1024;
-  S = (L + chunk - 1) / chunk;
-  void* ws = nullptr;
-  rc = workspace(c, ((uint64_t)NG * S * 2 + (uint64_t)NG * 2) * sizeof(float), &ws);
-  if (rc) return rc;
-  float* part = (float*)ws;
-  float* stats = part + (uint64_t)NG * S * 2;
-  k_gn_nchw_stats<T><<<dim3(S, NG), 256, 0, c->stream>>>((const T*)x, L, S, chunk, eps, part,
-                                                          stats, c->sync_words);
-  DI_LAUNCH_CHECK();
-  uint64_t n = (uint64_t)NG * L;
-  uint64_t blocks = (n + 1023) / 1024;
-  if (blocks > 65535ull * 8) blocks = 65535ull * 8;
-  k_gn_nchw_apply<T><<<(unsigned)blocks, 256, 0, c->stream>>>(
-      (const T*)x, gamma, beta, (T*)y, G, cpg, HW, n, silu ? 1 : 0, stats);
-  DI_LAUNCH_CHECK();
-  return DI_OK;
+  DI_REQUIRE((uint64_t)N * G <= 65535u, DI_EUNSUPPORTED, "group norm: %llu groups exceed 65535",
+             (unsigned long long)N * G);
+  DI_REQUIRE((uint64_t)cpg * HW < (1ull << 31), DI_EUNSUPPORTED,
+             "group norm: %llu elements per group exceed 2^31", (unsigned long long)cpg * HW);
+  constexpr int V = 16 / sizeof(T);
+  if (HW % V == 0) return gn_nchw_launch<T, V>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu);
+  return gn_nchw_launch<T, 1>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu);
 }
 
 }  // namespace
@@ -523,37 +619,65 @@ int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const floa
   return gn_nchw<f16>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu);
 }
 
-uint32_t gn_nhwc_chunks(uint32_t HW, uint32_t C) {
-  (void)C;
-  uint32_t ppc = (HW + 63) / 64;  // at most 64 chunks per image
+uint32_t gn_nhwc_chunks(uint32_t N, uint32_t HW) {
+  // ~256 partial-statistics workgroups over the batch, at most 64 per image
+  // (every apply workgroup folds one image's partials).
+  uint32_t c = (256 + N - 1) / N;
+  if (c > 64) c = 64;
+  if (c > HW) c = HW;
+  const uint32_t ppc = (HW + c - 1) / c;
   return (HW + ppc - 1) / ppc;
 }
 
 uint64_t gn_nhwc_ws_floats(uint32_t N, uint32_t C, uint32_t G, uint32_t HW) {
-  return (uint64_t)N * gn_nhwc_chunks(HW, C) * G * 2 + (uint64_t)N * G * 2;
+  (void)C;
+  return (uint64_t)N * gn_nhwc_chunks(N, HW) * G * 2;
 }
 
 void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const float* beta,
                             void* y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW, float eps,
-                            bool silu, float* ws, uint32_t* sync) {
-  uint32_t chunks = gn_nhwc_chunks(HW, C);
-  uint32_t ppc = (HW + chunks - 1) / chunks;
-  float* part = ws;
-  float* stats = ws + (uint64_t)N * chunks * G * 2;
+                            bool silu, float* ws) {
+  const uint32_t sch = gn_nhwc_chunks(N, HW);
+  const uint32_t sppc = (HW + sch - 1) / sch;
   const NhwcMap m = nhwc_map(C);
-  size_t lds = 2 * C * sizeof(float);
-  k_gn_nhwc_stats<<<dim3(chunks, N), 256, lds * m.R, s>>>(x, C, G, HW, ppc, eps, part, stats, sync);
-  k_gn_nhwc_apply<<<dim3(chunks, N), 256, lds, s>>>(x, gamma, beta, (f16*)y, C, G, HW, ppc,
-                                                    silu ? 1 : 0, stats);
+  // apply: ~2 workgroups per CU over the batch, >= 2 pixels per pixel lane
+  uint32_t ach = (512 + N - 1) / N;
+  const uint32_t maxch = (HW + 2 * m.R - 1) / (2 * m.R);
+  if (ach > maxch) ach = maxch;
+  if (ach < 1) ach = 1;
+  const uint32_t appc = (HW + ach - 1) / ach;
+  ach = (HW + appc - 1) / appc;
+  const size_t lds_p = (size_t)2 * C * m.R * sizeof(float);
+  const int si = silu ? 1 : 0;
+  if (m.kv == 1) {
+    k_gn_nhwc_partial<1><<<dim3(sch, N), 256, lds_p, s>>>(x, C, G, HW, sppc, ws);
+    k_gn_nhwc_apply<1><<<dim3(ach, N), 256, 0, s>>>(x, gamma, beta, (f16*)y, C, G, HW, appc, sch,
+                                                     eps, si, ws);
+  } else {
+    k_gn_nhwc_partial<2><<<dim3(sch, N), 256, lds_p, s>>>(x, C, G, HW, sppc, ws);
+    k_gn_nhwc_apply<2><<<dim3(ach, N), 256, 0, s>>>(x, gamma, beta, (f16*)y, C, G, HW, appc, sch,
+                                                     eps, si, ws);
+  }
 }
 
 void launch_layer_norm(hipStream_t s, const void* x, const float* gamma, const float* beta,
                        void* y, uint32_t rows, uint32_t inner, float eps, int dt) {
-  unsigned g = (rows + 3) / 4;
-  if (dt == DI_F32)
+  const unsigned g = (rows + 3) / 4;
+  if (dt == DI_F16 && inner % 8 == 0 && inner <= 64u * 8u * kLnMaxV) {
+    const f16* xp = (const f16*)x;
+    f16* yp = (f16*)y;
+    const uint32_t nv = (inner / 8 + 63) / 64;
+    if (nv == 1)
+      k_layer_norm_f16_reg<1><<<g, 256, 0, s>>>(xp, gamma, beta, yp, rows, inner, eps);
+    else if (nv == 2)
+      k_layer_norm_f16_reg<2><<<g, 256, 0, s>>>(xp, gamma, beta, yp, rows, inner, eps);
+    else
+      k_layer_norm_f16_reg<4><<<g, 256, 0, s>>>(xp, gamma, beta, yp, rows, inner, eps);
+  } else if (dt == DI_F32) {
     k_layer_norm<float><<<g, 256, 0, s>>>((const float*)x, gamma, beta, (float*)y, rows, inner, eps);
-  else
+  } else {
     k_layer_norm<f16><<<g, 256, 0, s>>>((const f16*)x, gamma, beta, (f16*)y, rows, inner, eps);
+  }
 }
 
 }  // namespace di
@@ -589,13 +713,13 @@ int32_t di_group_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
     DI_REQUIRE(dt == DI_F16, DI_EUNSUPPORTED, "di_group_norm: NHWC requires fp16");
     DI_REQUIRE(C % 8 == 0 && C <= 4096 && G <= 256, DI_EUNSUPPORTED,
                "di_group_norm: NHWC needs C %% 8 == 0, C <= 4096, G <= 256 (C=%u G=%u)", C, G);
-    DI_REQUIRE(N <= kGnMaxGroups, DI_EUNSUPPORTED, "di_group_norm: batch too large");
+    DI_REQUIRE(N <= 65535u, DI_EUNSUPPORTED, "di_group_norm: batch too large");
     void* ws = nullptr;
     int rc = workspace(ctx, gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float), &ws);
     if (rc) return rc;
     NhwcSrc src{(const f16*)x->ptr, (const f16*)x->ptr, C, C, C};
     launch_group_norm_nhwc(ctx->stream, src, (const float*)g->ptr, (const float*)b->ptr, y->ptr,
-                           N, C, G, HW, eps, silu, (float*)ws, ctx->sync_words);
+                           N, C, G, HW, eps, silu, (float*)ws);
   }
   DI_LAUNCH_CHECK();
   return DI_OK;

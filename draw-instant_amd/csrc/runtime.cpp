@@ -138,9 +138,6 @@ int32_t di_create(int32_t device, di_ctx** out) {
   c->clock_khz = prop.clockRate;
   c->hbm_bytes = prop.totalGlobalMem;
   DI_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
-  DI_HIP(hipMalloc(&c->sync_words, kSyncWords * sizeof(uint32_t)));
-  DI_HIP(hipMemsetAsync(c->sync_words, 0, kSyncWords * sizeof(uint32_t), c->stream));
-  DI_HIP(hipStreamSynchronize(c->stream));
   if (const char* lim = getenv("DI_ALLOC_LIMIT")) c->limit = strtoull(lim, nullptr, 10);
   *out = c;
   return DI_OK;
@@ -153,7 +150,6 @@ int32_t di_destroy(di_ctx* ctx) {
   for (auto& kv : ctx->free_list)
     for (void* p : kv.second) (void)hipFree(p);
   if (ctx->ws) (void)hipFree(ctx->ws);
-  if (ctx->sync_words) (void)hipFree(ctx->sync_words);
   for (int i = 0; i < kTimerSlots; i++) {
     if (ctx->ev_begin[i]) (void)hipEventDestroy(ctx->ev_begin[i]);
     if (ctx->ev_end[i]) (void)hipEventDestroy(ctx->ev_end[i]);
@@ -167,12 +163,6 @@ int32_t di_sync(di_ctx* ctx) {
   DI_CTX(ctx);
   DI_HIP(hipStreamSynchronize(ctx->stream));
   DI_HIP(hipGetLastError());
-  uint32_t fault = 0;
-  DI_HIP(hipMemcpy(&fault, ctx->sync_words + kFaultWord, sizeof(fault), hipMemcpyDeviceToHost));
-  DI_REQUIRE(fault == 0, DI_EHIP,
-             "a kernel's bounded cross-block wait expired (fault word 0x%x): results of "
-             "the last ops are invalid",
-             fault);
   return DI_OK;
 }
 

@@ -471,7 +471,7 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
     rc = workspace(c, gn_nhwc_ws_floats(B, ch, G, hh * ww) * sizeof(float), &ws);
     if (rc) return rc;
     launch_group_norm_nhwc(c->stream, one(hcur.h(), ch), u.f(u.nog), u.f(u.nob), no.h(), B, ch, G,
-                           hh * ww, cf.resnet_eps, true, (float*)ws, c->sync_words);
+                           hh * ww, cf.resnet_eps, true, (float*)ws);
   }
   ConvCall co;
   co.x = one(no.h(), ch);

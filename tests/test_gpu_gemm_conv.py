@@ -161,6 +161,48 @@ def test_linear_fp16(dev, rng, M, N, K, act, res):
     assert err <= 2e-3
 
 
+@pytest.mark.parametrize("M,N,K,act,res", [
+    (300, 640, 512, "none", True),    # ragged M, residual
+    (256, 1280, 512, "geglu", False),  # GEGLU pairs
+    (200, 104, 192, "gelu", False),   # N % 32 != 0, ragged tiles
+])
+def test_linear_fp16_every_plan(dev, rng, monkeypatch, M, N, K, act, res):
+    """Every tile shape x split-K factor (planner overridden) gives the same
+    result: covers the LDS-staged vector epilogue, split-K partial stores and
+    the vector reducer with bias / residual / activation / GEGLU."""
+    import drawinstant
+    x = _f16(rng.standard_normal((M, K)))
+    w = _f16(rng.standard_normal((N, K)) * math.sqrt(1.0 / K))
+    b = (0.01 * rng.standard_normal(N)).astype(np.float32)
+    nout = N // 2 if act == "geglu" else N
+    r = _f16(rng.standard_normal((M, nout))) if res else None
+    bx, bw, bb = dev.storage(x), dev.storage(w), dev.storage(b)
+    br = dev.storage(r) if res else None
+    y = dev.create_buffer(M * nout * 2)
+    full = oracle.linear(x.astype(np.float32), w.astype(np.float32), b)
+    if act == "geglu":
+        grp = full.reshape(M, N // 32, 2, 16)
+        ref = grp[:, :, 0, :].reshape(M, nout) * oracle.unary("GELU", grp[:, :, 1, :].reshape(M, nout))
+    elif act == "gelu":
+        ref = oracle.unary("GELU", full)
+    else:
+        ref = full
+    if res:
+        ref = ref + r.astype(np.float32)
+    for tile in (0, 1, 2, 3, 5):
+        for splits in (1, 2, 3):
+            monkeypatch.setenv("DI_GEMM_TILE", str(tile))
+            monkeypatch.setenv("DI_GEMM_SPLITS", str(splits))
+            dev.fill_normal(y, M * nout, 3, dtype=F16)  # stale output must be overwritten
+            _call(dev, "di_linear", bx.handle, bw.handle, bb.handle, _h(br), y.handle, M, N, K,
+                  ACT[act], F16)
+            got = dev.download(y, np.float16).astype(np.float32).reshape(M, nout)
+            err = rel_l2(got, ref)
+            print(f"[plan] M={M} N={N} K={K} {act} tile={tile} splits={splits} rel-L2 {err:.2e}",
+                  flush=True)
+            assert err <= 2e-3
+
+
 def _conv_case(dev, rng, n, cin, cout, h, w, k, s, pad, up=1, res=False, cin_pad=None):
     """NHWC fp16 conv vs the oracle's NCHW conv on the same fp16 values."""
     x = _f16(rng.standard_normal((n, h, w, cin)))

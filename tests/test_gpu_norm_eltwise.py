@@ -43,7 +43,8 @@ def _gn_inputs(dev, N, C, HW, seed, dt=F32):
     (2, 64, 8, 8, 32, 1e-6, True),
     (1, 96, 5, 7, 4, 1e-5, True),         # HW % 4 != 0: scalar path
     (1, 128, 128, 128, 32, 1e-5, True),   # many slices per group
-    (1, 32, 768, 768, 32, 1e-5, False),   # too large for registers: two-pass
+    (1, 32, 768, 768, 32, 1e-5, False),   # 256 slices, several rounds per thread
+    (16, 512, 4, 4, 512, 1e-5, False),    # 8192 groups of 16 elements
 ])
 def test_group_norm_nchw_f32(dev, N, C, H, W, G, eps, silu):
     import drawinstant
@@ -56,29 +57,33 @@ def test_group_norm_nchw_f32(dev, N, C, H, W, G, eps, silu):
     got = dev.download(y).reshape(N, C, H, W)
     ref = oracle.group_norm(xh.reshape(N, C, H, W), gh, bh, G, eps=eps, silu=silu)
     assert max_rel(got, ref) <= 1e-4
-    dev.sync()  # raises if a cross-workgroup wait expired
     for t in (x, g, b, y):
         t.destroy()
 
 
 def test_gn_silu_entry_point_and_repeat(dev):
-    """di_gn_silu == group_norm+SiLU; repeated launches stay correct (the
-    cross-workgroup barrier words reset themselves)."""
+    """di_gn_silu == group_norm+SiLU; repeated launches give bit-identical
+    results (partials are folded in a fixed order, no atomics)."""
     import drawinstant
     N, C, HW, G = 1, 320, 4096, 32
     x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, HW, 111)
     y = dev.create_buffer(N * C * HW * 4)
     ref = oracle.group_norm(xh.reshape(N, C, HW), gh, bh, G, eps=1e-5, silu=True)
+    first = None
     for _ in range(20):
         drawinstant.call("di_gn_silu", dev.ctx, x.handle, g.handle, b.handle, y.handle, N, C, G,
                          HW, 1e-5, F32, NCHW)
-    assert max_rel(dev.download(y).reshape(N, C, HW), ref) <= 1e-4
-    dev.sync()
+        got = dev.download(y)
+        if first is None:
+            first = got
+        np.testing.assert_array_equal(got, first)
+    assert max_rel(first.reshape(N, C, HW), ref) <= 1e-4
 
 
-def test_group_norm_nchw_f16(dev):
+@pytest.mark.parametrize("N,C,H,W,G", [(1, 320, 32, 32, 32), (2, 64, 6, 6, 32)])
+def test_group_norm_nchw_f16(dev, N, C, H, W, G):
+    """fp16 NCHW: 8-wide vectors, and the scalar path (HW % 8 != 0)."""
     import drawinstant
-    N, C, H, W, G = 1, 320, 32, 32, 32
     x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, H * W, 121, dt=F16)
     y = dev.create_buffer(N * C * H * W * 2)
     drawinstant.call("di_group_norm", dev.ctx, x.handle, g.handle, b.handle, y.handle, N, G,
@@ -92,6 +97,10 @@ def test_group_norm_nchw_f16(dev):
     (1, 320, 4096, 32, 1e-5), (1, 640, 1024, 32, 1e-6), (1, 960, 4096, 32, 1e-5),
     (1, 1280, 256, 32, 1e-5), (1, 2560, 64, 32, 1e-5), (2, 1920, 256, 32, 1e-6),
     (1, 1280, 64, 32, 1e-6),
+    (1, 2048, 64, 256, 1e-5),   # G > 128: 512 (group, stat) pairs per fold
+    (1, 2600, 64, 26, 1e-5),    # 325 vectors per pixel: second vector partly masked
+    (1, 4096, 16, 32, 1e-5),    # largest C
+    (3, 64, 63, 32, 1e-5),      # 32 pixel lanes, ragged chunks
 ])
 def test_group_norm_nhwc_f16(dev, N, C, HW, G, eps):
     import drawinstant
