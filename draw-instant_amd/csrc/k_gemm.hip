@@ -549,13 +549,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     const uint32_t k = kbase + kc * KV;
     const bool kval = k < k_end;
     if constexpr (AM == A_DENSE) {
-      const bool s2 = kbase >= g.c1;  // uniform: which concat source
-      const uint32_t kb = (s2 ? k - g.c1 : k) * 2u;
+      // single source (gemm_fast_ok): one descriptor, so it stays uniform; a
+      // per-stage choice between two descriptors merged with the per-lane k
+      // bound makes the compiler emit a waterfall loop around every load
 #pragma unroll
-      for (int i = 0; i < NVA; i++) {
-        const uint32_t off = kval ? (s2 ? fa2[i] : fa1[i]) + kb : kInv;
-        st.a[i] = buf_load16<typename MT::vec>(s2 ? rA2 : rA, off);
-      }
+      for (int i = 0; i < NVA; i++) st.a[i] = buf_load16<typename MT::vec>(rA, kval ? fa1[i] + k * 2u : kInv);
     } else {
       const bool s2 = f_ci0 >= g.c1;
       const uint32_t cb = ((s2 ? f_ci0 - g.c1 : f_ci0) + kc * KV) * 2u;
@@ -929,7 +927,7 @@ bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode) {
   if (elem != DI_F16 || b_mode != B_NK || !g.b_vec_ok) return false;
   if (g.a_bytes == 0 || g.a2_bytes == 0 || g.b_bytes == 0) return false;  // extents unknown
   const bool single = g.c1 == 0xffffffffu || g.a2 == g.a;
-  if (a_mode == A_DENSE) return g.a_vec_ok && (single || g.c1 % 64 == 0);
+  if (a_mode == A_DENSE) return g.a_vec_ok && single;
   if (a_mode == A_CONV_NHWC) return g.Cin % 64 == 0 && (single || g.c1 % 64 == 0) && (g.up == 1 || g.up == 2);
   return false;
 }
@@ -969,8 +967,10 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
   }
   const bool fast = gemm_fast_ok(g, elem, a_mode, b_mode);
   if (fast) {
+    // ring depth 2 measured as fast as 4 at U-Net shapes (short K); 4 is kept
+    // for tuning (DI_GEMM_DEPTH=4)
     static const char* env_depth = getenv("DI_GEMM_DEPTH");
-    const int depth = env_depth ? atoi(env_depth) : 4;
+    const int depth = env_depth ? atoi(env_depth) : 2;
     if (a_mode == A_DENSE) launch_fast<A_DENSE>(g, tile_cfg, depth, s);
     else launch_fast<A_CONV_NHWC>(g, tile_cfg, depth, s);
   } else if (elem == DI_F16) {
