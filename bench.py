@@ -7,12 +7,20 @@
 
 Prints ONE JSON line.  `value` = ms per step (lower is better), timed with
 HIP events on the library's stream over exactly K graph-replayed steps
-(bracketed by device synchronisation), inputs resident in HBM.  `roofline`
-covers the dominant kernel, timed live the same way at its U-Net shape;
-`blocks` gives per-config figures (cfg1 GN+SiLU HBM GB/s, cfg2 conv / cfg3
-ResNet / cfg4 transformer / self-attention MFMA %).  `cpu_baseline` is the
-repo's C restatement of the reference kernels (oracle/, OpenMP) running the
-same step on the host cores.
+(bracketed by device synchronisation), inputs resident in HBM.
+
+* `roofline`: the dominant kernel, the implicit-GEMM MFMA conv (k_gemm) at
+  its most frequent U-Net shape, conv3x3 320->320 on 64x64 NHWC fp16 (seven
+  launches per step; also BASELINE cfg2), timed live with HIP events on the
+  stream it is launched on.  achieved = 2*HW*Cout*Cin*9 FLOP per launch /
+  average launch time; `traffic` = HBM bytes per launch from the committed
+  rocprofv3 FETCH_SIZE / WRITE_SIZE summary (null without it).
+* `cpu_baseline`: the repo's C restatement of the reference kernels (oracle/,
+  OpenMP, fp64 accumulation) running a bounded sample of the same step
+  (down_blocks.0-1 of the same U-Net, same weights) on the host cores,
+  scaled by FLOPs to ms per step.  Skipped with --no-cpu.
+* `blocks` (unless --no-blocks): per-config figures (cfg1 GN+SiLU HBM GB/s,
+  cfg2 conv / cfg3 ResNet / cfg4 transformer / self-attention MFMA %).
 """
 import argparse
 import json
@@ -159,6 +167,83 @@ def bench_block_chains(dev, u):
     return res
 
 
+ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_gemm_conv3x3_64x64x320_pmc.md")
+
+
+def roofline_conv(dev, iters=50):
+    """Live roofline of the dominant kernel at its U-Net shape."""
+    from drawinstant import perf
+    from drawinstant.device import call
+    rng = np.random.default_rng(3)
+    x = dev.storage(rng.standard_normal((1, 64, 64, 320)).astype(np.float16))
+    w = dev.storage((rng.standard_normal((320, 3, 3, 320)) * 0.026).astype(np.float16))
+    bias = dev.storage((0.01 * rng.standard_normal(320)).astype(np.float32))
+    y = dev.create_buffer(64 * 64 * 320 * 2)
+    conv = lambda i: call("di_conv2d", dev.ctx, x.handle, w.handle, bias.handle, 0, y.handle, 1,
+                          320, 320, 64, 64, 3, 1, 1, 0, 1, 1)
+    for i in range(3):
+        conv(i)
+    ms = timed(dev, conv, iters)
+    fl = perf.conv_flops(1, 320, 320, 64, 64, 3)
+    achieved = fl / (ms * 1e-3) / 1e12
+    peak = perf.PEAK_FP16_FLOPS / 1e12
+    traffic = None
+    if os.path.exists(ROOFLINE_PMC):
+        for line in open(ROOFLINE_PMC):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(float(line.split(":", 1)[1]))
+    for b in (x, w, bias, y):
+        b.destroy()
+    return {"kernel": "k_gemm implicit-GEMM conv3x3 320->320 @64x64 NHWC fp16 (fp32 acc)",
+            "bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic,
+            "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3)}
+
+
+def cpu_baseline(u, budget_blocks=None):
+    """Oracle (C, OpenMP) on down_blocks.0-1 of the same U-Net, scaled to a step."""
+    import oracle
+    from oracle import unet_ref
+    from drawinstant import perf
+    sd = {k: v for k, v in u.state_dict(np.float32).items() if k.startswith("down_blocks.0.")
+          or k.startswith("down_blocks.1.")}
+    ops = unet_ref.OracleOps()
+    rng = np.random.default_rng(4)
+    h = rng.standard_normal((1, 320, 64, 64)).astype(np.float32)
+    ts = rng.standard_normal((1, 1280)).astype(np.float32)
+    ctx = rng.standard_normal((1, 77, 1024)).astype(np.float32)
+    w = perf.Work()
+    t0 = time.perf_counter()
+    for i, (cin, c, hw) in enumerate(((320, 320, 64), (320, 640, 32))):
+        for j in range(2):
+            h = unet_ref.resnet(ops, sd, f"down_blocks.{i}.resnets.{j}", h, ts)
+            perf.resnet_flops(w, 1, cin if j == 0 else c, c, hw, hw)
+            h = unet_ref.transformer(ops, sd, f"down_blocks.{i}.attentions.{j}", h, ctx)
+            perf.transformer_flops(w, 1, c, hw, hw)
+        if i == 0:
+            h = ops.conv(h, sd["down_blocks.0.downsamplers.0.conv.weight"],
+                         sd["down_blocks.0.downsamplers.0.conv.bias"], stride=2, pad=1)
+            w.add("sample_conv", perf.conv_flops(1, 320, 320, 32, 32, 3))
+    sec = time.perf_counter() - t0
+    step = perf.unet_work().total
+    return {"value": round(sec * 1e3 * step / w.total, 1), "unit": "ms",
+            "cores": int(oracle.lib().or_threads()), "kind": "port",
+            "sample": f"oracle/ C restatement (fp64 accumulation) of down_blocks.0-1 of the same "
+                      f"SD2.1 U-Net (4 ResNet + 4 transformer blocks + downsampler, "
+                      f"{w.total / 1e9:.1f} GFLOP) in {sec:.1f} s, scaled by FLOPs to the "
+                      f"{step / 1e9:.1f} GFLOP step"}
+
+
+def pcie_inclusive(u, inputs, iters=5):
+    """Host-buffer boundary: upload latent+context, eager step, download (ms)."""
+    x, ctx = inputs
+    u(x, 999.0, ctx)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        u(x, 999.0, ctx)
+    return (time.perf_counter() - t0) * 1e3 / iters
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +251,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-blocks", action="store_true", help="skip the per-block figures")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the roofline kernel and a 256 MiB copy (for rocprofv3 --pmc runs "
+                         "that calibrate FETCH_SIZE / WRITE_SIZE against a known byte count)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -174,6 +262,18 @@ def main():
     import drawinstant
     from drawinstant import perf
     dev = drawinstant.Device(0)
+    if args.roofline_only:
+        rl = roofline_conv(dev, iters=20)
+        # calibration: a streaming kernel of known traffic (di_unary NEG over
+        # 64 Mi floats reads 256 MiB and writes 256 MiB)
+        from drawinstant.device import call
+        n = 64 << 20
+        a, b = dev.create_buffer(n * 4), dev.create_buffer(n * 4)
+        call("di_unary", dev.ctx, 2, a.handle, b.handle, n, 0)
+        dev.sync()
+        print(json.dumps({"roofline": rl, "calibration_read_bytes": n * 4,
+                          "calibration_write_bytes": n * 4}), flush=True)
+        return
     u, ms, wall, eager, finite, inputs = bench_unet(dev, args)
     work = perf.unet_work()
     line = {
@@ -190,7 +290,11 @@ def main():
         "step_tflops": round(work.total / (ms * 1e-3) / 1e12, 1),
         "step_mfma_frac": round(work.total / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, 4),
         "output_finite": finite,
+        "pcie_inclusive_eager_ms_per_step": round(pcie_inclusive(u, inputs), 3),
+        "roofline": roofline_conv(dev),
     }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(u)
     if not args.no_blocks:
         blk = bench_blocks(dev)
         blk.update(bench_block_chains(dev, u))
