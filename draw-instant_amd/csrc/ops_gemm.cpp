@@ -163,7 +163,7 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_han
   DI_CTX(ctx);
   DI_DTYPE(dt);
   DI_REQUIRE(N && Cin && Cout && H && W && K && S, DI_EINVAL, "di_conv2d: zero dimension");
-  DI_REQUIRE((flags & ~(DI_CONV_F16_COMPUTE | DI_CONV_UPSAMPLE2X)) == 0, DI_EINVAL,
+  DI_REQUIRE((flags & ~(DI_CONV_F16_COMPUTE | DI_CONV_UPSAMPLE2X | DI_CONV_SILU)) == 0, DI_EINVAL,
              "di_conv2d: unknown flags 0x%x", flags);
   const uint32_t up = (flags & DI_CONV_UPSAMPLE2X) ? 2 : 1;
   const uint32_t Hi = H * up, Wi = W * up;
@@ -197,6 +197,7 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_han
   g.bias = b;
   g.res = res;
   g.res_f32 = dt == DI_F32;
+  if (flags & DI_CONV_SILU) g.act = ACT_SILU;  // silu(conv + bias) [+ R]
 
   if (layout == DI_NHWC) {
     DI_REQUIRE(dt == DI_F16, DI_EUNSUPPORTED, "di_conv2d: NHWC path is fp16 (OHWI weights)");

@@ -1,0 +1,1290 @@
+"""Graph executor: the op-dispatch API of draw-instant's wgsl-executor.js,
+driving libdrawinstant_hip.so.
+
+Mirrors, name for name (snake_case), the reference's executor contract:
+
+* ``Tensor`` (wgsl-executor.js:45-55): device buffer + dims + dtype; CPU-side
+  metadata tensors (shape vectors, int64 timesteps, scalar constants) are
+  ``CpuTensor`` objects with ``cpu_data`` and no buffer, as the reference's
+  ``{isShape, cpuData, dims, dtype}`` objects.
+* ``BufferPool`` (:62-94): acquire/release by 4 KiB-rounded size with
+  live / peak / allocs statistics, over ``di_alloc`` / ``di_free``.
+* ``OPS`` (:96-1114): ``OPS[op_type](ctx, node, inputs) -> tensor`` for the
+  37 op types of the reference, each GPU op one C-ABI call (shapes as scalars
+  instead of uniform buffers).  Activations are fp32 NCHW, as in the reference.
+* graph rewrites ``fuse_silu_pattern`` (:799-839), ``fuse_mul_add_pattern``
+  (:845-898), ``fuse_group_norm_pattern`` (:905-1008).
+* ``plan_execution`` (:1157-1170), ``create_dispatchers`` (:1174-1197),
+  ``infer_graph_io`` (:1205-1221), ``Executor.run`` (:1223-1466) with the
+  same input-seeding, CPU promotion, consumer counting, output snapshot and
+  error convention (``op @<i> <op> (<name>) failed: <msg>``).
+
+Differences by design: the in-order HIP stream replaces the command encoder
+(``run`` synchronises once at the end, as the reference's single submit);
+``Conv`` accepts batch N >= 1 (the reference's kernel computes batch 0 only,
+so it rejects N != 1); buffers created by CPU-to-device promotion and the
+graph outputs' pool buffers are returned to the pool at the end of ``run``
+(the reference never releases them, so its pool grows by a few buffers per
+run).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import time
+import weakref
+from dataclasses import dataclass, field
+from typing import Any, Callable, Dict, List, Optional
+
+import numpy as np
+
+from .device import F32, NCHW, Buffer, Device, call
+
+# ---------------------------------------------------------------- logging --
+LOG = {"verbose": False, "node_count": 0, "op_hist": {}, "t0": 0.0, "profile": False,
+       "profile_data": None, "traffic": False, "traffic_data": None}
+
+
+def set_verbose(v: bool) -> None:
+    LOG["verbose"] = bool(v)
+
+
+def _dlog(*a) -> None:
+    if LOG["verbose"]:
+        print("[hip-exec]", *a, flush=True)
+
+
+# ------------------------------------------------------------ graph types --
+@dataclass
+class TensorProto:
+    """An initializer / Constant payload: dims, ONNX dtype name, raw data."""
+    dims: List[int]
+    dtype: str = "float32"
+    data: Any = None  # bytes-like or numpy array
+
+    def array(self) -> np.ndarray:
+        dt = {"float32": np.float32, "float16": np.float16, "int64": np.int64,
+              "int32": np.int32, "bool": np.uint8}[self.dtype]
+        if isinstance(self.data, np.ndarray):
+            return np.ascontiguousarray(self.data, dt).reshape(-1)
+        return np.frombuffer(bytes(self.data or b""), dt).copy()
+
+
+@dataclass
+class Attr:
+    name: str
+    i: Optional[int] = None
+    f: Optional[float] = None
+    ints: Optional[List[int]] = None
+    floats: Optional[List[float]] = None
+    s: Optional[Any] = None
+    t: Optional[TensorProto] = None
+
+
+@dataclass
+class Node:
+    op_type: str
+    name: str = ""
+    inputs: List[str] = field(default_factory=list)
+    outputs: List[str] = field(default_factory=list)
+    attributes: List[Attr] = field(default_factory=list)
+
+
+@dataclass
+class Graph:
+    nodes: List[Node]
+    inputs: List[dict] = field(default_factory=list)   # [{"name": ...}]
+    outputs: List[dict] = field(default_factory=list)
+    tensors: Dict[str, TensorProto] = field(default_factory=dict)  # initializers
+
+
+# ----------------------------------------------------------------- tensors --
+class Tensor:
+    """Device tensor (wgsl-executor.js:45-55): fp32, byte_length = numel * 4."""
+
+    def __init__(self, buf: Optional[Buffer], dims, dtype: str = "float32", consumers: int = 0,
+                 cpu_data: Optional[np.ndarray] = None):
+        self.buf = buf
+        self.dims = [int(d) for d in dims]
+        self.dtype = dtype
+        self.consumers = consumers
+        self.cpu_data = cpu_data  # CPU mirror for scalar fast paths (Pow exponent, scales)
+        self.numel = int(np.prod(self.dims)) if self.dims else 1
+        self.byte_length = self.numel * 4
+        self.is_shape = False
+
+    def __repr__(self):
+        return f"Tensor(GPU{self.dims})"
+
+
+class CpuTensor:
+    """CPU-only metadata tensor: ``{isShape, cpuData, dims, dtype}``."""
+    buf = None
+
+    def __init__(self, cpu_data, dims, dtype: str, is_shape: bool = True):
+        self.cpu_data = np.asarray(cpu_data)
+        self.dims = [int(d) for d in dims]
+        self.dtype = dtype
+        self.is_shape = is_shape
+
+    @property
+    def numel(self) -> int:
+        return int(self.cpu_data.size)
+
+    def __repr__(self):
+        return f"CpuTensor({self.dims}:{self.dtype})"
+
+
+def _is_cpu(t) -> bool:
+    return t is not None and getattr(t, "buf", None) is None and getattr(t, "cpu_data", None) is not None
+
+
+def _dtype_of(a: np.ndarray) -> str:
+    if a.dtype == np.int64:
+        return "int64"
+    if a.dtype == np.int32:
+        return "int32"
+    if a.dtype == np.uint8 or a.dtype == np.bool_:
+        return "bool"
+    return "float32"
+
+
+# ------------------------------------------------------------ buffer pool --
+class BufferPool:
+    """Allocate once, reuse (wgsl-executor.js:62-94): free lists keyed by the
+    byte size rounded up to 4 KiB."""
+
+    def __init__(self, device: Device):
+        self.device = device
+        self.free: Dict[int, List[Buffer]] = {}
+        self.owned = weakref.WeakSet()  # pool-allocated buffers (ours to recycle)
+        self.live = 0
+        self.peak = 0
+        self.allocs = 0
+
+    @staticmethod
+    def key(nbytes: int) -> int:
+        return int(math.ceil(nbytes / 4096)) * 4096
+
+    def acquire(self, nbytes: int) -> Buffer:
+        k = self.key(nbytes)
+        lst = self.free.get(k)
+        self.live += 1
+        self.peak = max(self.peak, self.live)
+        if lst:
+            return lst.pop()
+        self.allocs += 1
+        buf = self.device.create_buffer(k)
+        self.owned.add(buf)
+        return buf
+
+    def release(self, buf: Buffer, _nbytes: int = 0) -> None:
+        """Release by the buffer's bucket capacity (an aliased reshape's
+        logical size differs from it)."""
+        if buf not in self.owned:
+            return
+        self.free.setdefault(buf.size, []).append(buf)
+        self.live -= 1
+
+    def owns(self, buf: Buffer) -> bool:
+        return buf in self.owned
+
+    def destroy(self) -> None:
+        for lst in self.free.values():
+            for b in lst:
+                b.destroy()
+        self.free.clear()
+
+
+# ------------------------------------------------------------ weight cache --
+class WeightCache:
+    """Initializers uploaded once on first use (wgsl-unet.js:55-104): floats
+    (fp16 widened to fp32) on the device, int64/int32/bool kept on the CPU as
+    shape tensors; scalar floats also expose ``cpu_data``."""
+
+    def __init__(self, device: Device, tensors: Dict[str, TensorProto]):
+        self.device = device
+        self.tensors = tensors
+        self.gpu: Dict[str, Any] = {}
+
+    def get(self, name: str):
+        if name in self.gpu:
+            return self.gpu[name]
+        t = self.tensors.get(name)
+        if t is None:
+            raise KeyError(f"weight not found: {name}")
+        a = t.array()
+        if t.dtype in ("int64", "int32", "bool"):
+            entry = CpuTensor(a, t.dims, t.dtype, is_shape=t.dtype != "bool")
+        else:
+            f = a.astype(np.float32)
+            entry = Tensor(self.device.storage(f if f.size else np.zeros(1, np.float32)), t.dims,
+                           cpu_data=f if f.size == 1 else None)
+        self.gpu[name] = entry
+        return entry
+
+    def has(self, name: str) -> bool:
+        return name in self.tensors
+
+    def names(self, prefix: str = "") -> List[str]:
+        return [k for k in self.tensors if k.startswith(prefix)]
+
+    def destroy(self) -> None:
+        for v in self.gpu.values():
+            if isinstance(v, Tensor) and v.buf is not None:
+                v.buf.destroy()
+        self.gpu.clear()
+
+
+# ------------------------------------------------------------- dispatchers --
+UNARY_CODE = {"Sigmoid": 0, "Sqrt": 1, "Neg": 2, "Abs": 3, "Sin": 4, "Cos": 5, "Exp": 6, "Log": 7,
+              "SiLU": 8, "GELU": 9, "Erf": 10}
+BINARY_CODE = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Pow": 4, "Max": 5, "Min": 6}
+
+
+def _u32x4(vals) -> ctypes.Array:
+    v = list(vals) + [0] * (4 - len(vals))
+    return (ctypes.c_uint32 * 4)(*[int(x) for x in v])
+
+
+class Dispatchers:
+    """Kernel closures built once per device (createDispatchers,
+    wgsl-executor.js:1174-1197); each is one C-ABI call on the device stream."""
+
+    def __init__(self, device: Device):
+        ctx = device.ctx
+        self.device = device
+        self.unary: Dict[str, Callable] = {}
+        self.binary: Dict[str, Callable] = {}
+        self.binary_bcast: Dict[str, Callable] = {}
+        for op, code in UNARY_CODE.items():
+            self.unary[op] = (lambda c: lambda x, y, n: call("di_unary", ctx, c, x.handle, y.handle,
+                                                                  n, F32))(code)
+        for op in ("Add", "Sub", "Mul", "Div", "Max", "Min"):
+            code = BINARY_CODE[op]
+            self.binary[op] = (lambda c: lambda a, b, y, n: call(
+                "di_binary", ctx, c, a.handle, b.handle, y.handle, n, F32))(code)
+            self.binary_bcast[op] = (lambda c: lambda a, b, y, rank, dims, sa, sb, n: call(
+                "di_binary_bcast", ctx, c, a.handle, b.handle, y.handle, rank, _u32x4(dims),
+                _u32x4(sa), _u32x4(sb), n, F32))(code)
+        self.softmax = lambda x, y, inner, rows: call("di_softmax", ctx, x.handle, y.handle, inner,
+                                                      rows, F32)
+        self.instance_norm = lambda x, g, b, y, n, c, hw, eps: call(
+            "di_instance_norm", ctx, x.handle, g.handle, b.handle, y.handle, n, c, hw, eps, F32)
+        self.group_norm = lambda x, g, b, y, n, G, cpg, hw, eps, flags=0: call(
+            "di_group_norm", ctx, x.handle, g.handle, b.handle, y.handle, n, G, cpg, hw, eps, flags,
+            F32, NCHW)
+        self.layer_norm = lambda x, g, b, y, rows, inner, eps: call(
+            "di_layer_norm", ctx, x.handle, g.handle, b.handle, y.handle, rows, inner, eps, F32)
+        self.matmul = lambda a, b, y, M, N, K, batch, bb: call(
+            "di_matmul", ctx, a.handle, b.handle, y.handle, M, N, K, batch, bb, F32)
+        self.gemm = lambda a, b, c, y, M, N, K, tb: call(
+            "di_gemm", ctx, a.handle, b.handle, c.handle if c is not None else 0, y.handle, M, N,
+            K, tb, F32)
+        self.conv_mm = lambda x, w, bias, y, n, cin, cout, h, wd, k, s, pad, flags=0: call(
+            "di_conv2d", ctx, x.handle, w.handle, bias.handle if bias is not None else 0, 0,
+            y.handle, n, cin, cout, h, wd, k, s, pad, flags, F32, NCHW)
+        self.resize_nearest = lambda x, y, planes, hi, wi, ho, wo: call(
+            "di_resize_nearest", ctx, x.handle, y.handle, planes, hi, wi, ho, wo, F32)
+        self.reduce_mean = lambda x, y, inner, rows: call("di_reduce_mean", ctx, x.handle, y.handle,
+                                                          inner, rows, F32)
+        self.concat_copy = lambda x, y, si, so, off, n: call(
+            "di_concat_copy", ctx, x.handle, y.handle, si, so, off, n, F32)
+        self.transpose = lambda x, y, rank, dims, strides, perm, n: call(
+            "di_transpose", ctx, x.handle, y.handle, rank, _u32x4(dims), _u32x4(strides),
+            _u32x4(perm), n, F32)
+        self.pow_scalar = lambda x, y, n, e: call("di_pow_scalar", ctx, x.handle, y.handle, n, e,
+                                                  F32)
+        self.slice = lambda x, y, rank, dims, strides, start, n: call(
+            "di_slice", ctx, x.handle, y.handle, rank, _u32x4(dims), _u32x4(strides),
+            _u32x4(start), n, F32)
+        self.affine_bcast = lambda x, g, b, y, rank, dims, sx, sg, n: call(
+            "di_affine_bcast", ctx, x.handle, g.handle, b.handle, y.handle, rank, _u32x4(dims),
+            _u32x4(sx), _u32x4(sg), n, F32)
+
+
+def create_dispatchers(device: Device) -> Dispatchers:
+    return Dispatchers(device)
+
+
+# ----------------------------------------------------------------- helpers --
+def _attr(node: Node, name: str) -> Optional[Attr]:
+    for a in node.attributes:
+        if a.name == name:
+            return a
+    return None
+
+
+def get_attr_int(node: Node, name: str, dflt):
+    a = _attr(node, name)
+    return a.i if a is not None and a.i is not None else dflt
+
+
+def get_attr_ints(node: Node, name: str, dflt):
+    a = _attr(node, name)
+    return list(a.ints) if a is not None and a.ints is not None else dflt
+
+
+def get_attr_float(node: Node, name: str, dflt):
+    a = _attr(node, name)
+    return float(a.f) if a is not None and a.f is not None else dflt
+
+
+def get_attr_string(node: Node, name: str, dflt):
+    a = _attr(node, name)
+    if a is None or not a.s:
+        return dflt
+    return a.s if isinstance(a.s, str) else bytes(a.s).decode()
+
+
+def row_major_strides(dims: List[int]) -> List[int]:
+    s = [1] * len(dims)
+    for i in range(len(dims) - 2, -1, -1):
+        s[i] = s[i + 1] * dims[i + 1]
+    return s
+
+
+def broadcast_shape(a: List[int], b: List[int]) -> List[int]:
+    n = max(len(a), len(b))
+    out = [0] * n
+    for i in range(n):
+        aa = a[len(a) - 1 - i] if i < len(a) else 1
+        bb = b[len(b) - 1 - i] if i < len(b) else 1
+        if aa == bb or bb == 1:
+            out[n - 1 - i] = aa
+        elif aa == 1:
+            out[n - 1 - i] = bb
+        else:
+            raise ValueError(f"cannot broadcast {a} vs {b}")
+    return out
+
+
+def _bcast_strides(t_dims: List[int], dims: List[int]) -> List[int]:
+    """Right-aligned element strides of an operand, 0 on broadcast dims
+    (wgsl-executor.js:646-657)."""
+    strides = [0] * len(dims)
+    st = 1
+    pad = len(dims) - len(t_dims)
+    for i in range(len(t_dims) - 1, -1, -1):
+        od, td = dims[pad + i], t_dims[i]
+        strides[pad + i] = 0 if (td == 1 and od != 1) else st
+        st *= td
+    return strides
+
+
+def _passthrough_with_dims(x, new_dims):
+    """Relabel dims; CPU tensors stay CPU when their data covers the new shape."""
+    if _is_cpu(x):
+        n = int(np.prod(new_dims)) if new_dims else 1
+        if x.cpu_data.size == n or (not new_dims and x.cpu_data.size == 1):
+            dtype = x.dtype or _dtype_of(x.cpu_data)
+            is_shape = x.is_shape if x.is_shape is not None else dtype in ("int64", "int32")
+            return CpuTensor(x.cpu_data, new_dims, dtype, is_shape)
+    return Tensor(x.buf, new_dims)
+
+
+def _trunc_div(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """BigInt division semantics: truncate toward zero."""
+    q = np.abs(a) // np.abs(b)
+    return np.where((a < 0) ^ (b < 0), -q, q)
+
+
+def _erf_as(v: np.ndarray) -> np.ndarray:
+    """Abramowitz-Stegun 7.1.26, the device erf (wgsl-executor.js:687-691)."""
+    t = 1.0 / (1.0 + 0.3275911 * np.abs(v))
+    y = 1.0 - (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t - 0.284496736) * t
+               + 0.254829592) * t * np.exp(-v * v)
+    return np.where(v >= 0, y, -y)
+
+
+UNARY_CPU = {
+    "Sigmoid": lambda v: 1.0 / (1.0 + np.exp(-v)),
+    "Sqrt": lambda v: np.sqrt(np.maximum(v, 0.0)),
+    "Abs": np.abs,
+    "Neg": lambda v: -v,
+    "Erf": _erf_as,
+}
+
+# -------------------------------------------------------------------- OPS --
+OPS: Dict[str, Callable] = {}
+
+
+def _op(name):
+    def deco(fn):
+        OPS[name] = fn
+        return fn
+    return deco
+
+
+@_op("Identity")
+def _identity(ctx, node, inputs):
+    x = inputs[0]
+    return _passthrough_with_dims(x, list(x.dims))
+
+
+@_op("Reshape")
+def _reshape(ctx, node, inputs):
+    x, shape = inputs[0], inputs[1] if len(inputs) > 1 else None
+    raw = [int(v) for v in shape.cpu_data.reshape(-1)] if shape is not None and _is_cpu(shape) \
+        else list(x.dims)
+    new = list(raw)
+    xn = int(np.prod(x.dims)) if x.dims else 1
+    for i in range(len(new)):
+        if new[i] == 0:
+            new[i] = x.dims[i]  # allowzero = 0: copy from the input
+    known = int(np.prod([d for d in new if d > 0])) if any(d > 0 for d in new) else 1
+    for i in range(len(new)):
+        if new[i] == -1:
+            new[i] = xn // known
+    return _passthrough_with_dims(x, new)
+
+
+@_op("Shape")
+def _shape(ctx, node, inputs):
+    x = inputs[0]
+    return CpuTensor(np.array(x.dims, np.int64), [len(x.dims)], "int64", True)
+
+
+@_op("Unsqueeze")
+def _unsqueeze(ctx, node, inputs):
+    x = inputs[0]
+    axes = inputs[1] if len(inputs) > 1 else None
+    ax = [int(v) for v in axes.cpu_data.reshape(-1)] if axes is not None and _is_cpu(axes) \
+        else get_attr_ints(node, "axes", [0])
+    dims = list(x.dims) if x.dims is not None else [x.cpu_data.size]
+    for a in ax:
+        dims.insert(len(dims) + 1 + a if a < 0 else a, 1)
+    if _is_cpu(x):
+        return CpuTensor(x.cpu_data, dims, x.dtype or "int64", x.is_shape is not False)
+    return Tensor(x.buf, dims)
+
+
+@_op("Squeeze")
+def _squeeze(ctx, node, inputs):
+    x = inputs[0]
+    axes = inputs[1] if len(inputs) > 1 else None
+    ax = [int(v) for v in axes.cpu_data.reshape(-1)] if axes is not None and _is_cpu(axes) \
+        else get_attr_ints(node, "axes", None)
+    dims = list(x.dims)
+    if ax:
+        rm = {a + len(dims) if a < 0 else a for a in ax}
+    else:
+        rm = {i for i, d in enumerate(dims) if d == 1}
+    return _passthrough_with_dims(x, [d for i, d in enumerate(dims) if i not in rm])
+
+
+@_op("Constant")
+def _constant(ctx, node, inputs):
+    a_t, a_ints, a_int = _attr(node, "value"), _attr(node, "value_ints"), _attr(node, "value_int")
+    a_floats, a_float = _attr(node, "value_floats"), _attr(node, "value_float")
+    if a_t is not None and a_t.t is not None:
+        t = a_t.t
+        arr = t.array()
+        if t.dtype in ("int64", "int32"):
+            return CpuTensor(arr, t.dims, t.dtype, True)
+        if t.dtype in ("float32", "float16"):
+            f = arr.astype(np.float32)
+            buf = ctx.pool.acquire(max(f.nbytes, 4))
+            ctx.device.upload(buf, f)
+            return Tensor(buf, list(t.dims), cpu_data=f)
+        return CpuTensor(arr, t.dims, t.dtype, True)
+    if a_ints is not None and a_ints.ints is not None:
+        return CpuTensor(np.array(a_ints.ints, np.int64), [len(a_ints.ints)], "int64", True)
+    if a_int is not None and a_int.i is not None:
+        return CpuTensor(np.array([a_int.i], np.int64), [], "int64", True)
+
+    def upload(vals, dims):
+        f = np.asarray(vals, np.float32).reshape(-1)
+        buf = ctx.pool.acquire(max(f.nbytes, 4))
+        ctx.device.upload(buf, f)
+        return Tensor(buf, dims, cpu_data=f)
+    if a_floats is not None and a_floats.floats is not None:
+        return upload(a_floats.floats, [len(a_floats.floats)])
+    if a_float is not None and a_float.f is not None:
+        return upload([a_float.f], [])
+    raise ValueError(f"Constant {node.name}: no recognised value attribute")
+
+
+@_op("ConstantOfShape")
+def _constant_of_shape(ctx, node, inputs):
+    dims = [int(v) for v in inputs[0].cpu_data.reshape(-1)]
+    numel = int(np.prod(dims)) if dims else 1
+    v = _attr(node, "value")
+    fill, vdt = 0.0, None
+    if v is not None and v.t is not None and v.t.data is not None and len(v.t.array()):
+        vdt = v.t.dtype
+        fill = v.t.array()[0]
+    if vdt in ("int64", "int32"):
+        dt = np.int64 if vdt == "int64" else np.int32
+        return CpuTensor(np.full(max(numel, 0), fill, dt), dims, vdt, True)
+    buf = ctx.pool.acquire(max(numel * 4, 4))
+    ctx.device.upload(buf, np.full(max(numel, 1), float(fill), np.float32))
+    return Tensor(buf, dims)
+
+
+@_op("Cast")
+def _cast(ctx, node, inputs):
+    x = inputs[0]
+    to = get_attr_int(node, "to", 1)
+    if _is_cpu(x):
+        d = x.cpu_data
+        if to == 7 and d.dtype != np.int64:
+            return CpuTensor(np.trunc(d.astype(np.float64)).astype(np.int64), x.dims, "int64",
+                             x.is_shape is not False)
+        if to == 6 and d.dtype != np.int32:
+            return CpuTensor(np.trunc(d.astype(np.float64)).astype(np.int32), x.dims, "int32",
+                             x.is_shape is not False)
+        if to == 1 and d.dtype != np.float32:
+            return CpuTensor(d.astype(np.float32), x.dims, "float32", False)
+        return CpuTensor(d, x.dims, x.dtype, x.is_shape is not False)
+    return Tensor(x.buf, list(x.dims))  # fp16 <-> fp32 on device: stored fp32 either way
+
+
+@_op("Slice")
+def _slice(ctx, node, inputs):
+    x = inputs[0]
+    get = lambda i: inputs[i] if len(inputs) > i and inputs[i] is not None else None
+    starts_t, ends_t, axes_t, steps_t = get(1), get(2), get(3), get(4)
+    vals = lambda t: [int(v) for v in t.cpu_data.reshape(-1)] if t is not None and \
+        getattr(t, "cpu_data", None) is not None else None
+    if _is_cpu(x):
+        data = x.cpu_data.reshape(-1)
+        n = data.size
+        s = (vals(starts_t) or [0])[0]
+        e = (vals(ends_t) or [n])[0]
+        st = (vals(steps_t) or [1])[0] or 1
+        if s < 0:
+            s += n
+        if e < 0:
+            e += n
+        s, e = max(0, min(n, s)), max(0, min(n, e))
+        out = np.array([data[i] for i in range(s, e, st)] if st > 0 else
+                       [data[i] for i in range(s, e, st)], data.dtype)
+        return CpuTensor(out, [out.size], x.dtype or "int64", x.is_shape is not False)
+    rank = len(x.dims)
+    if rank > 4:
+        raise ValueError(f"Slice: rank {rank} > 4 not supported")
+    s_arr, e_arr = vals(starts_t) or [], vals(ends_t) or []
+    a_arr = vals(axes_t) or list(range(len(s_arr)))
+    step_arr = vals(steps_t) or [1] * len(s_arr)
+    if any(v != 1 for v in step_arr):
+        raise ValueError("Slice: step != 1 not supported")
+    out_dim, start = list(x.dims), [0] * rank
+    for i, ax in enumerate(a_arr):
+        ax = ax + rank if ax < 0 else ax
+        ss, ee = s_arr[i], e_arr[i]
+        if ss < 0:
+            ss += x.dims[ax]
+        if ee < 0:
+            ee += x.dims[ax]
+        ss = max(0, min(x.dims[ax], ss))
+        ee = max(0, min(x.dims[ax], ee))
+        start[ax] = ss
+        out_dim[ax] = max(0, ee - ss)
+    numel = int(np.prod(out_dim))
+    out = ctx.pool.acquire(max(numel * 4, 4))
+    if numel:
+        ctx.dispatchers.slice(x.buf, out, rank, out_dim, row_major_strides(x.dims), start, numel)
+    return Tensor(out, out_dim)
+
+
+@_op("Gather")
+def _gather(ctx, node, inputs):
+    data, indices = inputs[0], inputs[1]
+    if getattr(data, "is_shape", False) and _is_cpu(data):
+        d = data.cpu_data.reshape(-1)
+        n = d.size
+        idx = [int(i) + n if int(i) < 0 else int(i) for i in
+               (indices.cpu_data.reshape(-1) if indices is not None else [0])]
+        out = np.array([d[i] if 0 <= i < n else 0 for i in idx], np.int64)
+        return CpuTensor(out, list(indices.dims) if indices is not None else [], "int64", True)
+    raise ValueError(f"Gather {node.name}: GPU-tensor path not implemented")
+
+
+@_op("Transpose")
+def _transpose(ctx, node, inputs):
+    x = inputs[0]
+    dims = list(x.dims or [])
+    perm = get_attr_ints(node, "perm", list(range(len(dims) - 1, -1, -1)))
+    new = [dims[i] for i in perm]
+    if _is_cpu(x):
+        return _passthrough_with_dims(x, new)
+    if len(dims) > 4:
+        raise ValueError(f"Transpose: rank {len(dims)} > 4 not supported")
+    rank = len(dims)
+    numel = int(np.prod(new))
+    out = ctx.pool.acquire(max(numel * 4, 4))
+    ctx.dispatchers.transpose(x.buf, out, rank, new + [1] * (4 - rank),
+                              row_major_strides(dims) + [0] * (4 - rank), perm + [0] * (4 - rank),
+                              numel)
+    return Tensor(out, new)
+
+
+@_op("Concat")
+def _concat(ctx, node, inputs):
+    axis = get_attr_int(node, "axis", 0)
+    ref = next((t for t in inputs if t is not None and (t.dims is not None)), None)
+    rank = len(ref.dims) if ref is not None else 1
+    if axis < 0:
+        axis += rank
+    all_cpu = all(_is_cpu(t) for t in inputs)
+    if not all_cpu and any(_is_cpu(t) for t in inputs):
+        inputs = [ctx.promote(t) if _is_cpu(t) else t for t in inputs]
+    if all_cpu:
+        first = inputs[0]
+        big = any(t.cpu_data.dtype == np.int64 for t in inputs)
+        out = np.concatenate([t.cpu_data.reshape(-1) for t in inputs]).astype(
+            np.int64 if big else np.float32)
+        return CpuTensor(out, [out.size], first.dtype or "int64", first.is_shape is not False)
+    dims = list(inputs[0].dims)
+    dims[axis] = sum(t.dims[axis] for t in inputs)
+    numel = int(np.prod(dims))
+    out = ctx.pool.acquire(max(numel * 4, 4))
+    stripe_out = int(np.prod(dims[axis:]))
+    off = 0
+    for t in inputs:
+        stripe_in = int(np.prod(t.dims[axis:]))
+        if t.numel:
+            ctx.dispatchers.concat_copy(t.buf, out, stripe_in, stripe_out, off, t.numel)
+        off += stripe_in
+    return Tensor(out, dims)
+
+
+@_op("ReduceMean")
+def _reduce_mean(ctx, node, inputs):
+    x = inputs[0]
+    axes = get_attr_ints(node, "axes", [len(x.dims) - 1])
+    keep = get_attr_int(node, "keepdims", 1)
+    if len(axes) != 1 or (axes[0] != -1 and axes[0] != len(x.dims) - 1):
+        raise ValueError(f"ReduceMean: only last-dim reduction supported, got axes {axes}")
+    inner = x.dims[-1]
+    rows = x.numel // inner
+    out = ctx.pool.acquire(rows * 4)
+    ctx.dispatchers.reduce_mean(x.buf, out, inner, rows)
+    return Tensor(out, x.dims[:-1] + [1] if keep else x.dims[:-1])
+
+
+def _unary_gpu(op):
+    def fn(ctx, node, inputs):
+        x = inputs[0]
+        if _is_cpu(x) and op in UNARY_CPU:
+            out = UNARY_CPU[op](x.cpu_data.astype(np.float64)).astype(np.float32)
+            return CpuTensor(out, list(x.dims or []), "float32", True)
+        out = ctx.pool.acquire(x.byte_length)
+        ctx.dispatchers.unary["SiLU" if op == "Silu" else op](x.buf, out, x.numel)
+        return Tensor(out, list(x.dims))
+    return fn
+
+
+for _u in ("Sigmoid", "Sqrt", "Erf", "Abs", "Neg", "Sin", "Cos", "Silu"):
+    OPS[_u] = _unary_gpu(_u)
+
+
+@_op("Pow")
+def _pow(ctx, node, inputs):
+    a, b = inputs[0], inputs[1]
+    exponent = None
+    if b is not None and getattr(b, "cpu_data", None) is not None and b.cpu_data.size >= 1 and \
+            (b.cpu_data.size == 1 or all(d == 1 for d in (b.dims or []))):
+        exponent = float(b.cpu_data.reshape(-1)[0])
+    if exponent is None:
+        raise ValueError(f"Pow: non-scalar exponent not yet supported (b.dims={getattr(b, 'dims', None)})")
+    ag = a if a.buf is not None else ctx.promote(a)
+    out = ctx.pool.acquire(ag.numel * 4)
+    ctx.dispatchers.pow_scalar(ag.buf, out, ag.numel, exponent)
+    return Tensor(out, list(ag.dims))
+
+
+@_op("Expand")
+def _expand(ctx, node, inputs):
+    x, shape = inputs[0], inputs[1]
+    new = [int(v) for v in shape.cpu_data.reshape(-1)] if shape is not None else list(x.dims)
+    if int(np.prod(new)) != int(np.prod(x.dims or [1])):
+        raise ValueError(f"Expand {node.name}: real broadcast {x.dims} -> {new} not implemented")
+    return _passthrough_with_dims(x, new)
+
+
+@_op("Equal")
+def _equal(ctx, node, inputs):
+    a, b = inputs
+    if _is_cpu(a) and _is_cpu(b):
+        av, bv = a.cpu_data.reshape(-1), b.cpu_data.reshape(-1)
+        out = (av.astype(np.float64) == bv.astype(np.float64)).astype(np.uint8)
+        dims = (a.dims if av.size >= bv.size else b.dims) or [out.size]
+        return CpuTensor(out, list(dims), "bool", True)
+    raise ValueError(f"Equal {node.name}: GPU path not implemented")
+
+
+@_op("Where")
+def _where(ctx, node, inputs):
+    c, a, b = inputs
+    if _is_cpu(c) and _is_cpu(a) and _is_cpu(b):
+        cv, av, bv = (t.cpu_data.reshape(-1) for t in (c, a, b))
+        n = max(cv.size, av.size, bv.size)
+        dt = av.dtype if av.size >= bv.size else bv.dtype
+        pick = lambda v, i: v[0] if v.size == 1 else v[i]
+        out = np.array([pick(av, i) if pick(cv, i) else pick(bv, i) for i in range(n)], dt)
+        return CpuTensor(out, [n], a.dtype or b.dtype or "int64",
+                         a.is_shape is not False or b.is_shape is not False)
+    raise ValueError(f"Where {node.name}: GPU path not implemented")
+
+
+def _binary(op):
+    def fn(ctx, node, inputs):
+        a, b = inputs
+        if _is_cpu(a) and _is_cpu(b):
+            dims = broadcast_shape(list(a.dims), list(b.dims))
+            big = a.cpu_data.dtype == np.int64 or b.cpu_data.dtype == np.int64
+            av = a.cpu_data.reshape(a.dims) if a.dims else a.cpu_data.reshape(())
+            bv = b.cpu_data.reshape(b.dims) if b.dims else b.cpu_data.reshape(())
+            if big:
+                av, bv = av.astype(np.int64), bv.astype(np.int64)
+                out = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply,
+                       "Div": _trunc_div}[op](av, bv)
+            else:
+                av, bv = av.astype(np.float32), bv.astype(np.float32)
+                out = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply,
+                       "Div": np.divide}[op](av, bv).astype(np.float32)
+            out = np.broadcast_to(out, dims).reshape(-1).copy()
+            return CpuTensor(out, dims, "int64" if big else "float32",
+                             bool(a.is_shape or b.is_shape))
+        if _is_cpu(a):
+            a = ctx.promote(a)
+        if _is_cpu(b):
+            b = ctx.promote(b)
+        dims = broadcast_shape(list(a.dims), list(b.dims))
+        numel = int(np.prod(dims)) if dims else 1
+        out = ctx.pool.acquire(max(numel * 4, 4))
+        if list(a.dims) == dims and list(b.dims) == dims:
+            ctx.dispatchers.binary[op](a.buf, b.buf, out, numel)
+        else:
+            if len(dims) > 4:
+                raise ValueError(f"{op} broadcast: rank {len(dims)} > 4 not supported")
+            ctx.dispatchers.binary_bcast[op](a.buf, b.buf, out, len(dims), dims,
+                                             _bcast_strides(list(a.dims), dims),
+                                             _bcast_strides(list(b.dims), dims), numel)
+        return Tensor(out, dims)
+    return fn
+
+
+for _b in ("Add", "Sub", "Mul", "Div"):
+    OPS[_b] = _binary(_b)
+
+
+@_op("GroupNorm")
+def _group_norm(ctx, node, inputs):
+    x, g, b = (t if t is None or t.buf is not None else ctx.promote(t) for t in inputs[:3])
+    if not x.dims or len(x.dims) < 2:
+        raise ValueError(f"GroupNorm {node.name}: expected rank>=2 input, got dims={x.dims}")
+    N, C = x.dims[0], x.dims[1]
+    HW = int(np.prod(x.dims[2:])) if len(x.dims) > 2 else 1
+    G = int(get_attr_int(node, "num_groups", 32))
+    if C % G:
+        raise ValueError(f"GroupNorm: C={C} not divisible by G={G}")
+    eps = get_attr_float(node, "epsilon", 1e-5)
+    out = ctx.pool.acquire(N * C * HW * 4)
+    ctx.dispatchers.group_norm(x.buf, g.buf, b.buf, out, N, G, C // G, HW, eps)
+    return Tensor(out, list(x.dims))
+
+
+@_op("AffineBcast")
+def _affine_bcast(ctx, node, inputs):
+    x, g, b = (t if t.buf is not None else ctx.promote(t) for t in inputs[:3])
+    dims = list(x.dims)
+    if len(dims) > 4:
+        raise ValueError(f"AffineBcast: rank {len(dims)} > 4")
+    numel = int(np.prod(dims))
+    out = ctx.pool.acquire(numel * 4)
+    ctx.dispatchers.affine_bcast(x.buf, g.buf, b.buf, out, len(dims), dims,
+                                 _bcast_strides(dims, dims), _bcast_strides(list(g.dims), dims),
+                                 numel)
+    return Tensor(out, dims)
+
+
+@_op("InstanceNormalization")
+def _instance_norm(ctx, node, inputs):
+    """eps 1e-5 regardless of the node attribute, as the reference kernel
+    hard-codes it (wgsl-executor.js:1020; GroupNorm carries the real eps)."""
+    x, g, b = inputs[:3]
+    if len(x.dims) == 4:
+        N, C, HW = x.dims[0], x.dims[1], x.dims[2] * x.dims[3]
+    elif len(x.dims) == 3:
+        N, C, HW = x.dims
+    else:
+        raise ValueError(f"InstanceNorm needs 3D or 4D input, got {len(x.dims)}D")
+    g = g if g.buf is not None else ctx.promote(g)
+    b = b if b.buf is not None else ctx.promote(b)
+    out = ctx.pool.acquire(x.byte_length)
+    ctx.dispatchers.instance_norm(x.buf, g.buf, b.buf, out, N, C, HW, 1e-5)
+    return Tensor(out, list(x.dims))
+
+
+@_op("Softmax")
+def _softmax(ctx, node, inputs):
+    x = inputs[0]
+    axis = get_attr_int(node, "axis", -1)
+    ax = axis + len(x.dims) if axis < 0 else axis
+    if ax != len(x.dims) - 1:
+        raise ValueError(f"Softmax: only last-axis supported, got axis={axis} dims={x.dims}")
+    inner = x.dims[ax]
+    out = ctx.pool.acquire(x.byte_length)
+    ctx.dispatchers.softmax(x.buf, out, inner, x.numel // inner)
+    return Tensor(out, list(x.dims))
+
+
+@_op("MatMul")
+def _matmul(ctx, node, inputs):
+    a, b = inputs
+    M, K, N = a.dims[-2], a.dims[-1], b.dims[-1]
+    batch = int(np.prod(a.dims[:-2])) if len(a.dims) > 2 else 1
+    b_batch = int(np.prod(b.dims[:-2])) if len(b.dims) > 2 else 1
+    if b_batch != 1 and b_batch != batch:
+        raise ValueError(f"MatMul: batch mismatch a={a.dims} b={b.dims}")
+    if batch == 1 and b_batch > 1:
+        raise ValueError("MatMul: batched B with unbatched A not supported")
+    out = ctx.pool.acquire(batch * M * N * 4)
+    ctx.dispatchers.matmul(a.buf, b.buf, out, M, N, K, batch, 1 if b_batch > 1 else 0)
+    return Tensor(out, list(a.dims[:-2]) + [M, N])
+
+
+@_op("Gemm")
+def _gemm(ctx, node, inputs):
+    a, b = inputs[0], inputs[1]
+    c = inputs[2] if len(inputs) > 2 else None
+    tb = get_attr_int(node, "transB", 0)
+    M, K = a.dims
+    N = b.dims[0] if tb else b.dims[1]
+    out = ctx.pool.acquire(M * N * 4)
+    ctx.dispatchers.gemm(a.buf, b.buf, c.buf if c is not None else None, out, M, N, K, tb)
+    return Tensor(out, [M, N])
+
+
+@_op("Conv")
+def _conv(ctx, node, inputs):
+    x, w = inputs[0], inputs[1]
+    bias = inputs[2] if len(inputs) > 2 else None
+    ks = get_attr_ints(node, "kernel_shape", [3, 3])
+    if ks[0] != ks[1]:
+        raise ValueError(f"Conv: non-square kernel {ks} not supported")
+    K = ks[0]
+    st = get_attr_ints(node, "strides", [1, 1])
+    if st[0] != st[1]:
+        raise ValueError(f"Conv: non-square stride {st} not supported")
+    S = st[0]
+    pads = get_attr_ints(node, "pads", [(K - 1) >> 1] * 4)
+    if not (pads[0] == pads[1] == pads[2] == pads[3]):
+        raise ValueError(f"Conv: asymmetric pads {pads} not supported")
+    P = pads[0]
+    N, Cin, H, W = x.dims
+    Cout = w.dims[0]
+    Ho, Wo = (H + 2 * P - K) // S + 1, (W + 2 * P - K) // S + 1
+    out = ctx.pool.acquire(N * Cout * Ho * Wo * 4)
+    ctx.dispatchers.conv_mm(x.buf, w.buf, bias.buf if bias is not None else None, out, N, Cin,
+                            Cout, H, W, K, S, P)
+    return Tensor(out, [N, Cout, Ho, Wo])
+
+
+@_op("Resize")
+def _resize(ctx, node, inputs):
+    x = inputs[0]
+    if get_attr_string(node, "mode", "nearest") != "nearest":
+        raise ValueError(f"Resize mode {get_attr_string(node, 'mode', '')} not yet supported")
+    sc = inputs[2] if len(inputs) > 2 else None
+    scales = sc.cpu_data.reshape(-1) if sc is not None and getattr(sc, "cpu_data", None) is not None \
+        else None
+    sh = float(scales[2]) if scales is not None else 2.0
+    sw = float(scales[3]) if scales is not None else 2.0
+    N, C, H, W = x.dims
+    Ho, Wo = int(round(H * sh)), int(round(W * sw))
+    out = ctx.pool.acquire(N * C * Ho * Wo * 4)
+    ctx.dispatchers.resize_nearest(x.buf, out, N * C, H, W, Ho, Wo)
+    return Tensor(out, [N, C, Ho, Wo])
+
+
+# ---------------------------------------------------------- graph rewrites --
+def _consumers_and_producers(graph: Graph):
+    consumers: Dict[str, int] = {}
+    for n in graph.nodes:
+        for i in n.inputs:
+            if i:
+                consumers[i] = consumers.get(i, 0) + 1
+    for o in graph.outputs or []:
+        consumers[o["name"]] = consumers.get(o["name"], 0) + 1
+    producer = {}
+    for idx, n in enumerate(graph.nodes):
+        for o in n.outputs:
+            producer[o] = idx
+    return consumers, producer
+
+
+def fuse_silu_pattern(graph: Graph) -> dict:
+    """Sigmoid(X) -> Mul(X, sig) => Silu(X) when the Sigmoid output has the
+    Mul as its only consumer (wgsl-executor.js:799-839)."""
+    nodes = graph.nodes
+    consumers, producer = _consumers_and_producers(graph)
+    drop, fused = set(), 0
+    for i, mul in enumerate(nodes):
+        if mul.op_type != "Mul":
+            continue
+        a, b = (mul.inputs + [None, None])[:2]
+
+        def try_fuse(sig_out, other):
+            nonlocal fused
+            if not sig_out or not other or consumers.get(sig_out, 0) != 1:
+                return False
+            pi = producer.get(sig_out)
+            if pi is None:
+                return False
+            sig = nodes[pi]
+            if sig.op_type != "Sigmoid" or sig.inputs[0] != other:
+                return False
+            nodes[i] = Node("Silu", (mul.name or "") + "_fused", [other], list(mul.outputs), [])
+            drop.add(pi)
+            fused += 1
+            return True
+        if not try_fuse(a, b):
+            try_fuse(b, a)
+    if fused:
+        graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
+    return {"fused": fused}
+
+
+def fuse_mul_add_pattern(graph: Graph, tensor_shapes: Optional[dict] = None) -> dict:
+    """Mul(X, gamma) -> Add(., beta) => AffineBcast(X, gamma, beta) when gamma
+    and beta have identical shapes and the Mul output has one consumer
+    (wgsl-executor.js:845-898)."""
+    nodes = graph.nodes
+    consumers, producer = _consumers_and_producers(graph)
+    drop, fused = set(), 0
+
+    def shape_of(name):
+        if tensor_shapes and name in tensor_shapes:
+            return list(tensor_shapes[name])
+        t = graph.tensors.get(name) if graph.tensors else None
+        return list(t.dims) if t is not None else None
+
+    for i, add in enumerate(nodes):
+        if add.op_type != "Add":
+            continue
+        a, b = (add.inputs + [None, None])[:2]
+
+        def try_fuse(mul_out, beta):
+            nonlocal fused
+            if consumers.get(mul_out, 0) != 1:
+                return False
+            pi = producer.get(mul_out)
+            if pi is None or nodes[pi].op_type != "Mul":
+                return False
+            mul = nodes[pi]
+            ma, mb = mul.inputs[:2]
+            sa, sb, sbeta = shape_of(ma), shape_of(mb), shape_of(beta)
+            if not sbeta:
+                return False
+            if sa is not None and sa == sbeta:
+                x, gamma = mb, ma
+            elif sb is not None and sb == sbeta:
+                x, gamma = ma, mb
+            else:
+                return False
+            nodes[i] = Node("AffineBcast", (mul.name or "") + "_affinefused", [x, gamma, beta],
+                            list(add.outputs), [])
+            drop.add(pi)
+            fused += 1
+            return True
+        if not try_fuse(a, b):
+            try_fuse(b, a)
+    if fused:
+        graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
+    return {"fused": fused}
+
+
+def _uniform_value(t: TensorProto):
+    if t.dtype not in ("float32", "float16") or t.data is None:
+        return None
+    f = t.array().astype(np.float32)
+    if f.size == 0:
+        return None
+    return float(f[0]) if np.all(f == f[0]) else None
+
+
+def fuse_group_norm_pattern(graph: Graph) -> dict:
+    """Reshape(X,[N,G,-1]) -> InstanceNorm(., ones, zeros) -> Reshape(., shape)
+    -> AffineBcast(., gamma, beta) => GroupNorm(X, gamma, beta)
+    (wgsl-executor.js:905-1008).  Scale/bias constants resolve from Constant
+    nodes or initializers; G is read from a Constant-node reshape shape (index
+    1), default 32, as in the reference.  Run after fuse_mul_add_pattern."""
+    nodes = graph.nodes
+    consumers, producer = _consumers_and_producers(graph)
+
+    def const_val(name):
+        init = graph.tensors.get(name) if graph.tensors else None
+        if init is not None and init.data is not None:
+            return _uniform_value(init)
+        pi = producer.get(name)
+        if pi is None or nodes[pi].op_type != "Constant":
+            return None
+        a = _attr(nodes[pi], "value")
+        return _uniform_value(a.t) if a is not None and a.t is not None and a.t.data is not None \
+            else None
+
+    drop, fused = set(), 0
+    for i, aff in enumerate(nodes):
+        if aff.op_type != "AffineBcast":
+            continue
+        aff_x, gamma, beta = aff.inputs[:3]
+        if consumers.get(aff_x, 0) != 1:
+            continue
+        r1 = producer.get(aff_x)
+        if r1 is None or nodes[r1].op_type != "Reshape":
+            continue
+        in_out = nodes[r1].inputs[0]
+        if consumers.get(in_out, 0) != 1:
+            continue
+        ii = producer.get(in_out)
+        if ii is None or nodes[ii].op_type != "InstanceNormalization":
+            continue
+        in_node = nodes[ii]
+        resh_out, scale, bias = in_node.inputs[:3]
+        if const_val(scale) != 1 or const_val(bias) != 0:
+            continue
+        if consumers.get(resh_out, 0) != 1:
+            continue
+        r0 = producer.get(resh_out)
+        if r0 is None or nodes[r0].op_type != "Reshape":
+            continue
+        x_name, shape0 = nodes[r0].inputs[:2]
+        G = 32
+        rsp = producer.get(shape0)
+        if rsp is not None and nodes[rsp].op_type == "Constant":
+            a = _attr(nodes[rsp], "value")
+            if a is not None and a.t is not None and a.t.dtype == "int64" and a.t.data is not None:
+                v = a.t.array()
+                if v.size >= 2:
+                    G = int(v[1])
+        eps = get_attr_float(in_node, "epsilon", 1e-5)
+        nodes[i] = Node("GroupNorm", (aff.name or "") + "_gn", [x_name, gamma, beta],
+                        list(aff.outputs), [Attr("num_groups", i=G), Attr("epsilon", f=eps)])
+        drop.update((r1, ii, r0))
+        fused += 1
+    if fused:
+        graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
+    return {"fused": fused}
+
+
+# ---------------------------------------------------------------- planning --
+def plan_execution(graph: Graph) -> dict:
+    unsupported: Dict[str, int] = {}
+    supported = 0
+    for n in graph.nodes:
+        if n.op_type in OPS:
+            supported += 1
+        else:
+            unsupported[n.op_type] = unsupported.get(n.op_type, 0) + 1
+    total = len(graph.nodes)
+    return {"total": total, "supported_count": supported,
+            "coverage": supported / total if total else 1.0,
+            "unsupported_ops": sorted(unsupported.items(), key=lambda kv: -kv[1])}
+
+
+def infer_graph_io(nodes: List[Node], weight_names) -> dict:
+    """Graph inputs = consumed but never produced and not weights; outputs =
+    produced but never consumed (wgsl-executor.js:1205-1221)."""
+    produced, consumed = [], []
+    ps, cs = set(), set()
+    for n in nodes:
+        for i in n.inputs:
+            if i and i not in cs:
+                cs.add(i)
+                consumed.append(i)
+        for o in n.outputs:
+            if o not in ps:
+                ps.add(o)
+                produced.append(o)
+    return {"inputs": [{"name": c} for c in consumed if c not in ps and c not in weight_names],
+            "outputs": [{"name": p} for p in produced if p not in cs]}
+
+
+# ---------------------------------------------------------------- executor --
+METADATA_OPS = {"Reshape", "Shape", "Unsqueeze", "Squeeze", "Gather", "Slice", "Concat", "Constant",
+                "ConstantOfShape", "Cast", "Expand", "Equal", "Where", "Identity", "Transpose"}
+BINARY_SHAPE_AWARE = {"Add", "Sub", "Mul", "Div"}
+
+
+class ExecutorError(RuntimeError):
+    pass
+
+
+class _Ctx:
+    def __init__(self, device, pool, dispatchers, weights, promote):
+        self.device = device
+        self.pool = pool
+        self.dispatchers = dispatchers
+        self.weights = weights
+        self.promote = promote
+
+
+class Executor:
+    """Walks a topologically sorted graph, one C-ABI dispatch per GPU node
+    (wgsl-executor.js:1223-1466)."""
+
+    def __init__(self, device: Device, graph: Graph, weight_cache: WeightCache):
+        self.device = device
+        self.graph = graph
+        self.weights = weight_cache
+        self.pool = BufferPool(device)
+        self.dispatchers = create_dispatchers(device)
+        if not graph.inputs or not graph.outputs:
+            io = infer_graph_io(graph.nodes, set(weight_cache.tensors.keys()))
+            if not graph.inputs:
+                graph.inputs = io["inputs"]
+            if not graph.outputs:
+                graph.outputs = io["outputs"]
+        self.consumers: Dict[str, int] = {}
+        for n in graph.nodes:
+            for i in n.inputs:
+                if i:
+                    self.consumers[i] = self.consumers.get(i, 0) + 1
+        for o in graph.outputs:
+            self.consumers[o["name"]] = self.consumers.get(o["name"], 0) + 1
+        self.graph_input_names = {i["name"] for i in graph.inputs}
+        self._temps: List[Buffer] = []
+
+    def _promote(self, t):
+        """CPU-only tensor -> device fp32 tensor (a pool buffer released at the
+        end of the run)."""
+        if t is None or getattr(t, "buf", None) is not None:
+            return t
+        f = np.asarray(t.cpu_data).astype(np.float32).reshape(-1)
+        buf = self.pool.acquire(max(f.nbytes, 4))
+        self.device.upload(buf, f)
+        self._temps.append(buf)
+        return Tensor(buf, list(t.dims) if t.dims is not None else [f.size])
+
+    def run(self, inputs: Dict[str, Any]) -> Dict[str, Tensor]:
+        """One forward pass.  ``inputs``: name -> Tensor | CpuTensor | numpy
+        array (uploaded as fp32; float arrays keep their shape, int arrays
+        stay on the CPU as shape tensors)."""
+        consumers = dict(self.consumers)
+        env: Dict[str, Any] = {}
+        self._temps = []
+        for name, val in inputs.items():
+            if isinstance(val, (Tensor, CpuTensor)):
+                env[name] = val
+            elif isinstance(val, np.ndarray):
+                if val.dtype.kind in "iu":
+                    env[name] = CpuTensor(val.reshape(-1), list(val.shape), _dtype_of(val), True)
+                else:
+                    f = np.ascontiguousarray(val, np.float32)
+                    env[name] = Tensor(self.device.storage(f), list(f.shape))
+            else:
+                raise ExecutorError(f'unsupported input seed for "{name}": {type(val).__name__}')
+        ctx = _Ctx(self.device, self.pool, self.dispatchers, self.weights, self._promote)
+        LOG["t0"] = time.perf_counter()
+        LOG["node_count"] = len(self.graph.nodes)
+        LOG["op_hist"] = {}
+        if LOG["profile"]:
+            LOG["profile_data"] = []
+        deferred: List[Buffer] = []
+        for ni, node in enumerate(self.graph.nodes):
+            op = OPS.get(node.op_type)
+            if op is None:
+                raise ExecutorError(f"unsupported op @{ni}: {node.op_type} ({node.name})")
+            LOG["op_hist"][node.op_type] = LOG["op_hist"].get(node.op_type, 0) + 1
+            ins = []
+            for name in node.inputs:
+                if not name:
+                    ins.append(None)
+                elif name in env:
+                    ins.append(env[name])
+                elif self.weights.has(name):
+                    ins.append(self.weights.get(name))
+                else:
+                    raise ExecutorError(f"tensor not found @{ni} {node.op_type}: {name}")
+            if node.op_type not in METADATA_OPS:
+                keep_int = node.op_type in BINARY_SHAPE_AWARE
+                promoted = []
+                for t in ins:
+                    if t is None or getattr(t, "buf", None) is not None:
+                        promoted.append(t)
+                    elif keep_int and t.cpu_data.dtype in (np.int64, np.int32):
+                        promoted.append(t)
+                    elif t.cpu_data.size == 1:
+                        promoted.append(t)  # scalar CPU constants feed CPU fast paths
+                    else:
+                        promoted.append(self._promote(t))
+                ins = promoted
+            t_prof = time.perf_counter()
+            try:
+                out = op(ctx, node, ins)
+            except Exception as e:  # noqa: BLE001 - re-raised with the node context
+                descs = ",".join("null" if t is None else (f"GPU{t.dims}" if getattr(t, "buf", None)
+                                 is not None else f"CPU{t.dims}:{t.dtype}") for t in ins)
+                _dlog(f"FAIL @{ni} {node.op_type} ({node.name}): {e} ins={descs}")
+                raise ExecutorError(f"op @{ni} {node.op_type} ({node.name}) failed: {e}") from e
+            if len(node.outputs) > 1:
+                raise ExecutorError(f"multi-output op not supported yet: {node.op_type}")
+            _dlog(f"@{ni} {node.op_type:<18} {node.name} -> {out!r} pool.live={self.pool.live}")
+            if LOG["traffic"] and node.op_type not in METADATA_OPS:
+                td = LOG["traffic_data"] = LOG["traffic_data"] or {"weights": 0, "acts": 0,
+                                                                   "out": 0, "by_op": {}}
+                nb = 0
+                for name, t in zip(node.inputs, ins):
+                    if t is None or getattr(t, "buf", None) is None:
+                        continue
+                    nb += t.byte_length
+                    td["weights" if self.weights.has(name) else "acts"] += t.byte_length
+                if getattr(out, "buf", None) is not None:
+                    td["out"] += out.byte_length
+                    nb += out.byte_length
+                td["by_op"][node.op_type] = td["by_op"].get(node.op_type, 0) + nb
+            env[node.outputs[0]] = out
+            if LOG["profile"] and getattr(out, "buf", None) is not None:
+                self.device.sync()
+                LOG["profile_data"].append({"ni": ni, "op": node.op_type, "name": node.name,
+                                            "dims": out.dims,
+                                            "ms": (time.perf_counter() - t_prof) * 1e3})
+            out_buf = getattr(out, "buf", None)
+            for name in node.inputs:
+                if not name or name not in env:
+                    continue
+                t = env[name]
+                consumers[name] = consumers.get(name, 0) - 1
+                if consumers[name] <= 0 and getattr(t, "buf", None) is not None and \
+                        t.buf is not out_buf and not self.weights.has(name) and \
+                        name not in self.graph_input_names:
+                    deferred.append(t.buf)
+                    del env[name]
+        # snapshot graph outputs into fresh buffers owned by the caller
+        snaps: Dict[str, Tensor] = {}
+        for o in self.graph.outputs:
+            t = env.get(o["name"])
+            if getattr(t, "buf", None) is None:
+                continue
+            stable = self.device.create_buffer(max(t.numel * 4, 4))
+            self.device.copy(stable, t.buf, t.numel * 4)
+            snaps[o["name"]] = Tensor(stable, list(t.dims))
+        self.device.sync()
+        # Everything pool-owned goes back once the device is done: deferred
+        # intermediates, alias-held env entries, CPU promotions and the graph
+        # outputs' own buffers (the caller holds the snapshots).  The reference
+        # keeps the last two live forever, so its pool grows on every run.
+        released = set()
+        for buf in deferred + self._temps:
+            if id(buf) in released:
+                continue
+            released.add(id(buf))
+            self.pool.release(buf)
+        for name, t in env.items():
+            b = getattr(t, "buf", None)
+            if b is None or id(b) in released or self.weights.has(name) or \
+                    name in self.graph_input_names or not self.pool.owns(b):
+                continue
+            released.add(id(b))
+            self.pool.release(b)
+        self._temps = []
+        _dlog(f"run: done in {(time.perf_counter() - LOG['t0']) * 1e3:.1f} ms "
+              f"pool.allocs={self.pool.allocs} peak={self.pool.peak}")
+        return {o["name"]: snaps.get(o["name"], env.get(o["name"])) for o in self.graph.outputs}
+
+    def destroy(self) -> None:
+        self.pool.destroy()

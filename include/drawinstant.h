@@ -78,6 +78,8 @@ typedef uint64_t di_handle;
 /* ---- conv flags ---- */
 #define DI_CONV_F16_COMPUTE 1 /* NCHW fp32 tensors through the fp16 MFMA path */
 #define DI_CONV_UPSAMPLE2X 2  /* convolve the 2x nearest-upsampled input */
+#define DI_CONV_SILU 4        /* epilogue silu(conv + bias) before the residual:
+                                 WGSL_CONV silu(sum) + residual, fused-conv.js:50-100 */
 
 /* ---- attention tensor layouts ---- */
 #define DI_ATTN_BSHD 0 /* [B, S, H, d]: fused-attn.js:69-70 */
@@ -249,7 +251,8 @@ int32_t di_linear(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_hand
  *   layout DI_NCHW: X NCHW, W OIHW, dtype fp32 (exact fp32 MFMA), or with
  *                   DI_CONV_F16_COMPUTE fp16-in / fp32-acc MFMA;
  *   layout DI_NHWC: X NHWC fp16, W OHWI fp16 ([Cout][K][K][Cin]), Cin % 8 == 0.
- * DI_CONV_UPSAMPLE2X convolves the 2x nearest upsample of X (H, W are X's). */
+ * DI_CONV_UPSAMPLE2X convolves the 2x nearest upsample of X (H, W are X's).
+ * DI_CONV_SILU applies SiLU to conv + bias; R (if any) is added after it. */
 int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_handle R,
                   di_handle Y, uint32_t N, uint32_t Cin, uint32_t Cout, uint32_t H,
                   uint32_t Wd, uint32_t K, uint32_t S, uint32_t pad, int32_t flags,
