@@ -194,3 +194,37 @@ class UNet:
 def load_unet(device: Device, config: UNetConfig | None = None, seed: int = 0) -> UNet:
     """loadUNetWGSL counterpart: build the model on the device."""
     return UNet(device, config, seed)
+
+
+_state: dict = {}
+
+
+def unet_forward_hip(sample: np.ndarray, timestep, cond: np.ndarray, B: int = 1, H: int = 64,
+                     W: int = 64, tokens: int = 77, dim: int = 1024, seed: int = 0,
+                     graph: bool = True) -> dict:
+    """unetForwardWGSL (unet-wgsl.js:145-195): sample [B,4,H,W] fp32, one
+    scheduler timestep, cond [B,tokens,dim] -> {"out": [B,4,H,W] fp32,
+    "dims", "ms"}.  The timestep is rounded to an integer, as the reference
+    passes it to its int64 graph input; the model is built once per process
+    (the reference's ``_state``) from seeded weights."""
+    st = _state.get("unet")
+    if st is None:
+        dev = Device(0)
+        st = _state["unet"] = (dev, UNet(dev, seed=seed))
+    dev, u = st
+    sample = np.ascontiguousarray(sample, np.float32).reshape(B, 4, H, W)
+    cond = np.ascontiguousarray(cond, np.float32).reshape(B, tokens, dim)
+    ts_val = timestep if np.isscalar(timestep) else np.asarray(timestep).reshape(-1)[0]
+    ts = np.full(B, float(round(float(ts_val))), np.float32)
+    bs, bt, bc = dev.storage(sample), dev.storage(ts), dev.storage(cond)
+    bo = dev.create_buffer(sample.nbytes)
+    try:
+        import time
+        t0 = time.perf_counter()
+        u.forward(bs, bt, bc, bo, B, H, W, tokens, graph)
+        out = dev.download(bo, np.float32, (B, 4, H, W))  # implicit sync; raises on faults
+        ms = (time.perf_counter() - t0) * 1e3
+    finally:
+        for b in (bs, bt, bc, bo):
+            b.destroy()
+    return {"out": out, "dims": [B, 4, H, W], "ms": ms}

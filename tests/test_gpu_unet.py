@@ -127,3 +127,15 @@ def test_state_dict_round_trip(dev):
     finally:
         a.destroy()
         b.destroy()
+
+
+def test_unet_forward_hip_entry_point(sd21, rng):
+    """unetForwardWGSL counterpart: integer-rounded timestep, host arrays in
+    and out; equals UNet.forward on the same (seed 0) weights."""
+    from drawinstant import unet as U
+    x, ctx = _inputs(rng, 1, 64, 64, 77, 1024)
+    res = U.unet_forward_hip(x, 998.6, ctx)
+    assert res["dims"] == [1, 4, 64, 64] and res["ms"] > 0
+    dev, u = U._state["unet"]
+    direct = u(x, 999.0, ctx)
+    np.testing.assert_array_equal(res["out"], direct)
