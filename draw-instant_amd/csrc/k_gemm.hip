@@ -84,6 +84,12 @@ template <typename V>
 __device__ __forceinline__ V buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// voff per lane, soff uniform (scalar register): the per-stage advance costs
+// no vector instructions
+template <typename V>
+__device__ __forceinline__ V buf_load16s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
 
 // ---- epilogue (shared by the GEMM kernel and the split-K reducer) ----
 template <typename T>
@@ -297,7 +303,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   constexpr int KV = MT::KV;
   constexpr int BK = 128 / sizeof(T);  // k elements per stage (128 bytes per row)
   constexpr int VPR = BK / KV;         // 16-byte vectors per row per stage (8)
-  constexpr int LDK = BK + KV;         // padded LDS row (elements)
+  // LDS rows are BK elements (128 bytes, 8 chunks of 16 bytes) with the
+  // chunk position XOR-swizzled by (row >> 1) & 7: the 8 lanes writing one row
+  // and the 16 lanes reading one fragment column (16 rows) hit distinct banks.
+  constexpr int LDK = BK;
   constexpr int NVA = BM * VPR / 256;  // A vectors per thread per stage
   constexpr int NVB = BN * VPR / 256;
   constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
@@ -307,9 +316,15 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
   // Pipeline buffers sA[2][BM*LDK], sB[2][BN*LDK]; reused by the fp32 C tile
   // of the vector epilogue.
-  __shared__ __attribute__((aligned(16))) T smem[2 * (BM + BN) * LDK];
+  constexpr int kSmemPipe = 2 * (BM + BN) * LDK;
+  constexpr int kSmemC = BM * (BN + 4) * 4 / (int)sizeof(T);  // fp32 C tile of the vector epilogue
+  __shared__ __attribute__((aligned(16))) T smem[kSmemPipe > kSmemC ? kSmemPipe : kSmemC];
   T (*sA)[BM * LDK] = reinterpret_cast<T (*)[BM * LDK]>(smem);
   T (*sB)[BN * LDK] = reinterpret_cast<T (*)[BN * LDK]>(smem + 2 * BM * LDK);
+  // element offset of (row r, k element e) inside one buffer
+  auto lds_at = [](int r, int e) {
+    return r * LDK + (((e / KV) ^ ((r >> 1) & 7)) * KV) + e % KV;
+  };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
@@ -386,14 +401,15 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < NVA; i++) {
       const uint32_t m = m0 + (tid + i * 256) / VPR;
-      fa1[i] = m < g.M ? m * (uint32_t)g.lda * 2u : kInv;
+      // row base + this thread's k chunk at k_begin; stages add a scalar offset
+      fa1[i] = m < g.M ? m * (uint32_t)g.lda * 2u + (k_begin + kc * KV) * 2u : kInv;
       fa2[i] = m < g.M ? m * (uint32_t)g.lda2 * 2u : kInv;
       fimg[i] = (uint32_t)a_row_off[i] * g.H;
     }
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
       const uint32_t n = n0 + (tid + i * 256) / VPR;
-      fb[i] = n < g.N ? n * (uint32_t)g.ldb * 2u : kInv;
+      fb[i] = n < g.N ? n * (uint32_t)g.ldb * 2u + (k_begin + kc * KV) * 2u : kInv;
     }
     if constexpr (AM == A_CONV_NHWC) {
       const uint32_t tap0 = k_begin / g.Cin;
@@ -507,18 +523,18 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < NVA; i++) {
       uint32_t r = (tid + i * 256) / VPR;
-      *(typename MT::vec*)&sA[buf][r * LDK + kc * KV] = st.a[i];
+      *(typename MT::vec*)&sA[buf][lds_at(r, kc * KV)] = st.a[i];
     }
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
       if constexpr (BMD == B_NK) {
         uint32_t r = (tid + i * 256) / VPR;
-        *(typename MT::vec*)&sB[buf][r * LDK + kc * KV] = st.b[i];
+        *(typename MT::vec*)&sB[buf][lds_at(r, kc * KV)] = st.b[i];
       } else {
         constexpr int VPK = BN / KV;
         uint32_t kr = (tid + i * 256) / VPK, nc = (tid + i * 256) % VPK;
 #pragma unroll
-        for (int j = 0; j < KV; j++) sB[buf][(nc * KV + j) * LDK + kr] = st.b[i][j];
+        for (int j = 0; j < KV; j++) sB[buf][lds_at(nc * KV + j, kr)] = st.b[i][j];
       }
     }
   };
@@ -535,25 +551,27 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     for (int kk = 0; kk < BK; kk += MT::KM) {
       typename MT::frag af[TM], bf[TN];
 #pragma unroll
-      for (int a = 0; a < TM; a++) af[a] = ld_frag<T>(&sA[buf][(wm0 + a * 16 + fr) * LDK + kk + fk]);
+      for (int a = 0; a < TM; a++) af[a] = ld_frag<T>(&sA[buf][lds_at(wm0 + a * 16 + fr, kk + fk)]);
 #pragma unroll
-      for (int b = 0; b < TN; b++) bf[b] = ld_frag<T>(&sB[buf][(wn0 + b * 16 + fr) * LDK + kk + fk]);
+      for (int b = 0; b < TN; b++) bf[b] = ld_frag<T>(&sB[buf][lds_at(wn0 + b * 16 + fr, kk + fk)]);
 #pragma unroll
       for (int a = 0; a < TM; a++)
 #pragma unroll
         for (int b = 0; b < TN; b++) acc[a][b] = MT::mma(af[a], bf[b], acc[a][b]);
     }
   };
+  // FAST loads need K % BK == 0 (gemm_fast_ok), so every stage of a split is
+  // whole: no per-lane k bound.  Stages past the split's end (the ring's
+  // padding) read whatever lies beyond (zeros past the buffer) and are never
+  // computed; rows past M / N carry an out-of-range offset and read zeros.
   auto load_fast = [&](int stage, Stage& st) {
-    const uint32_t kbase = k_begin + stage * BK;
-    const uint32_t k = kbase + kc * KV;
-    const bool kval = k < k_end;
+    const uint32_t sk = (uint32_t)stage * (BK * 2u);
     if constexpr (AM == A_DENSE) {
       // single source (gemm_fast_ok): one descriptor, so it stays uniform; a
-      // per-stage choice between two descriptors merged with the per-lane k
-      // bound makes the compiler emit a waterfall loop around every load
+      // per-stage choice between two descriptors merged with a per-lane
+      // condition makes the compiler emit a waterfall loop around every load
 #pragma unroll
-      for (int i = 0; i < NVA; i++) st.a[i] = buf_load16<typename MT::vec>(rA, kval ? fa1[i] + k * 2u : kInv);
+      for (int i = 0; i < NVA; i++) st.a[i] = buf_load16s<typename MT::vec>(rA, fa1[i], sk);
     } else {
       const bool s2 = f_ci0 >= g.c1;
       const uint32_t cb = ((s2 ? f_ci0 - g.c1 : f_ci0) + kc * KV) * 2u;
@@ -562,7 +580,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < NVA; i++) {
         const int iy = a_iy0[i] + (int)f_ky, ix = a_ix0[i] + (int)f_kx;
-        const bool ok = a_row_ok[i] && kval && iy >= 0 && iy < Hi_ && ix >= 0 && ix < Wi_;
+        const bool ok = a_row_ok[i] && iy >= 0 && iy < Hi_ && ix >= 0 && ix < Wi_;
         const uint32_t pix = (fimg[i] + ((uint32_t)iy >> upsh)) * g.W + ((uint32_t)ix >> upsh);
         st.a[i] = buf_load16<typename MT::vec>(s2 ? rA2 : rA, ok ? pix * ld2 + cb : kInv);
       }
@@ -576,7 +594,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
       }
     }
 #pragma unroll
-    for (int i = 0; i < NVB; i++) st.b[i] = buf_load16<typename MT::vec>(rB, kval ? fb[i] + k * 2u : kInv);
+    for (int i = 0; i < NVB; i++) st.b[i] = buf_load16s<typename MT::vec>(rB, fb[i], sk);
   };
   auto load = [&](int stage, Stage& st) {
     if constexpr (FAST) {
@@ -587,14 +605,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
   };
 
-  // FAST path: a ring of D register stages.  Sub-step s issues the loads of
-  // stage s+D into the slot stage s just left, computes stage s from LDS
-  // buffer s%2, then stores stage s+1 (loaded D-1 sub-steps earlier) into the
-  // other buffer; one barrier per stage.  D stages are in flight, so each
-  // global load has D-1 stages of work to arrive.  Loads past the last stage
-  // read zeros (offsets out of range) and stages past the end skip their MFMA
-  // work, so the loop body has no branches around loads and the waitcnt pass
-  // keeps exact vmcnt counts.
+  // FAST path: a ring of D register stages and two LDS buffers.  Sub-step s
+  // first writes stage s+1 (loaded D sub-steps earlier) into LDS buffer
+  // (s+1)%2, refills that register slot with stage s+1+D, then computes stage
+  // s from buffer s%2; one barrier per stage.  Writing before computing keeps
+  // the LDS-write latency and the global-load wait off the end of the stage,
+  // where they would sit in front of the barrier.  Buffer (s+1)%2 was last
+  // read by compute(s-1), which every wave finished before the previous
+  // barrier.  Loads past the last stage read zeros (offsets out of range) and
+  // stages past the end skip their MFMA work, so the loop body has no branches
+  // around loads and the waitcnt pass keeps exact vmcnt counts.
   Stage r0, r1;
   if constexpr (FAST) {
     static_assert(D % 2 == 0, "even ring depth: LDS buffer = stage parity");
@@ -603,14 +623,30 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < D; j++) load(j, r[j]);
       store_stage(0, r[0]);
+      load(D, r[0]);
       __syncthreads();
-      for (int s0 = 0; s0 < n_stages; s0 += D) {
+      // steady state: whole rounds of D stages, no conditions (a conditional
+      // compute makes the compiler copy the accumulators around it)
+      int s0 = 0;
+      for (; s0 + D <= n_stages; s0 += D) {
 #pragma unroll
         for (int j = 0; j < D; j++) {
-          const int s = s0 + j;
-          load(s + D, r[j]);
-          if (s < n_stages) compute(j & 1);
           store_stage((j + 1) & 1, r[(j + 1) % D]);
+          load(s0 + j + 1 + D, r[(j + 1) % D]);
+          // issue the loads here, not after the MFMAs (the scheduler would
+          // otherwise sink them and shorten the prefetch distance)
+          __builtin_amdgcn_sched_barrier(0);
+          compute(j & 1);
+          __syncthreads();
+        }
+      }
+      // tail: the last n_stages % D stages (stage s0 + j in LDS buffer j & 1)
+      const int rem = n_stages - s0;
+#pragma unroll
+      for (int j = 0; j + 1 < D; j++) {
+        if (j < rem) {
+          if (j + 1 < rem) store_stage((j + 1) & 1, r[(j + 1) % D]);
+          compute(j & 1);
           __syncthreads();
         }
       }
@@ -641,7 +677,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   if constexpr (sizeof(T) == 2) {
     if (g.vec_epi) {
       constexpr int LDC = BN + 4;
-      static_assert(BM * LDC * 4 <= (int)sizeof(smem), "C tile fits the pipeline LDS");
+      static_assert(BM * LDC * 4 <= (int)sizeof(smem), "C tile fits the LDS allocation");
       float* sC = reinterpret_cast<float*>(smem);
       __syncthreads();  // every wave is done reading the last stage
 #pragma unroll
@@ -927,6 +963,7 @@ bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode) {
   if (elem != DI_F16 || b_mode != B_NK || !g.b_vec_ok) return false;
   if (g.a_bytes == 0 || g.a2_bytes == 0 || g.b_bytes == 0) return false;  // extents unknown
   const bool single = g.c1 == 0xffffffffu || g.a2 == g.a;
+  if (g.K % 64 != 0) return false;  // whole 64-element stages (no per-lane k bound)
   if (a_mode == A_DENSE) return g.a_vec_ok && single;
   if (a_mode == A_CONV_NHWC) return g.Cin % 64 == 0 && (single || g.c1 % 64 == 0) && (g.up == 1 || g.up == 2);
   return false;
