@@ -221,7 +221,8 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   sa.Sq = HW;
   sa.Skv = HW;
   sa.scale_log2 = scale_log2;
-  launch_attention(sa, s.B, c->stream);
+  rc = run_attention(c, sa, s.B);
+  if (rc) return rc;
   rc = linear_f16(c, a.h(), C, rows, C, w.o1_w, C, w.o1_b, ACT_NONE, h.h(), C, h.h(), C);
   if (rc) return rc;
   // cross-attention
@@ -247,7 +248,8 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   ca.Sq = HW;
   ca.Skv = s.Sctx;
   ca.scale_log2 = scale_log2;
-  launch_attention(ca, s.B, c->stream);
+  rc = run_attention(c, ca, s.B);
+  if (rc) return rc;
   rc = linear_f16(c, a.h(), C, rows, C, w.o2_w, C, w.o2_b, ACT_NONE, h.h(), C, h.h(), C);
   if (rc) return rc;
   // GEGLU feed-forward

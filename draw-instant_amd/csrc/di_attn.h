@@ -21,8 +21,22 @@ struct AttnArgs {
   uint64_t bq = 0, bk = 0, bv = 0, bo = 0;      // batch stride
   uint32_t H = 1, Sq = 0, Skv = 0;
   float scale_log2 = 0.0f;  // softmax scale * log2(e)
+  // key-range split (set by run_attention): workspace of `splits` x rows
+  // normalised fp16 outputs [rows][64] and (max, row sum) float pairs, where
+  // rows = B * H * Sq enumerates (b, h, q) with q fastest
+  uint32_t splits = 1;
+  uint64_t rows = 0;
+  f16* part_o = nullptr;
+  float* part_ml = nullptr;
 };
 
+struct Ctx;
+
+// Picks the split, takes the workspace from the context's pool and enqueues
+// the attention (and, when split, the merge) on the context's stream.
+int run_attention(Ctx* c, AttnArgs a, uint32_t B);
+uint32_t attn_splits(const Ctx* c, uint32_t B, uint32_t H, uint32_t Sq, uint32_t Skv);
+// Enqueue with a.splits / a.rows / workspace already set.
 void launch_attention(const AttnArgs& a, uint32_t B, hipStream_t s);
 
 }  // namespace di

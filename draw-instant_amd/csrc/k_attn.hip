@@ -4,176 +4,368 @@
 // Computes softmax(Q K^T * scale) V per (batch, head) - the maths of
 // WGSL_FUSED_ATTN (fused-attn.js:199-307) and the cross-attention kernel
 // WGSL_FUSED (fused-cross-attn.js:112-173) - without materialising scores:
-// online softmax over 64-key tiles (running max m, sum l, rescaled O), in
-// the exp2 domain with scale*log2(e) folded into one multiply.
+// online softmax over 64-key tiles in the exp2 domain.
 //
 // MFMA mapping (v_mfma_f32_16x16x32_f16), one wavefront = 16 queries:
-//  * S^T = K Q^T: A = K tile rows (keys) from LDS, B = Q^T kept in registers.
-//    The C layout leaves lane l with query r = l%16 and keys 4g..4g+3
-//    (g = l/16) of each 16-key tile;
-//  * O^T += V^T P^T: those 8 probabilities of two adjacent key tiles are
-//    exactly one B fragment of P^T if the k index of the PV product runs over
-//    keys in the order {4g..4g+3, 16+4g..16+4g+3} per 32-key block.  V is
-//    staged in LDS transposed ([d][slot]) in that same slot order, so the PV
-//    product needs no shuffles of P and reads V^T as 16-byte fragments.
-// Each workgroup (4 wavefronts = 64 queries) shares double-buffered K / V^T
-// tiles in LDS, the next tile prefetched into registers during the MFMAs.
-// Keys past Skv (cross-attention's 77) are masked to -inf.
+//  * S^T = K Q'^T: A = K tile rows (keys) from LDS, B = Q'^T in registers,
+//    where Q' = Q * scale * log2(e) (rounded to fp16 once), so scores come
+//    out in log2 units.  The accumulator starts at -m (the running row max),
+//    so the MFMA itself subtracts the max and p = exp2(S') is one
+//    instruction per score.  The C layout leaves lane l with query l%16 and
+//    keys 4g..4g+3 (g = l/16) of each 16-key tile;
+//  * O^T += V^T P^T: those 8 probabilities of two adjacent key tiles are one
+//    B fragment of P^T when the PV product's k index runs over keys in the
+//    order {4g..4g+3, 16+4g..16+4g+3} per 32-key block.  V stays row-major in
+//    LDS; ds_read_b64_tr_b16 gathers the V^T A fragment in that key order.
+//
+// VALU and MFMA work of one SIMD do not overlap on gfx950 (measured), so the
+// softmax is kept to the minimum per score: one max (3-input), one exp2, one
+// add, half a convert.  The running max is raised only when some row's tile
+// max exceeds it by more than kRescale (p <= 2^kRescale in between), and the
+// row sums are reduced across the 4 lanes of a query once, at the end.
+//
+// Each workgroup (4 wavefronts = 64 queries) shares double-buffered K / V
+// tiles in LDS (XOR-swizzled 16-byte chunks, conflict-free for the K
+// fragment reads and the transposed V reads; 32 KiB per workgroup, four
+// resident per CU); the next tile is loaded into registers during the
+// MFMAs, by buffer loads whose descriptor ends at the head's last key.  Keys
+// past Skv (cross-attention's 77) read as zeros and are masked to -inf.
+//
+// KV split: a wave of 16 queries that walks all keys is the smallest unit of
+// work, and 64x64-latent self-attention has 1280 of them for 1024 SIMDs, so
+// some SIMDs would run two while most run one.  The keys are therefore split
+// into `splits` ranges (attn_splits picks it so the whole grid is resident
+// at once, four workgroups per CU); each workgroup writes its range's output normalised by
+// its own row sum (fp16) plus that row sum and max, and k_attn_combine merges
+// the ranges: O = sum_s l_s 2^(m_s - M) O_s / sum_s l_s 2^(m_s - M).  Workgroups are numbered so
+// that each XCD (blocks are dealt round-robin over the 8 XCDs) gets a
+// contiguous range of work, i.e. at most two heads' K / V in its L2.
 #include "di_attn.h"
 #include "di_device.h"
 #include "di_kernels.h"
+
+#include <cstdlib>
+#include <type_traits>
 
 namespace di {
 
 namespace {
 
-constexpr int D = 64;       // head dim
-constexpr int BKV = 64;     // keys per tile
-constexpr int LDS_ROW = 72; // padded row (elements)
+constexpr int D = 64;              // head dim
+constexpr int BKV = 64;            // keys per tile
+constexpr int K_BYTES = BKV * D * 2;      // 128-byte rows, XOR-swizzled 16-byte chunks
+constexpr int BUF_BYTES = 2 * K_BYTES;    // K tile, then V tile
+constexpr float kRescale = 8.0f;   // log2 units
 
-__device__ __forceinline__ uint32_t v_slot(uint32_t kk) {
-  const uint32_t block = kk >> 5, w = kk & 31, t = w >> 4, rr = w & 15;
-  return block * 32 + (rr >> 2) * 8 + (rr & 3) + 4 * t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <int N>
+using Int = std::integral_constant<int, N>;
+
+// byte offset of 16-byte chunk c of K row r: chunk index XOR (r/2)%8, so the
+// 16 rows read by one 16-lane pass of a fragment load hit distinct banks
+__device__ __forceinline__ uint32_t k_off(uint32_t r, uint32_t c) {
+  return r * 128u + ((c ^ ((r >> 1) & 7u)) << 4);
+}
+// V rows: chunk index XOR r%8.  One 32-lane pass of a transposed read covers
+// 8 consecutive rows x 2 adjacent chunks (2dt, 2dt+1); the XOR spreads those
+// 16 chunk reads over all 64 banks.
+__device__ __forceinline__ uint32_t v_off(uint32_t r, uint32_t c) {
+  return r * 128u + ((c ^ (r & 7u)) << 4);
 }
 
-__global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) f16 sK[2][BKV * LDS_ROW];
-  __shared__ __attribute__((aligned(16))) f16 sV[2][D * LDS_ROW];
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  // raw buffer, stride 0; dword3 0x00020000 is the gfx9-family data format
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ f16x8 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, g = lane >> 4;
-  const uint32_t b = blockIdx.z, h = blockIdx.y;
-  const uint32_t q0 = blockIdx.x * 64 + wave * 16;
+// lanes l, l^16, l^32, l^48 hold the same query
+__device__ __forceinline__ float max_q4(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_q4(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * BUF_BYTES];  // [buf][K | V]
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t r = lane & 15, g = lane >> 4;
+
+  // XCD-aware numbering: block i runs on XCD i % 8; give XCD x the x-th
+  // contiguous slice of the work list (slices differ by at most one block)
+  const uint32_t T = gridDim.x, bid = blockIdx.x, xcd = bid & 7u, idx = bid >> 3;
+  const uint32_t per = T >> 3, extra = T & 7u;
+  const uint32_t w = xcd < extra ? xcd * (per + 1) + idx : extra * (per + 1) + (xcd - extra) * per + idx;
+  const uint32_t qb = w % nqb, rest = w / nqb, split = rest % a.splits, hb = rest / a.splits;
+  const uint32_t h = hb % a.H, b = hb / a.H;
+
   const f16* Q = a.q + b * a.bq + h * a.hq;
   const f16* K = a.k + b * a.bk + h * a.hk;
   const f16* V = a.v + b * a.bv + h * a.hv;
   f16* O = a.o + b * a.bo + h * a.ho;
 
-  // Q^T fragments for the two 32-wide d steps
+  // Q'^T fragments for the two 32-wide d steps
+  const uint32_t qrow = qb * 64 + wave * 16 + r;
   f16x8 qf[2];
-  const uint32_t qrow = q0 + r;
 #pragma unroll
   for (int ks = 0; ks < 2; ks++) {
-    if (qrow < a.Sq) qf[ks] = *(const f16x8*)(Q + (uint64_t)qrow * a.ldq + ks * 32 + g * 8);
-    else
+    f16x8 t = {};
+    if (qrow < a.Sq) t = *(const f16x8*)(Q + (uint64_t)qrow * a.ldq + ks * 32 + g * 8);
 #pragma unroll
-      for (int j = 0; j < 8; j++) qf[ks][j] = (f16)0.0f;
+    for (int j = 0; j < 8; j++) qf[ks][j] = (f16)((float)t[j] * a.scale_log2);
   }
 
+  // K / V tile loads: thread tid moves 16-byte chunk tid%8 of rows tid/8 and
+  // tid/8 + 32.  The buffer descriptor of tile t starts at key 64t and ends
+  // after the head's last key, so rows past Skv read as zeros.
+  const uint32_t ld_row = tid >> 3, ld_c = tid & 7;
+  const uint32_t kvo0 = ld_row * (uint32_t)a.ldk * 2u + ld_c * 16u;
+  const uint32_t kvo1 = (ld_row + 32) * (uint32_t)a.ldk * 2u + ld_c * 16u;
+  const uint32_t vvo0 = ld_row * (uint32_t)a.ldv * 2u + ld_c * 16u;
+  const uint32_t vvo1 = (ld_row + 32) * (uint32_t)a.ldv * 2u + ld_c * 16u;
+  const uint32_t k_st = k_off(ld_row, ld_c), v_st = v_off(ld_row, ld_c);
   f16x8 rk[2], rv[2];
   auto load_kv = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t vi = tid + i * 256, kk = vi >> 3, dc = vi & 7;
-      const uint32_t key = t * BKV + kk;
-      if (key < a.Skv) {
-        rk[i] = *(const f16x8*)(K + (uint64_t)key * a.ldk + dc * 8);
-        rv[i] = *(const f16x8*)(V + (uint64_t)key * a.ldv + dc * 8);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++) rk[i][j] = rv[i][j] = (f16)0.0f;
-      }
-    }
+    const uint32_t key0 = (uint32_t)t * BKV, left = a.Skv - key0;
+    const __amdgpu_buffer_rsrc_t rK =
+        make_rsrc(K + (uint64_t)key0 * a.ldk, (left - 1) * (uint32_t)a.ldk * 2u + D * 2);
+    const __amdgpu_buffer_rsrc_t rV =
+        make_rsrc(V + (uint64_t)key0 * a.ldv, (left - 1) * (uint32_t)a.ldv * 2u + D * 2);
+    rk[0] = buf_load16(rK, kvo0);
+    rk[1] = buf_load16(rK, kvo1);
+    rv[0] = buf_load16(rV, vvo0);
+    rv[1] = buf_load16(rV, vvo1);
   };
-  auto store_kv = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t vi = tid + i * 256, kk = vi >> 3, dc = vi & 7;
-      *(f16x8*)&sK[buf][kk * LDS_ROW + dc * 8] = rk[i];
-      const uint32_t slot = v_slot(kk);
-#pragma unroll
-      for (int j = 0; j < 8; j++) sV[buf][(dc * 8 + j) * LDS_ROW + slot] = rv[i][j];
-    }
+  auto store_kv = [&](auto buf_c) {
+    unsigned char* base = smem + decltype(buf_c)::value * BUF_BYTES;
+    // rows +32 keep the XOR pattern of rows 0..31
+    *(f16x8*)(base + k_st) = rk[0];
+    *(f16x8*)(base + k_st + 32 * 128) = rk[1];
+    *(f16x8*)(base + K_BYTES + v_st) = rv[0];
+    *(f16x8*)(base + K_BYTES + v_st + 32 * 128) = rv[1];
   };
 
-  float m = -INFINITY, l = 0.0f;
+  float m = 0.0f, l = 0.0f;  // running max (log2 units) and this lane's partial row sum
   f32x4 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // K fragment (kt, ks): row kt*16 + r, chunk 4ks + g
+  const uint32_t k_rd0 = k_off(r, g), k_rd1 = k_off(r, 4 + g);
+  // V^T fragment (dt, ks) by transposed reads (see the header): lane r of
+  // 16-lane group g reads 4 elements of key row 4g + r/4 (+16 for the second
+  // half, +32 per k step: multiples of 8 rows, same XOR) at columns
+  // 16dt + 4(r%4), i.e. chunk 2dt + (r%4)/2, bytes (r%2)*8 of it.
+  uint32_t v_rd[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++)
+    v_rd[dt] = K_BYTES + v_off(4 * g + (r >> 2), 2 * dt + ((r & 3) >> 1)) + (r & 1) * 8;
+
+  // this workgroup's key tiles [t0, t1)
   const int n_tiles = (int)((a.Skv + BKV - 1) / BKV);
-  load_kv(0);
-  store_kv(0);
-  __syncthreads();
-  for (int t = 0; t < n_tiles; t++) {
-    const int cur = t & 1;
-    if (t + 1 < n_tiles) load_kv(t + 1);
-    // scores S^T for 4 key tiles of 16
+  const int tps = (n_tiles + (int)a.splits - 1) / (int)a.splits;
+  const int t0 = (int)split * tps, t1 = min(t0 + tps, n_tiles);
+
+  auto tile = [&](auto cur_c, int t) {
+    constexpr int cur = decltype(cur_c)::value;
+    const unsigned char* sb = smem + cur * BUF_BYTES;
+    const bool more = t + 1 < t1;
+    if (more) load_kv(t + 1);
+
+    // S' = K Q'^T - m
+    const f32x4 cinit = {-m, -m, -m, -m};
     f32x4 s[4];
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
-      s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        f16x8 kf = *(const f16x8*)&sK[cur][(kt * 16 + r) * LDS_ROW + ks * 32 + g * 8];
-        s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s[kt], 0, 0, 0);
-      }
+      const f16x8 k0 = *(const f16x8*)(sb + k_rd0 + kt * 2048);
+      const f16x8 k1 = *(const f16x8*)(sb + k_rd1 + kt * 2048);
+      s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qf[0], cinit, 0, 0, 0);
+      s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qf[1], s[kt], 0, 0, 0);
     }
-    // online softmax (exp2 domain); lanes r, r+16, r+32, r+48 share a query
-    float mx = -INFINITY;
+    if ((uint32_t)(t + 1) * BKV > a.Skv) {
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if ((uint32_t)(t * BKV + kt * 16 + 4 * g + i) >= a.Skv) s[kt][i] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+    for (int kt = 1; kt < 4; kt++)
+      mx = fmaxf(fmaxf(mx, fmaxf(s[kt][0], s[kt][1])), fmaxf(s[kt][2], s[kt][3]));
+    mx = max_q4(mx);
+    // raise the running max on the first tile, or when a row's scores exceed
+    // it by more than kRescale (wave-uniform branch)
+    if (t == t0 || __builtin_amdgcn_ballot_w64(mx > kRescale) != 0) {
+      const float dl = t == t0 ? mx : fmaxf(mx, 0.0f);
+      m += dl;
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++) s[kt] -= dl;
+      // dl >= 0 after the first tile; on the first, o and l are still zero
+      const float alpha = t == t0 ? 0.0f : __builtin_amdgcn_exp2f(-dl);
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+    }
+    f16x8 pf[2];
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const uint32_t key = t * BKV + kt * 16 + g * 4 + i;
-        float v = key < a.Skv ? s[kt][i] * a.scale_log2 : -INFINITY;
-        s[kt][i] = v;
-        mx = fmaxf(mx, v);
+        const float p = __builtin_amdgcn_exp2f(s[kt][i]);
+        l += p;
+        pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-    float rs = 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float p = __builtin_amdgcn_exp2f(s[kt][i] - m_new);
-        s[kt][i] = p;
-        rs += p;
-      }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
-    l = l * alpha + rs;
-    m = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
     // O^T += V^T P^T over two 32-key k steps
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      f16x8 pf;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        pf[j] = (f16)s[2 * ks][j];
-        pf[j + 4] = (f16)s[2 * ks + 1][j];
-      }
 #pragma unroll
       for (int dt = 0; dt < 4; dt++) {
-        f16x8 vf = *(const f16x8*)&sV[cur][(dt * 16 + r) * LDS_ROW + ks * 32 + g * 8];
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
+        const unsigned char* vp = sb + v_rd[dt] + ks * 32 * 128;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)vp);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vp + 16 * 128));
+        const f16x8 vf = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[ks], o[dt], 0, 0, 0);
       }
     }
-    if (t + 1 < n_tiles) store_kv(cur ^ 1);
+    if (more) store_kv(Int<cur ^ 1>{});
     __syncthreads();
+  };
+
+  load_kv(t0);
+  store_kv(Int<0>{});
+  __syncthreads();
+  // two tiles per iteration so each LDS buffer has fixed offsets
+  for (int t = t0; t < t1; t += 2) {
+    tile(Int<0>{}, t);
+    if (t + 1 < t1) tile(Int<1>{}, t + 1);
   }
+  l = sum_q4(l);
   if (qrow < a.Sq) {
     const float inv = 1.0f / l;
+    f16* dst = O + (uint64_t)qrow * a.ldo;
+    if (a.splits > 1) {
+      // this key range's normalised output and (max, row sum), per row
+      // (b, h, q) of the [splits][B*H*Sq] workspace
+      const uint64_t prow = ((uint64_t)split * a.rows + (uint64_t)hb * a.Sq + qrow);
+      dst = a.part_o + prow * D;
+      if (g == 0) *(float2*)(a.part_ml + prow * 2) = float2{m, l};
+    }
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
       f16x4 ov;
 #pragma unroll
       for (int i = 0; i < 4; i++) ov[i] = (f16)(o[dt][i] * inv);
-      *(f16x4*)(O + (uint64_t)qrow * a.ldo + dt * 16 + g * 4) = ov;
+      *(f16x4*)(dst + dt * 16 + g * 4) = ov;
     }
   }
 }
 
+// Merge the key ranges of a split launch: one thread per 8 outputs (a
+// 16-byte chunk) of a (b, h, q) row; all SP ranges are loaded up front.
+template <int SP>
+__global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x, row = i >> 3, c = i & 7;
+  if (row >= a.rows) return;
+  float2 ml[SP];
+  f16x8 v[SP];
+#pragma unroll
+  for (int sp = 0; sp < SP; sp++) {
+    const uint64_t prow = (uint64_t)sp * a.rows + row;
+    ml[sp] = *(const float2*)(a.part_ml + prow * 2);
+    v[sp] = *(const f16x8*)(a.part_o + prow * D + c * 8);
+  }
+  float mx = ml[0].x;
+#pragma unroll
+  for (int sp = 1; sp < SP; sp++) mx = fmaxf(mx, ml[sp].x);
+  float wsum = 0.0f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sp = 0; sp < SP; sp++) {
+    const float w = ml[sp].y * __builtin_amdgcn_exp2f(ml[sp].x - mx);
+    wsum += w;
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] += w * (float)v[sp][j];
+  }
+  const float inv = 1.0f / wsum;
+  const uint32_t q = row % a.Sq, hb = row / a.Sq, h = hb % a.H, b = hb / a.H;
+  f16x8 out;
+#pragma unroll
+  for (int j = 0; j < 8; j++) out[j] = (f16)(acc[j] * inv);
+  *(f16x8*)(a.o + b * a.bo + h * a.ho + (uint64_t)q * a.ldo + c * 8) = out;
+}
+
 }  // namespace
 
+constexpr uint32_t kMaxSplits = 8;
+
+uint32_t attn_splits(const Ctx* c, uint32_t B, uint32_t H, uint32_t Sq, uint32_t Skv) {
+  // Largest split that keeps the grid resident at once and every range >= 16
+  // key tiles (shorter ranges lose more to the merge than they gain).  A CU's 160 KiB of LDS holds workgroups in two 80 KiB halves
+  // (measured: 32 KiB workgroups reside 4 per CU, not 5), so the budget is
+  // 4 workgroups per CU.
+  const uint32_t blocks = ((Sq + 63) / 64) * H * B, cap = 4u * (uint32_t)c->num_cus;
+  const uint32_t n_tiles = (Skv + BKV - 1) / BKV;
+  uint32_t sp = blocks ? cap / blocks : 1;
+  sp = sp < n_tiles / 16 ? sp : n_tiles / 16;
+  sp = sp < kMaxSplits ? sp : kMaxSplits;
+  if (sp < 2) return 1;
+  // ranges of tps = ceil(n_tiles / sp) tiles: drop the ones that would be empty
+  const uint32_t tps = (n_tiles + sp - 1) / sp;
+  return (n_tiles + tps - 1) / tps;
+}
+
 void launch_attention(const AttnArgs& a, uint32_t B, hipStream_t s) {
-  dim3 grid((a.Sq + 63) / 64, a.H, B);
-  k_flash_attn<<<grid, 256, 0, s>>>(a);
+  const uint32_t nqb = (a.Sq + 63) / 64;
+  k_flash_attn<<<dim3(nqb * a.H * B * a.splits), 256, 0, s>>>(a, nqb);
+  const dim3 cg((uint32_t)((a.rows * 8 + 255) / 256));
+  switch (a.splits) {
+    case 1: break;
+    case 2: k_attn_combine<2><<<cg, 256, 0, s>>>(a); break;
+    case 3: k_attn_combine<3><<<cg, 256, 0, s>>>(a); break;
+    case 4: k_attn_combine<4><<<cg, 256, 0, s>>>(a); break;
+    case 5: k_attn_combine<5><<<cg, 256, 0, s>>>(a); break;
+    case 6: k_attn_combine<6><<<cg, 256, 0, s>>>(a); break;
+    case 7: k_attn_combine<7><<<cg, 256, 0, s>>>(a); break;
+    default: k_attn_combine<8><<<cg, 256, 0, s>>>(a); break;
+  }
+}
+
+int run_attention(Ctx* c, AttnArgs a, uint32_t B) {
+  a.splits = attn_splits(c, B, a.H, a.Sq, a.Skv);
+  // tuning override: DI_ATTN_SPLITS=n (clamped so no key range is empty)
+  static const char* env_splits = getenv("DI_ATTN_SPLITS");
+  if (env_splits) {
+    const uint32_t n_tiles = (a.Skv + BKV - 1) / BKV, want = (uint32_t)atoi(env_splits);
+    uint32_t sp = want < 1 ? 1 : (want > n_tiles ? n_tiles : want);
+    sp = sp < kMaxSplits ? sp : kMaxSplits;
+    const uint32_t tps = (n_tiles + sp - 1) / sp;
+    a.splits = (n_tiles + tps - 1) / tps;
+  }
+  a.rows = (uint64_t)B * a.H * a.Sq;
+  void* ws = nullptr;
+  uint64_t cap = 0;
+  if (a.splits > 1) {
+    const uint64_t ob = a.splits * a.rows * D * 2;
+    const int rc = pool_alloc(c, ob + a.splits * a.rows * 8, &ws, &cap);
+    if (rc) return rc;
+    a.part_o = (f16*)ws;
+    a.part_ml = (float*)((char*)ws + ob);
+  }
+  launch_attention(a, B, c->stream);
+  if (ws) pool_release(c, ws, cap);
+  return DI_OK;
 }
 
 }  // namespace di
@@ -204,6 +396,9 @@ int attention_entry(di_ctx* ctx, di_handle Q, di_handle K, di_handle V, di_handl
   DI_REQUIRE(B && H && Sq && Skv, DI_EINVAL, "%s: zero dimension", fn);
   DI_REQUIRE(layout == DI_ATTN_BSHD || layout == DI_ATTN_BHSD, DI_EINVAL, "%s: bad layout %d", fn,
              layout);
+  // K / V rows of one head are addressed with 32-bit byte offsets
+  DI_REQUIRE((uint64_t)(Skv + 64) * H * d * 2 < (1ull << 31), DI_EUNSUPPORTED,
+             "%s: Skv*H = %llu too large", fn, (unsigned long long)Skv * H);
   const uint64_t nq = (uint64_t)B * H * Sq * d, nkv = (uint64_t)B * H * Skv * d;
   const size_t es = dtype_size(dt);
   DI_BUF(ctx, Q, q, nq * es);
@@ -228,7 +423,8 @@ int attention_entry(di_ctx* ctx, di_handle Q, di_handle K, di_handle V, di_handl
     a.k = (const f16*)k->ptr;
     a.v = (const f16*)v->ptr;
     a.o = (f16*)o->ptr;
-    launch_attention(a, B, ctx->stream);
+    const int rc = run_attention(ctx, a, B);
+    if (rc) return rc;
     DI_LAUNCH_CHECK();
     return DI_OK;
   }
@@ -247,8 +443,8 @@ int attention_entry(di_ctx* ctx, di_handle Q, di_handle K, di_handle V, di_handl
     a.k = (const f16*)tk;
     a.v = (const f16*)tv;
     a.o = (f16*)to;
-    launch_attention(a, B, ctx->stream);
-    launch_convert(ctx->stream, to, DI_F16, o->ptr, DI_F32, nq);
+    rc = run_attention(ctx, a, B);
+    if (!rc) launch_convert(ctx->stream, to, DI_F16, o->ptr, DI_F32, nq);
   }
   if (tq) pool_release(ctx, tq, cq);
   if (tk) pool_release(ctx, tk, ck);

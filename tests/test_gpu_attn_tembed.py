@@ -63,6 +63,8 @@ def test_attn_self_fp16(dev, rng, B, H, S, layout):
     (2, 20, 256, 77, BHSD),   # fused-cross-attn.js SHAPE
     (1, 4, 130, 1, BHSD),     # single key: output = V
     (1, 2, 64, 65, BSHD),     # one key past a tile boundary
+    (1, 2, 130, 2113, BHSD),  # key-range split: 34 tiles in 2 ranges, last tile 1 key
+    (2, 3, 200, 3100, BSHD),  # key-range split (3 ranges of 17/17/15 tiles) with batch 2
 ])
 def test_attn_cross_fp16(dev, rng, B, H, Sq, Skv, layout):
     print(f"[attn cross] B={B} H={H} Sq={Sq} Skv={Skv}", flush=True)
