@@ -18,7 +18,11 @@ enum TileCfg {
   TILE_128x128 = 3,
   TILE_128x160 = 4,
   TILE_64x160 = 5,
-  TILE_COUNT = 6
+  // eight wavefronts: two per output wave tile, splitting each stage's k steps
+  TILE_64x64_K2 = 6,
+  TILE_128x64_K2 = 7,
+  TILE_64x128_K2 = 8,
+  TILE_COUNT = 9
 };
 
 struct GemmPlan {

@@ -167,17 +167,17 @@ __device__ __forceinline__ void epi_math8(const GemmArgs& g, float* x, const f32
 // one C tile staged in LDS as fp32 sC[BM][LDC].  Split-K partials are
 // stored as fp32 vectors instead.  All operand loads of a batch of vectors
 // are issued before any is consumed.
-template <int BM, int BN, int LDC>
+template <int BM, int BN, int LDC, int NT>
 __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float* sC, uint32_t m0,
                                                   uint32_t n0, uint32_t bz, uint32_t split) {
   const int tid = threadIdx.x;
   if (g.splits > 1) {
     constexpr int VPR4 = BN / 4;
-    constexpr int NV = (BM * VPR4 + 255) / 256;
+    constexpr int NV = (BM * VPR4 + NT - 1) / NT;
     float* P = g.part + ((uint64_t)split * g.batch + bz) * (uint64_t)g.M * g.N;
 #pragma unroll
     for (int v = 0; v < NV; v++) {
-      const int idx = tid + v * 256;
+      const int idx = tid + v * NT;
       if (idx < BM * VPR4) {
         const int r = idx / VPR4, c4 = (idx % VPR4) * 4;
         const uint32_t m = m0 + r, n = n0 + c4;
@@ -192,10 +192,10 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     // 32-column groups [16 hidden | 16 gate]; a vector is 8 outputs from
     // hidden columns cl..cl+7 and gate columns cl+16..cl+23.
     constexpr int VPRG = BN / 16;
-    constexpr int NV = (BM * VPRG + 255) / 256;
+    constexpr int NV = (BM * VPRG + NT - 1) / NT;
 #pragma unroll
     for (int v = 0; v < NV; v++) {
-      const int idx = tid + v * 256;
+      const int idx = tid + v * NT;
       if (idx >= BM * VPRG) break;
       const int r = idx / VPRG, q = idx % VPRG, cl = (q >> 1) * 32 + (q & 1) * 8;
       const uint32_t m = m0 + r, nh = n0 + cl;
@@ -235,7 +235,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     return;
   }
   constexpr int VPR8 = BN / 8;
-  constexpr int NV = (BM * VPR8 + 255) / 256;
+  constexpr int NV = (BM * VPR8 + NT - 1) / NT;
   constexpr int CH = NV < 4 ? NV : 4;  // vectors per load batch
 #pragma unroll
   for (int v0 = 0; v0 < NV; v0 += CH) {
@@ -245,7 +245,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     bool okv[CH];
 #pragma unroll
     for (int u = 0; u < CH; u++) {
-      const int idx = tid + (v0 + u) * 256;
+      const int idx = tid + (v0 + u) * NT;
       const int r = idx / VPR8, c8 = (idx % VPR8) * 8;
       mm[u] = m0 + r;
       nn[u] = n0 + c8;
@@ -278,7 +278,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
 #pragma unroll
     for (int u = 0; u < CH; u++) {
       if (!okv[u]) continue;
-      const int idx = tid + (v0 + u) * 256;
+      const int idx = tid + (v0 + u) * NT;
       const int r = idx / VPR8, c8 = (idx % VPR8) * 8;
       float x[8];
       const f32x4 a0 = ld4(&sC[r * LDC + c8]), a1 = ld4(&sC[r * LDC + c8 + 4]);
@@ -297,8 +297,8 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
 }
 
 // ---- the GEMM kernel ----
-template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D, int KS>
+__global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
   using MT = Mfma<T>;
   constexpr int KV = MT::KV;
   constexpr int BK = 128 / sizeof(T);  // k elements per stage (128 bytes per row)
@@ -307,12 +307,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   // chunk position XOR-swizzled by (row >> 1) & 7: the 8 lanes writing one row
   // and the 16 lanes reading one fragment column (16 rows) hit distinct banks.
   constexpr int LDK = BK;
-  constexpr int NVA = BM * VPR / 256;  // A vectors per thread per stage
-  constexpr int NVB = BN * VPR / 256;
+  // KS = 2: eight wavefronts, two per output wave tile, each computing half
+  // of every stage's k steps (the halves are summed through LDS at the end).
+  // A lone workgroup per CU then still has two waves per SIMD, which lets
+  // LDS reads of one overlap MFMAs of the other.
+  constexpr int NT = 256 * KS;         // threads
+  constexpr int NVA = BM * VPR / NT;   // A vectors per thread per stage
+  constexpr int NVB = BN * VPR / NT;
   constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
   constexpr int TM = WM / 16, TN = WN / 16;
-  static_assert(WGM * WGN == 4, "4 wavefronts");
+  constexpr int KSTEPS = BK / MT::KM;  // MFMA k steps per stage
+  static_assert(WGM * WGN == 4, "4 wavefronts per k half");
+  static_assert(KS == 1 || (FAST && KSTEPS % KS == 0), "k halves: fast path, whole k steps");
   static_assert(NVA >= 1 && NVB >= 1 && TM >= 1 && TN >= 1, "tile too small");
+  static_assert(NVA * NT == BM * VPR && NVB * NT == BN * VPR, "whole vectors per thread");
 
   // Pipeline buffers sA[2][BM*LDK], sB[2][BN*LDK]; reused by the fp32 C tile
   // of the vector epilogue.
@@ -327,7 +335,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  const int wq = wave & 3, kh = wave >> 2;  // output wave tile, k half
+  const int wm0 = (wq / WGN) * WM, wn0 = (wq % WGN) * WN;
 
   // Tile order: N fastest, so consecutive tiles share A rows.  Workgroups are
   // dealt round-robin to the 8 XCDs (each with its own L2); remap so that
@@ -358,7 +367,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   bool a_row_ok[NVA];
 #pragma unroll
   for (int i = 0; i < NVA; i++) {
-    uint32_t r = (tid + i * 256) / VPR;
+    uint32_t r = (tid + i * NT) / VPR;
     uint32_t m = m0 + r;
     a_row_ok[i] = m < g.M;
     if constexpr (AM == A_DENSE) {
@@ -400,7 +409,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   if constexpr (FAST) {
 #pragma unroll
     for (int i = 0; i < NVA; i++) {
-      const uint32_t m = m0 + (tid + i * 256) / VPR;
+      const uint32_t m = m0 + (tid + i * NT) / VPR;
       // row base + this thread's k chunk at k_begin; stages add a scalar offset
       fa1[i] = m < g.M ? m * (uint32_t)g.lda * 2u + (k_begin + kc * KV) * 2u : kInv;
       fa2[i] = m < g.M ? m * (uint32_t)g.lda2 * 2u : kInv;
@@ -408,7 +417,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
-      const uint32_t n = n0 + (tid + i * 256) / VPR;
+      const uint32_t n = n0 + (tid + i * NT) / VPR;
       fb[i] = n < g.N ? n * (uint32_t)g.ldb * 2u + (k_begin + kc * KV) * 2u : kInv;
     }
     if constexpr (AM == A_CONV_NHWC) {
@@ -490,7 +499,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     for (int i = 0; i < NVB; i++) {
       typename MT::vec v = zero_vec<T>();
       if constexpr (BMD == B_NK) {
-        uint32_t r = (tid + i * 256) / VPR;
+        uint32_t r = (tid + i * NT) / VPR;
         uint32_t n = n0 + r, k = kbase + kc * KV;
         if (n < g.N) {
           if (b_fast && k + KV <= k_end) {
@@ -503,7 +512,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         }
       } else {  // B_KN: vector along n at fixed k; transposed into LDS at store
         constexpr int VPK = BN / KV;  // vectors per k row
-        uint32_t kr = (tid + i * 256) / VPK, nc = (tid + i * 256) % VPK;
+        uint32_t kr = (tid + i * NT) / VPK, nc = (tid + i * NT) % VPK;
         uint32_t k = kbase + kr, n = n0 + nc * KV;
         if (k < k_end) {
           if (b_fast && n + KV <= g.N) {
@@ -522,17 +531,17 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   auto store_stage = [&](int buf, const Stage& st) {
 #pragma unroll
     for (int i = 0; i < NVA; i++) {
-      uint32_t r = (tid + i * 256) / VPR;
+      uint32_t r = (tid + i * NT) / VPR;
       *(typename MT::vec*)&sA[buf][lds_at(r, kc * KV)] = st.a[i];
     }
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
       if constexpr (BMD == B_NK) {
-        uint32_t r = (tid + i * 256) / VPR;
+        uint32_t r = (tid + i * NT) / VPR;
         *(typename MT::vec*)&sB[buf][lds_at(r, kc * KV)] = st.b[i];
       } else {
         constexpr int VPK = BN / KV;
-        uint32_t kr = (tid + i * 256) / VPK, nc = (tid + i * 256) % VPK;
+        uint32_t kr = (tid + i * NT) / VPK, nc = (tid + i * NT) % VPK;
 #pragma unroll
         for (int j = 0; j < KV; j++) sB[buf][lds_at(nc * KV + j, kr)] = st.b[i][j];
       }
@@ -548,7 +557,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   const int fr = lane & 15, fk = (lane >> 4) * MT::FK;
   auto compute = [&](int buf) {
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += MT::KM) {
+    for (int ks = 0; ks < KSTEPS / KS; ks++) {
+      const int kk = (kh * (KSTEPS / KS) + ks) * MT::KM;
       typename MT::frag af[TM], bf[TN];
 #pragma unroll
       for (int a = 0; a < TM; a++) af[a] = ld_frag<T>(&sA[buf][lds_at(wm0 + a * 16 + fr, kk + fk)]);
@@ -680,6 +690,32 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
       static_assert(BM * LDC * 4 <= (int)sizeof(smem), "C tile fits the LDS allocation");
       float* sC = reinterpret_cast<float*>(smem);
       __syncthreads();  // every wave is done reading the last stage
+      // k half 0 writes the C tile, k half 1 (same positions) adds to it
+#pragma unroll
+      for (int h = 0; h < KS; h++) {
+        if (kh == h) {
+#pragma unroll
+          for (int a = 0; a < TM; a++)
+#pragma unroll
+            for (int b = 0; b < TN; b++)
+#pragma unroll
+              for (int i = 0; i < 4; i++) {
+                float& c = sC[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr];
+                c = h == 0 ? acc[a][b][i] : c + acc[a][b][i];
+              }
+        }
+        __syncthreads();
+      }
+      gemm_epilogue_vec<BM, BN, LDC, NT>(g, sC, m0, n0, bz, split);
+      return;
+    }
+  }
+  if constexpr (KS > 1) {
+    // k half 1 hands its sums to half 0 through LDS; half 0 runs the epilogue
+    constexpr int LDC = BN + 4;
+    float* sC = reinterpret_cast<float*>(smem);
+    __syncthreads();
+    if (kh == 1) {
 #pragma unroll
       for (int a = 0; a < TM; a++)
 #pragma unroll
@@ -687,10 +723,15 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
           for (int i = 0; i < 4; i++)
             sC[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr] = acc[a][b][i];
-      __syncthreads();
-      gemm_epilogue_vec<BM, BN, LDC>(g, sC, m0, n0, bz, split);
-      return;
     }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int a = 0; a < TM; a++)
+#pragma unroll
+      for (int b = 0; b < TN; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[a][b][i] += sC[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr];
   }
   if (splits > 1) {
     float* P = g.part + ((uint64_t)split * g.batch + bz) * (uint64_t)g.M * g.N;
@@ -846,17 +887,20 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
   }
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D = 2>
+template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D = 2,
+          int KS = 1>
 void launch_cfg(const GemmArgs& g, hipStream_t s) {
   uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D><<<dim3(tiles, 1, g.batch * g.splits), 256, 0, s>>>(g);
+  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D, KS>
+      <<<dim3(tiles, 1, g.batch * g.splits), 256 * KS, 0, s>>>(g);
 }
 
 // Generic (bounds-checked) variants: two tile shapes.
 template <typename T, int AM, int BMD>
 void launch_slow(const GemmArgs& g, int tile_cfg, hipStream_t s) {
   if (tile_cfg == TILE_64x64 || tile_cfg == TILE_128x64 || tile_cfg == TILE_64x128 ||
-      tile_cfg == TILE_64x160)
+      tile_cfg == TILE_64x160 || tile_cfg == TILE_64x64_K2 || tile_cfg == TILE_128x64_K2 ||
+      tile_cfg == TILE_64x128_K2)
     launch_cfg<T, 64, 64, 2, 2, AM, BMD, false>(g, s);
   else
     launch_cfg<T, 128, 128, 2, 2, AM, BMD, false>(g, s);
@@ -870,6 +914,9 @@ void launch_fast_d(const GemmArgs& g, int tile_cfg, hipStream_t s) {
     case TILE_128x64: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D>(g, s); break;
     case TILE_64x160: launch_cfg<f16, 64, 160, 2, 2, AM, B_NK, true, D>(g, s); break;
     case TILE_64x128: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D>(g, s); break;
+    case TILE_64x64_K2: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D, 2>(g, s); break;
+    case TILE_128x64_K2: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D, 2>(g, s); break;
+    case TILE_64x128_K2: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D, 2>(g, s); break;
     default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D>(g, s); break;
   }
 }
@@ -879,11 +926,41 @@ void launch_fast(const GemmArgs& g, int tile_cfg, int depth, hipStream_t s) {
   else launch_fast_d<AM, 2>(g, tile_cfg, s);
 }
 
-const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64};
-const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160};
+const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64, 64, 128, 64};
+const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160, 64, 64, 128};
 // Relative per-CU MFMA efficiency of each tile shape (the 2x2 wavefront tile
 // sets LDS bytes per MFMA cycle); tuned by measurement.
-const double kTileEff[TILE_COUNT] = {0.35, 0.5, 0.5, 0.8, 0.85, 0.55};
+const double kTileEff[TILE_COUNT] = {0.35, 0.5, 0.5, 0.8, 0.85, 0.55, 0.35, 0.5, 0.5};
+
+}  // namespace
+
+namespace {
+
+// Measured plans for the U-Net step's GEMM shapes (gemm_tune.py); other
+// shapes use the cost model below.
+struct TunedPlan {
+  uint32_t M, N, K, conv, ks, stride, up, geglu;
+  int tile;
+  uint32_t splits;
+};
+const TunedPlan kTuned[] = {
+#include "gemm_tuned.inc"
+    {0, 0, 0, 0, 0, 0, 0, 0, TILE_64x64, 1},  // end
+};
+
+bool tuned_plan(const GemmArgs& g, GemmPlan* out) {
+  const uint32_t conv = g.Cin > 0 ? 1 : 0;
+  const uint32_t ks = conv ? g.ks : 0, stride = conv ? g.stride : 0, up = conv ? g.up : 0;
+  const uint32_t geglu = g.act == ACT_GEGLU ? 1 : 0;
+  for (const TunedPlan& t : kTuned) {
+    if (t.M == g.M && t.N == g.N && t.K == g.K && t.conv == conv && t.ks == ks &&
+        t.stride == stride && t.up == up && t.geglu == geglu && t.M != 0) {
+      *out = GemmPlan{t.tile, t.splits};
+      return true;
+    }
+  }
+  return false;
+}
 
 }  // namespace
 
@@ -891,6 +968,12 @@ GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
   const char* env_tile = getenv("DI_GEMM_TILE");
   const char* env_split = getenv("DI_GEMM_SPLITS");
   GemmPlan best{TILE_64x64, 1};
+  if (elem == DI_F16 && tuned_plan(g, &best)) {
+    if (env_tile) best.tile = atoi(env_tile);
+    if (env_split) best.splits = (uint32_t)atoi(env_split);
+    if (best.splits < 1) best.splits = 1;
+    return best;
+  }
   if (elem == DI_F32) {
     uint64_t t = (uint64_t)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
     best.tile = t >= (uint64_t)num_cus / 2 ? TILE_128x128 : TILE_64x64;
@@ -983,7 +1066,7 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
     g.a2_bytes = g.a_bytes;
     if (g.c1 == 0) g.c1 = 0xffffffffu;
   }
-  static const bool trace = getenv("DI_TRACE_GEMM") != nullptr;
+  const bool trace = getenv("DI_TRACE_GEMM") != nullptr;
   if (trace)
     fprintf(stderr,
             "[di_gemm] M=%u N=%u K=%u batch=%u amode=%d bmode=%d elem=%d cin=%u hw=%ux%u ks=%u "
@@ -1006,7 +1089,7 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
   if (fast) {
     // ring depth 2 measured as fast as 4 at U-Net shapes (short K); 4 is kept
     // for tuning (DI_GEMM_DEPTH=4)
-    static const char* env_depth = getenv("DI_GEMM_DEPTH");
+    const char* env_depth = getenv("DI_GEMM_DEPTH");
     const int depth = env_depth ? atoi(env_depth) : 2;
     if (a_mode == A_DENSE) launch_fast<A_DENSE>(g, tile_cfg, depth, s);
     else launch_fast<A_CONV_NHWC>(g, tile_cfg, depth, s);

@@ -189,7 +189,7 @@ def test_linear_fp16_every_plan(dev, rng, monkeypatch, M, N, K, act, res):
         ref = full
     if res:
         ref = ref + r.astype(np.float32)
-    for tile in (0, 1, 2, 3, 5):
+    for tile in (0, 1, 2, 3, 5, 6, 7, 8):
         for splits in (1, 2, 3):
             monkeypatch.setenv("DI_GEMM_TILE", str(tile))
             monkeypatch.setenv("DI_GEMM_SPLITS", str(splits))
@@ -244,6 +244,17 @@ def _conv_case(dev, rng, n, cin, cout, h, w, k, s, pad, up=1, res=False, cin_pad
 def test_conv_nhwc_fp16(dev, rng, n, cin, cout, h, w, k, s, pad, up, res):
     print(f"[conv f16] n={n} cin={cin} cout={cout} {h}x{w} k={k} s={s} up={up}", flush=True)
     assert _conv_case(dev, rng, n, cin, cout, h, w, k, s, pad, up, res) <= 2e-3
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 5, 6, 7, 8])
+def test_conv_nhwc_fp16_every_tile(dev, rng, monkeypatch, tile):
+    """conv3x3 (implicit GEMM, buffer-load path) with every tile shape forced,
+    including the eight-wavefront k-half variants, split-K 1 and 2."""
+    for splits in (1, 2):
+        monkeypatch.setenv("DI_GEMM_TILE", str(tile))
+        monkeypatch.setenv("DI_GEMM_SPLITS", str(splits))
+        print(f"[conv tile] tile={tile} splits={splits}", flush=True)
+        assert _conv_case(dev, rng, 1, 128, 192, 12, 12, 3, 1, 1, res=True) <= 2e-3
 
 
 def test_conv_nchw_f32_via_f16_compute_cfg2(dev, rng):
