@@ -195,7 +195,7 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   if (!rc) rc = n.alloc(c, rows * C * 2);
   if (!rc) rc = qkv.alloc(c, rows * 3 * C * 2);
   if (!rc) rc = a.alloc(c, rows * C * 2);
-  if (!rc) rc = kv.alloc(c, (uint64_t)s.B * s.Sctx * 2 * C * 2);
+  if (!rc && !w.kv_pre) rc = kv.alloc(c, (uint64_t)s.B * s.Sctx * 2 * C * 2);
   if (!rc) rc = gg.alloc(c, rows * 4 * C * 2);
   if (rc) return rc;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
@@ -228,21 +228,25 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   // cross-attention
   launch_layer_norm(c->stream, h.h(), w.ln2_g, w.ln2_b, n.h(), rows, C, s.ln_eps, DI_F16);
   rc = linear_f16(c, n.h(), C, rows, C, w.q2_w, C, nullptr, ACT_NONE, nullptr, 0, qkv.h(), C);
-  if (!rc)
+  const f16* kvp = w.kv_pre;
+  const uint64_t kvld = w.kv_pre ? w.kv_ld : 2 * C;
+  if (!rc && !kvp) {
     rc = linear_f16(c, context, s.cross, (uint64_t)s.B * s.Sctx, s.cross, w.kv2_w, 2 * C, nullptr,
                     ACT_NONE, nullptr, 0, kv.h(), 2 * C);
+    kvp = kv.h();
+  }
   if (rc) return rc;
   AttnArgs ca;
   ca.q = qkv.h();
-  ca.k = kv.h();
-  ca.v = kv.h() + C;
+  ca.k = kvp;
+  ca.v = kvp + C;
   ca.o = a.h();
   ca.ldq = C;
-  ca.ldk = ca.ldv = 2 * C;
+  ca.ldk = ca.ldv = kvld;
   ca.ldo = C;
   ca.hq = ca.hk = ca.hv = ca.ho = 64;
   ca.bq = (uint64_t)HW * C;
-  ca.bk = ca.bv = (uint64_t)s.Sctx * 2 * C;
+  ca.bk = ca.bv = (uint64_t)s.Sctx * kvld;
   ca.bo = (uint64_t)HW * C;
   ca.H = C / 64;
   ca.Sq = HW;

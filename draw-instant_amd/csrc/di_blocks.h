@@ -78,6 +78,10 @@ struct TransformerW {
   const float *ln2_g = nullptr, *ln2_b = nullptr;
   const f16* q2_w = nullptr;   // attn2.to_q [C][C]
   const f16* kv2_w = nullptr;  // [2C][cross] = to_k ; to_v
+  // Optional: attn2 K / V already projected (rows [b*Sctx + s], K at columns
+  // [0, C), V at [C, 2C), row stride kv_ld); kv2_w is then unused.
+  const f16* kv_pre = nullptr;
+  uint64_t kv_ld = 0;
   const f16* o2_w = nullptr;
   const float* o2_b = nullptr;
   const float *ln3_g = nullptr, *ln3_b = nullptr;

@@ -343,6 +343,12 @@ void launch_attention(const AttnArgs& a, uint32_t B, hipStream_t s) {
 }
 
 int run_attention(Ctx* c, AttnArgs a, uint32_t B) {
+  // K / V rows of one head are addressed with 32-bit byte offsets
+  const uint64_t ld = a.ldk > a.ldv ? a.ldk : a.ldv;
+  if ((uint64_t)(a.Skv + BKV) * ld * 2 >= (1ull << 31)) {
+    set_error("attention: Skv %u x row stride %llu too large", a.Skv, (unsigned long long)ld);
+    return DI_EUNSUPPORTED;
+  }
   a.splits = attn_splits(c, B, a.H, a.Sq, a.Skv);
   // tuning override: DI_ATTN_SPLITS=n (clamped so no key range is empty)
   static const char* env_splits = getenv("DI_ATTN_SPLITS");

@@ -14,7 +14,9 @@
 // [3C][C] matrix, attn2 to_k/to_v into [2C][cross], the GEGLU proj rows
 // grouped as 32-row blocks [16 hidden | 16 gate], every ResNet's
 // time_emb_proj stacked into one [sum Cout][1280] matrix (one GEMV per step),
-// biases and norm affines fp32.  di_unet_param_info describes each tensor.
+// every attn2 to_k/to_v pair stacked into one [sum 2C][1024] matrix (all
+// transformers' context projections are one GEMM per step), biases and norm
+// affines fp32.  di_unet_param_info describes each tensor.
 #include <cstring>
 #include <string>
 #include <vector>
@@ -27,7 +29,8 @@ namespace di {
 
 namespace {
 
-enum Arena { AR_W16 = 0, AR_TEMB16 = 1, AR_F32 = 2, AR_TEMB32 = 3, AR_COUNT = 4 };
+// AR_TEMB16 / AR_TEMB32 / AR_KV16 hold stacked matrices (no gaps between tensors)
+enum Arena { AR_W16 = 0, AR_TEMB16 = 1, AR_F32 = 2, AR_TEMB32 = 3, AR_KV16 = 4, AR_COUNT = 5 };
 
 struct Param {
   std::string name;
@@ -47,6 +50,7 @@ struct ResIdx {
 
 struct TfIdx {
   uint32_t c;
+  uint64_t kv_row;  // row offset inside the stacked attn2 to_kv matrix
   int ng, nb, piw, pib, l1g, l1b, qkv, o1w, o1b, l2g, l2b, q2, kv2, o2w, o2b, l3g, l3b, f1w, f1b,
       f2w, f2b, pow_, pob;
 };
@@ -62,9 +66,9 @@ struct Level {
 struct UNet {
   di_unet_config cfg;
   std::vector<Param> params;
-  uint64_t arena_elems[AR_COUNT] = {0, 0, 0, 0};
-  void* arena[AR_COUNT] = {nullptr, nullptr, nullptr, nullptr};
-  uint64_t arena_cap[AR_COUNT] = {0, 0, 0, 0};
+  uint64_t arena_elems[AR_COUNT] = {};
+  void* arena[AR_COUNT] = {};
+  uint64_t arena_cap[AR_COUNT] = {};
   // scratch buffers baked into the captured graph (owned until it is dropped)
   std::vector<std::pair<void*, uint64_t>> graph_scratch;
   int conv_in_w, conv_in_b, t1w, t1b, t2w, t2b, nog, nob, cow, cob;
@@ -72,6 +76,7 @@ struct UNet {
   ResIdx mid_res[2];
   TfIdx mid_tf;
   uint32_t temb_rows = 0;
+  uint32_t kv_rows = 0;
   // captured step
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
@@ -87,7 +92,7 @@ struct UNet {
     for (uint32_t d : shape) p.numel *= d;
     // keep every tensor 16-byte aligned inside its arena
     const uint64_t align = (arena == AR_F32 || arena == AR_TEMB32) ? 4 : 8;
-    if (arena != AR_TEMB16 && arena != AR_TEMB32)
+    if (arena != AR_TEMB16 && arena != AR_TEMB32 && arena != AR_KV16)
       arena_elems[arena] = (arena_elems[arena] + align - 1) / align * align;
     p.offset = arena_elems[arena];
     arena_elems[arena] += p.numel;
@@ -155,8 +160,10 @@ TfIdx add_transformer(UNet& u, const std::string& p, uint32_t c) {
   t.o1b = u.add(tb + ".attn1.to_out.0.bias", {c}, AR_F32, 0.0f, 0.01f, DI_PARAM_VECTOR);
   add_norm(u, tb + ".norm2", c, &t.l2g, &t.l2b);
   t.q2 = add_linear_w(u, tb + ".attn2.to_q", c, c, DI_PARAM_LINEAR);
-  t.kv2 = u.add(tb + ".attn2.to_kv.weight", {2 * c, x}, AR_W16, 0.0f, xavier(x, c),
+  t.kv_row = u.kv_rows;
+  t.kv2 = u.add(tb + ".attn2.to_kv.weight", {2 * c, x}, AR_KV16, 0.0f, xavier(x, c),
                 DI_PARAM_LINEAR_STACKED);
+  u.kv_rows += 2 * c;
   t.o2w = add_linear_w(u, tb + ".attn2.to_out.0", c, c, DI_PARAM_LINEAR);
   t.o2b = u.add(tb + ".attn2.to_out.0.bias", {c}, AR_F32, 0.0f, 0.01f, DI_PARAM_VECTOR);
   add_norm(u, tb + ".norm3", c, &t.l3g, &t.l3b);
@@ -278,6 +285,16 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   launch_layout(c->stream, sample, DI_F32, DI_NCHW, x16.p, DI_F16, DI_NHWC, B, cf.in_channels, H,
                 W, cin_p);
   launch_convert(c->stream, context, DI_F32, ctx16.p, DI_F16, (uint64_t)B * Sctx * cf.cross_dim);
+  // every transformer's attn2 K / V of the context: one GEMM over the
+  // stacked [kv_rows][cross] weights -> kvall [B*Sctx][kv_rows]
+  Scratch kvall;
+  if (u.kv_rows) {
+    rc = kvall.alloc(c, (uint64_t)B * Sctx * u.kv_rows * 2);
+    if (!rc)
+      rc = linear_f16(c, ctx16.h(), cf.cross_dim, B * Sctx, cf.cross_dim, (const f16*)u.arena[AR_KV16],
+                      u.kv_rows, nullptr, ACT_NONE, nullptr, 0, kvall.h(), u.kv_rows);
+    if (rc) return rc;
+  }
   // time embedding: sinusoid -> linear_1 + SiLU -> linear_2 -> every
   // ResNet's time_emb_proj(SiLU(temb)) in one GEMV
   GemvArgs g1;
@@ -328,7 +345,10 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   };
   auto transformer = [&](const TfIdx& t, const f16* x, uint32_t hh, uint32_t ww, f16* y) {
     TransformerShape s{B, hh, ww, t.c, Sctx, cf.cross_dim, G, cf.transformer_gn_eps, cf.ln_eps};
-    return transformer_forward(c, tf_w(u, t), s, x, ctx16.h(), y);
+    TransformerW w = tf_w(u, t);
+    w.kv_pre = kvall.h() + t.kv_row;
+    w.kv_ld = u.kv_rows;
+    return transformer_forward(c, w, s, x, ctx16.h(), y);
   };
   auto one = [](const f16* p, uint32_t ch) { return NhwcSrc{p, p, ch, ch, ch}; };
 
@@ -553,7 +573,7 @@ int32_t di_unet_create(di_ctx* ctx, const di_unet_config* cfg, uint64_t seed, di
   auto* u = new di_unet();
   u->cfg = c;
   build_params(*u);
-  const size_t esz[AR_COUNT] = {2, 2, 4, 4};
+  const size_t esz[AR_COUNT] = {2, 2, 4, 4, 2};
   for (int a = 0; a < AR_COUNT; a++) {
     int rc = pool_alloc(ctx, std::max<uint64_t>(u->arena_elems[a] * esz[a], 256), &u->arena[a],
                         &u->arena_cap[a]);
