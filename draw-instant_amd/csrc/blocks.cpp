@@ -23,10 +23,15 @@ namespace di {
 
 namespace {
 
-int run(Ctx* c, GemmArgs& g, int a_mode) {
+int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr) {
   const GemmPlan plan = gemm_plan(g, DI_F16, c->num_cus);
   const int tile = plan.tile;
   g.splits = plan.splits;
+  g.stats = nullptr;
+  if (st && st->p) {
+    st->done = gemm_stats_ok(g, DI_F16, a_mode, B_NK, tile);
+    if (st->done) g.stats = st->p;
+  }
   if (g.splits > 1) {
     void* ws = nullptr;
     int rc = workspace(c, gemm_ws_bytes(g), &ws);
@@ -38,7 +43,9 @@ int run(Ctx* c, GemmArgs& g, int a_mode) {
 }
 
 int gn_nhwc(Ctx* c, NhwcSrc x, const float* g, const float* b, f16* y, uint32_t N, uint32_t C,
-            uint32_t G, uint32_t HW, float eps, bool silu) {
+            uint32_t G, uint32_t HW, float eps, bool silu, const GnStats* st = nullptr) {
+  if (st && launch_group_norm_nhwc_st(c->stream, x, *st, g, b, y, N, C, G, HW, eps, silu))
+    return DI_OK;
   void* ws = nullptr;
   int rc = workspace(c, gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float), &ws);
   if (rc) return rc;
@@ -90,12 +97,12 @@ int conv_nhwc(Ctx* c, const ConvCall& cc) {
   } else {
     g.ldc = cc.ldc ? cc.ldc : cc.Cout;
   }
-  return run(c, g, A_CONV_NHWC);
+  return run(c, g, A_CONV_NHWC, cc.stats);
 }
 
 int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const f16* w,
                uint32_t N, const float* b, int act, const f16* res, uint64_t ldr, f16* y,
-               uint64_t ldy) {
+               uint64_t ldy, StatsOut* stats) {
   GemmArgs g;
   g.a = x;
   g.lda = ldx;
@@ -114,19 +121,22 @@ int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const
   g.b_vec_ok = K % 8 == 0;
   g.a_bytes = gemm_extent((uint64_t)M * ldx * 2);
   g.b_bytes = gemm_extent((uint64_t)N * K * 2);
-  return run(c, g, A_DENSE);
+  return run(c, g, A_DENSE, stats);
 }
 
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, const float* temb,
-                   uint32_t ld_temb, f16* out) {
+                   uint32_t ld_temb, f16* out, const GnStats* x_st, StatsOut* out_st) {
   const uint32_t HW = s.H * s.W;
   const uint64_t rows = (uint64_t)s.B * HW;
-  Scratch t1, t2, t3, sk;
+  // conv1 hands GN2 the statistics of its output (no partial pass)
+  const bool st2 = HW % 64 == 0;
+  Scratch t1, t2, t3, sk, t2st;
   int rc = t1.alloc(c, rows * s.Cin * 2);
   if (!rc) rc = t2.alloc(c, rows * s.Cout * 2);
   if (!rc) rc = t3.alloc(c, rows * s.Cout * 2);
+  if (!rc && st2) rc = t2st.alloc(c, gn_stats_floats(rows, s.Cout) * sizeof(float));
   if (rc) return rc;
-  rc = gn_nhwc(c, x, w.n1_g, w.n1_b, t1.h(), s.B, s.Cin, s.groups, HW, s.eps, true);
+  rc = gn_nhwc(c, x, w.n1_g, w.n1_b, t1.h(), s.B, s.Cin, s.groups, HW, s.eps, true, x_st);
   if (rc) return rc;
   ConvCall c1;
   c1.x = single(t1.h(), s.Cin);
@@ -141,10 +151,13 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
   c1.rows_b2 = HW;
   c1.ld_b2 = ld_temb;
   c1.y = t2.h();
+  StatsOut so2{st2 ? t2st.f() : nullptr};
+  c1.stats = &so2;
   rc = conv_nhwc(c, c1);
   if (rc) return rc;
+  const GnStats s2{t2st.f(), t2st.f(), s.Cout, s.Cout, s.Cout};
   rc = gn_nhwc(c, single(t2.h(), s.Cout), w.n2_g, w.n2_b, t3.h(), s.B, s.Cout, s.groups, HW,
-               s.eps, true);
+               s.eps, true, so2.done ? &s2 : nullptr);
   if (rc) return rc;
   const f16* res = nullptr;
   uint64_t ldr = s.Cout;
@@ -182,11 +195,12 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
   c2.res = res;
   c2.ldr = ldr;
   c2.y = out;
+  c2.stats = out_st;
   return conv_nhwc(c, c2);
 }
 
 int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s, const f16* x,
-                        const f16* context, f16* out) {
+                        const f16* context, f16* out, const GnStats* x_st, StatsOut* out_st) {
   const uint32_t HW = s.H * s.W, C = s.C;
   const uint64_t rows = (uint64_t)s.B * HW;
   Scratch t, h, n, qkv, a, q, kv, gg;
@@ -200,7 +214,7 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   if (rc) return rc;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
   // GN (eps 1e-6 in diffusers Transformer2DModel) -> proj_in
-  rc = gn_nhwc(c, single(x, C), w.n_g, w.n_b, t.h(), s.B, C, s.groups, HW, s.gn_eps, false);
+  rc = gn_nhwc(c, single(x, C), w.n_g, w.n_b, t.h(), s.B, C, s.groups, HW, s.gn_eps, false, x_st);
   if (!rc) rc = linear_f16(c, t.h(), C, rows, C, w.pin_w, C, w.pin_b, ACT_NONE, nullptr, 0, h.h(), C);
   if (rc) return rc;
   // self-attention
@@ -263,7 +277,7 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
     rc = linear_f16(c, gg.h(), 4 * C, rows, 4 * C, w.ff2_w, C, w.ff2_b, ACT_NONE, h.h(), C, h.h(), C);
   if (rc) return rc;
   // proj_out + block input residual
-  return linear_f16(c, h.h(), C, rows, C, w.pout_w, C, w.pout_b, ACT_NONE, x, C, out, C);
+  return linear_f16(c, h.h(), C, rows, C, w.pout_w, C, w.pout_b, ACT_NONE, x, C, out, C, out_st);
 }
 
 }  // namespace di

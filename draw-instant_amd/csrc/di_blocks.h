@@ -14,6 +14,14 @@ namespace di {
 // Stream-ordered scratch allocation from the context pool; released (to the
 // pool, not the driver) when the owner goes out of scope.  Safe because all
 // work is on the context's single in-order stream.
+// Request for the GroupNorm statistics of a GEMM's output (GemmArgs::stats
+// layout): p is the destination; done reports whether the GEMM wrote them
+// (it cannot on every path, e.g. K % 64 != 0).
+struct StatsOut {
+  float* p = nullptr;
+  bool done = false;
+};
+
 struct Scratch {
   Ctx* c = nullptr;
   void* p = nullptr;
@@ -64,8 +72,13 @@ struct ResnetShape {
 // out[B][HW][Cout] = conv2(SiLU(GN2(conv1(SiLU(GN1(x))) + temb))) + skip(x).
 // x is a channel concat of one or two NHWC sources.  temb: fp32 rows per
 // image, temb[b * ld_temb + c] (already offset to this block), may be null.
+// x_st: GroupNorm statistics of x from its producer (null: GN1 computes
+// them); out_st: if non-null, asks for out's statistics ([B*HW/64][Cout]
+// pairs, see GnStats; needs HW % 64 == 0) and reports whether they were
+// written.
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x,
-                   const float* temb, uint32_t ld_temb, f16* out);
+                   const float* temb, uint32_t ld_temb, f16* out, const GnStats* x_st = nullptr,
+                   StatsOut* out_st = nullptr);
 
 struct TransformerW {
   const float *n_g = nullptr, *n_b = nullptr;       // GroupNorm
@@ -99,8 +112,10 @@ struct TransformerShape {
 };
 
 // out = proj_out(block(proj_in(GN(x)))) + x; context fp16 [B][Sctx][cross].
+// x_st / out_st: GroupNorm statistics of x and out, as for resnet_forward.
 int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s, const f16* x,
-                        const f16* context, f16* out);
+                        const f16* context, f16* out, const GnStats* x_st = nullptr,
+                        StatsOut* out_st = nullptr);
 
 // NHWC conv through the implicit-GEMM kernel (fp16 in, fp16 or NCHW fp32 out).
 struct ConvCall {
@@ -115,12 +130,17 @@ struct ConvCall {
   void* y = nullptr;
   uint64_t ldc = 0;
   int y_nchw_f32 = 0;
+  StatsOut* stats = nullptr;  // GroupNorm statistics of y (GemmArgs::stats), optional
 };
 int conv_nhwc(Ctx* c, const ConvCall& cc);
 
-// Linear on token rows: y = act(x w^T + b) (+ res); fp16.
+// Linear on token rows: y = act(x w^T + b) (+ res); fp16.  stats: optional
+// GroupNorm statistics of y (GemmArgs::stats).
 int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const f16* w,
                uint32_t N, const float* b, int act, const f16* res, uint64_t ldr, f16* y,
-               uint64_t ldy);
+               uint64_t ldy, StatsOut* stats = nullptr);
+
+// Floats of the GroupNorm statistics of a [rows][C] output (rows % 64 == 0).
+inline uint64_t gn_stats_floats(uint64_t rows, uint32_t C) { return rows / 64 * C * 2; }
 
 }  // namespace di

@@ -64,6 +64,10 @@ struct GemmArgs {
   int c_nchw = 0;     // store C[(img*N + n)*c_hw + p] with m = img*c_hw + p
   uint32_t c_hw = 1;
   float* part = nullptr;  // split-K partials [splits][batch][M][N]
+  // Optional GroupNorm statistics of the stored output (see gemm_stats_ok):
+  // per 64-row chunk of the M rows and per column, (sum, sum of squares) at
+  // stats[((bz * ceil(M/64) + m/64) * N + n) * 2].
+  float* stats = nullptr;
   // Set by launch_gemm: fp16 NHWC output whose rows, bias, temb bias and
   // residual allow 16-byte vectors (the C tile is then staged through LDS
   // and written 8 columns per thread).
@@ -80,6 +84,10 @@ bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode);
 inline uint32_t gemm_extent(uint64_t bytes) { return bytes < 0x7fff0000ull ? (uint32_t)bytes : 0; }
 // elem: DI_F16 or DI_F32 operand element type.
 void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s);
+// Whether launch_gemm can produce g.stats for this call: buffer-load fp16
+// path with the vector epilogue, no GEGLU, batch 1, and N % 32 == 0 when
+// split-K is used.
+bool gemm_stats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile_cfg);
 // OIHW (any dtype) -> OHWI fp16 with optional zero channel padding Cin -> Cin_pad.
 void launch_repack_oihw_ohwi(hipStream_t s, const void* w, int wdt, void* out, uint32_t Cout,
                              uint32_t Cin, uint32_t ks, uint32_t Cin_pad);

@@ -45,6 +45,22 @@ struct NhwcSrc {
                   : *(const f16x8*)(p2 + pix * ld2 + (c - c1));
   }
 };
+// Producer statistics of an NHWC fp16 tensor (or channel concat of two):
+// per 64-pixel chunk and channel, (sum, sum of squares) of the stored
+// values; channels < c1 at s1[(chunk * ld1 + c) * 2], the rest at
+// s2[(chunk * ld2 + c - c1) * 2].  Chunks count over all images (HW % 64 == 0).
+struct GnStats {
+  const float* s1;
+  const float* s2;
+  uint32_t c1;
+  uint32_t ld1, ld2;
+};
+// GroupNorm apply from producer statistics (one kernel, no partial pass);
+// returns false when the shape is not supported (the caller then runs
+// launch_group_norm_nhwc).
+bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st, const float* gamma,
+                               const float* beta, void* y, uint32_t N, uint32_t C, uint32_t G,
+                               uint32_t HW, float eps, bool silu);
 void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const float* beta,
                             void* y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW,
                             float eps, bool silu, float* ws);

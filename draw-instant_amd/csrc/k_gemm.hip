@@ -292,7 +292,40 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
 #pragma unroll
       for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rr[u][j] : x[j]);
       *(f16x8*)(C + (uint64_t)mm[u] * g.ldc + nn[u]) = o;
+      if (g.stats) {
+        // the stored values, for the per-channel statistics of the tile
+        float* w = const_cast<float*>(&sC[r * LDC + c8]);
+        *(f32x4*)w = f32x4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+        *(f32x4*)(w + 4) = f32x4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+      }
     }
+  }
+}
+
+// GroupNorm statistics of an output tile (g.stats): for each 64-row chunk of
+// the tile and each column, the sum and sum of squares of the stored fp16
+// values over the chunk's rows < M, in row order, written to
+// stats[(chunk * N + n) * 2 + {0, 1}] with chunk = global row / 64.  sC holds
+// the stored values (written back by the epilogue).
+template <int BM, int BN, int LDC, int NT>
+__device__ __forceinline__ void gemm_tile_stats(const GemmArgs& g, const float* sC, uint32_t m0,
+                                                uint32_t n0) {
+  static_assert(BM % 64 == 0, "whole 64-row chunks");
+  constexpr int NCH = BM / 64;
+  for (int i = threadIdx.x; i < NCH * BN; i += NT) {
+    const int ch = i / BN, n = i % BN;
+    const uint32_t r0 = m0 + ch * 64;
+    if (r0 >= g.M || n0 + n >= g.N) continue;
+    const int rows = (int)min(64u, g.M - r0);
+    float s = 0.0f, q = 0.0f;
+    for (int r = 0; r < rows; r++) {
+      const float v = sC[(ch * 64 + r) * LDC + n];
+      s += v;
+      q += v * v;
+    }
+    float* st = g.stats + ((uint64_t)(r0 / 64) * g.N + n0 + n) * 2;
+    st[0] = s;
+    st[1] = q;
   }
 }
 
@@ -707,6 +740,10 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
         __syncthreads();
       }
       gemm_epilogue_vec<BM, BN, LDC, NT>(g, sC, m0, n0, bz, split);
+      if (g.stats && splits == 1) {
+        __syncthreads();
+        gemm_tile_stats<BM, BN, LDC, NT>(g, sC, m0, n0);
+      }
       return;
     }
   }
@@ -887,6 +924,60 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
   }
 }
 
+// Split-K reduction + epilogue + GroupNorm statistics (g.stats, vec_epi, no
+// GEGLU, N % 32 == 0): grid (N / 32, ceil(M / 64), batch); workgroup (x, y)
+// owns rows [64y, 64y + 64) x columns [32x, 32x + 32); thread t reduces
+// columns 32x + 8*(t % 4) .. +8 of row 64y + t/4.
+__global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
+  __shared__ float red[2][64][33];
+  const uint32_t t = threadIdx.x, cv = t % 4, rr = t / 4;
+  const uint32_t n = blockIdx.x * 32 + cv * 8, bz = blockIdx.z;
+  const uint32_t m = blockIdx.y * 64 + rr;
+  float s[8], q[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) s[j] = q[j] = 0.0f;
+  if (m < g.M) {
+    f32x4 bb[2] = {}, tb[2] = {};
+    if (g.bias) {
+      bb[0] = ld4(g.bias + n);
+      bb[1] = ld4(g.bias + n + 4);
+    }
+    if (g.bias2) {
+      const float* tp = g.bias2 + (uint64_t)(m / g.rows_b2) * g.ld_b2 + n;
+      tb[0] = ld4(tp);
+      tb[1] = ld4(tp + 4);
+    }
+    f16x8 rv = {};
+    if (g.res) rv = *(const f16x8*)((const f16*)g.res + (uint64_t)bz * g.sr + (uint64_t)m * g.ldr + n);
+    float x[8];
+    sum_splits8(g, bz, m, n, x);
+    epi_math8(g, x, bb, tb);
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rv[j] : x[j]);
+    *(f16x8*)((f16*)g.c + (uint64_t)bz * g.sc + (uint64_t)m * g.ldc + n) = o;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float v = (float)o[j];
+      s[j] = v;
+      q[j] = v * v;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    red[0][rr][cv * 8 + j] = s[j];
+    red[1][rr][cv * 8 + j] = q[j];
+  }
+  __syncthreads();
+  if (t < 64) {
+    const uint32_t col = t % 32, st = t / 32;
+    float a = 0.0f;
+    for (int r = 0; r < 64; r++) a += red[st][r][col];
+    const uint64_t chunk = (uint64_t)bz * ((g.M + 63) / 64) + blockIdx.y;
+    g.stats[(chunk * g.N + blockIdx.x * 32 + col) * 2 + st] = a;
+  }
+}
+
 template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D = 2,
           int KS = 1>
 void launch_cfg(const GemmArgs& g, hipStream_t s) {
@@ -1052,6 +1143,29 @@ bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode) {
   return false;
 }
 
+namespace {
+bool vec_epi_ok(const GemmArgs& g, int elem, int tile_cfg) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  return elem == DI_F16 && !g.c_nchw && !g.c_f32 && g.N % 8 == 0 && g.ldc % 8 == 0 &&
+         g.sc % 8 == 0 && al16(g.c) && (!g.bias || al16(g.bias)) &&
+         (!g.bias2 || (al16(g.bias2) && g.ld_b2 % 4 == 0)) &&
+         (!g.res || (!g.res_f32 && g.ldr % 8 == 0 && g.sr % 8 == 0 && al16(g.res))) &&
+         (g.act != ACT_GEGLU || g.N % 32 == 0) && tile_cfg != TILE_128x160;
+}
+}  // namespace
+
+bool gemm_stats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile_cfg) {
+  GemmArgs h = g;
+  if (!h.a2) {
+    h.a2 = h.a;
+    h.lda2 = h.lda;
+    h.a2_bytes = h.a_bytes;
+    if (h.c1 == 0) h.c1 = 0xffffffffu;
+  }
+  return gemm_fast_ok(h, elem, a_mode, b_mode) && vec_epi_ok(g, elem, tile_cfg) &&
+         g.act != ACT_GEGLU && g.batch == 1 && (g.splits <= 1 || g.N % 32 == 0);
+}
+
 void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s) {
   // k_split in elements, multiple of the stage depth
   const uint32_t bk = elem == DI_F32 ? 32 : 64;
@@ -1077,14 +1191,7 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
   if (a_mode == AMv && b_mode == BMv) {                  \
     launch_slow<T, AMv, BMv>(g, tile_cfg, s);            \
   }
-  {
-    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-    g.vec_epi = elem == DI_F16 && !g.c_nchw && !g.c_f32 && g.N % 8 == 0 && g.ldc % 8 == 0 &&
-                g.sc % 8 == 0 && al16(g.c) && (!g.bias || al16(g.bias)) &&
-                (!g.bias2 || (al16(g.bias2) && g.ld_b2 % 4 == 0)) &&
-                (!g.res || (!g.res_f32 && g.ldr % 8 == 0 && g.sr % 8 == 0 && al16(g.res))) &&
-                (g.act != ACT_GEGLU || g.N % 32 == 0) && tile_cfg != TILE_128x160;
-  }
+  g.vec_epi = vec_epi_ok(g, elem, tile_cfg);
   const bool fast = gemm_fast_ok(g, elem, a_mode, b_mode);
   if (fast) {
     // ring depth 2 measured as fast as 4 at U-Net shapes (short K); 4 is kept
@@ -1103,7 +1210,9 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
     else DI_GEMM_CASE(float, A_CONV_NCHW, B_NK)
   }
 #undef DI_GEMM_CASE
-  if (g.splits > 1) {
+  if (g.splits > 1 && g.stats) {
+    k_splitk_reduce_stats<<<dim3(g.N / 32, (g.M + 63) / 64, g.batch), 256, 0, s>>>(g);
+  } else if (g.splits > 1) {
     uint32_t ncols = g.act == ACT_GEGLU ? g.N / 2 : g.N;
     uint64_t total = (uint64_t)g.batch * g.M * ncols;
     uint64_t blocks = (total + 255) / 256;

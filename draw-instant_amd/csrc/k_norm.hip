@@ -336,6 +336,138 @@ __device__ __forceinline__ float gn_fold(const float* __restrict__ pn, uint32_t 
   return a;
 }
 
+// Apply pass from producer statistics (no partial pass): the kernel that
+// wrote x also wrote, per 64-pixel chunk and per channel, the sum and sum of
+// squares of the values it stored (GnStats; two sources for a channel
+// concat).  Grid (pixel blocks, C / SW, N): workgroup (pb, slice, n) folds the
+// statistics of its slice's channels over image n's chunks in chunk order,
+// then per group over the group's channels in channel order (so every
+// workgroup of a group computes the same mean / rstd), and applies
+// y = x*a[c] + b[c] (+SiLU) to its pixel block.  SW is a multiple of cpg and
+// of 8.  Thread t keeps vector t % NV of the slice for pixels t / NV + R*i.
+constexpr int kGnSliceMax = 128;
+
+__global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
+    NhwcSrc x, GnStats st, const float* __restrict__ gamma, const float* __restrict__ beta,
+    f16* __restrict__ y, uint32_t C, uint32_t cpg, uint32_t SW, uint32_t HW, uint32_t ppb,
+    float eps, int silu) {
+  __shared__ float chs[2][kGnSliceMax];
+  __shared__ float gms[2][kGnSliceMax];
+  const uint32_t tid = threadIdx.x, n = blockIdx.z, c0 = blockIdx.y * SW;
+  const uint32_t cpi = HW / 64;
+  // apply mapping; the first round of pixels and gamma / beta are loaded
+  // before the fold so the two memory round trips overlap
+  const uint32_t NV = SW / 8, R = 256 / NV, v = tid % NV, lane = tid / NV;
+  const bool act = lane < R;
+  const uint32_t c = c0 + v * 8;
+  const uint32_t p0 = blockIdx.x * ppb, p1 = min(p0 + ppb, HW);
+  const uint64_t pix0 = (uint64_t)n * HW;
+  constexpr int U = 4;
+  f16x8 pre[U];
+  f32x4 gmv[2], btv[2];
+  if (act) {
+#pragma unroll
+    for (int u = 0; u < U; u++) pre[u] = x.load8(pix0 + min(p0 + lane + u * R, p1 - 1), c);
+    gmv[0] = *(const f32x4*)(gamma + c);
+    gmv[1] = *(const f32x4*)(gamma + c + 4);
+    btv[0] = *(const f32x4*)(beta + c);
+    btv[1] = *(const f32x4*)(beta + c + 4);
+  }
+  // per channel: sums over the image's chunks.  Thread t takes channel quad
+  // t % Q (4 channels x 2 statistics = two 16-byte loads per chunk) and the
+  // chunks k = t / Q, + KL, ... (all loads in flight at once); the KL chunk
+  // lanes are then added in lane order.
+  __shared__ float fold[256 * 8];
+  const uint32_t Q = SW / 4, KL = 256 / Q;
+  {
+    const uint32_t qd = tid % Q, kl = tid / Q, c = c0 + qd * 4;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (kl < KL) {
+      const bool first = c < st.c1;  // 4-channel quads never straddle c1 (c1 % 8 == 0)
+      const float* base = first ? st.s1 : st.s2;
+      const uint64_t ld = first ? st.ld1 : st.ld2;
+      const uint64_t cc = first ? c : c - st.c1;
+      const float* p = base + ((uint64_t)n * cpi * ld + cc) * 2;
+      for (uint32_t k0 = kl; k0 < cpi; k0 += 8 * KL) {
+        f32x4 t[8][2];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const uint32_t k = k0 + u * KL < cpi ? k0 + u * KL : kl;
+          t[u][0] = *(const f32x4*)(p + (uint64_t)k * ld * 2);
+          t[u][1] = *(const f32x4*)(p + (uint64_t)k * ld * 2 + 4);
+        }
+        sched_fence();
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          if (k0 + u * KL < cpi) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              acc[e] += t[u][0][e];
+              acc[e + 4] += t[u][1][e];
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) fold[tid * 8 + e] = acc[e];
+  }
+  __syncthreads();
+  // acc layout per quad: (s, q) of channels 4qd .. 4qd+3 interleaved
+  for (uint32_t i = tid; i < 2 * SW; i += 256) {
+    const uint32_t cl = i % SW, sti = i / SW, qd = cl / 4, e = (cl % 4) * 2 + sti;
+    float a = 0.0f;
+    for (uint32_t kl = 0; kl < KL; kl++) a += fold[(kl * Q + qd) * 8 + e];
+    chs[sti][cl] = a;
+  }
+  __syncthreads();
+  const uint32_t GS = SW / cpg;
+  for (uint32_t g = tid; g < GS; g += 256) {
+    float ps = 0.0f, pq = 0.0f;
+    for (uint32_t cl = g * cpg; cl < (g + 1) * cpg; cl++) {
+      ps += chs[0][cl];
+      pq += chs[1][cl];
+    }
+    const float L = (float)cpg * (float)HW;
+    const float mean = ps / L;
+    const float var = fmaxf(pq / L - mean * mean, 0.0f);
+    gms[0][g] = mean;
+    gms[1][g] = 1.0f / sqrtf(var + eps);
+  }
+  __syncthreads();
+  if (!act) return;
+  float a[8], b[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t gl = (v * 8 + j) / cpg;
+    a[j] = gms[1][gl] * gmv[j >> 2][j & 3];
+    b[j] = btv[j >> 2][j & 3] - gms[0][gl] * a[j];
+  }
+  for (uint32_t p = p0 + lane; p < p1; p += U * R) {
+    f16x8 t[U];
+    if (p == p0 + lane) {
+#pragma unroll
+      for (int u = 0; u < U; u++) t[u] = pre[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; u++) t[u] = x.load8(pix0 + min(p + u * R, p1 - 1), c);
+    }
+    sched_fence();
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (p + u * R < p1) {
+        f16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float r = (float)t[u][j] * a[j] + b[j];
+          o[j] = (f16)(silu ? silu_f(r) : r);
+        }
+        *(f16x8*)(y + (pix0 + p + u * R) * C + c) = o;
+      }
+    }
+  }
+}
+
 // Pass 2, grid (achunks, N): every workgroup folds the image's partials in
 // the same fixed order into mean/rstd per group (so all workgroups agree
 // bit-for-bit) and applies y = x*a[c] + b[c] (+SiLU), a = rstd*gamma[c],
@@ -658,6 +790,39 @@ void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const 
     k_gn_nhwc_apply<2><<<dim3(ach, N), 256, 0, s>>>(x, gamma, beta, (f16*)y, C, G, HW, appc, sch,
                                                      eps, si, ws);
   }
+}
+
+bool gn_stats_slice(uint32_t C, uint32_t G, uint32_t HW, uint32_t* sw) {
+  if (G == 0 || C % G != 0 || HW % 64 != 0) return false;
+  const uint32_t cpg = C / G;
+  uint32_t l = cpg;
+  while (l % 8 != 0) l += cpg;  // lcm(cpg, 8)
+  for (uint32_t w = l; w <= (uint32_t)kGnSliceMax; w += l) {
+    if (C % w == 0 && (w >= 64 || w == C || w + l > (uint32_t)kGnSliceMax)) {
+      *sw = w;
+      return true;
+    }
+  }
+  return false;
+}
+
+bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st, const float* gamma,
+                               const float* beta, void* y, uint32_t N, uint32_t C, uint32_t G,
+                               uint32_t HW, float eps, bool silu) {
+  uint32_t sw = 0;
+  if (!gn_stats_slice(C, G, HW, &sw) || x.c1 % 8 != 0 || (st.c1 < C && st.c1 % 8 != 0))
+    return false;
+  const uint32_t slices = C / sw, R = 256 / (sw / 8);
+  // about 512 workgroups over the batch, at least one pixel per lane
+  uint32_t pbs = 512 / (N * slices);
+  const uint32_t maxpb = (HW + R - 1) / R;
+  if (pbs > maxpb) pbs = maxpb;
+  if (pbs < 1) pbs = 1;
+  const uint32_t ppb = (HW + pbs - 1) / pbs;
+  pbs = (HW + ppb - 1) / ppb;
+  k_gn_nhwc_apply_st<<<dim3(pbs, slices, N), 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw,
+                                                          HW, ppb, eps, silu ? 1 : 0);
+  return true;
 }
 
 void launch_layer_norm(hipStream_t s, const void* x, const float* gamma, const float* beta,

@@ -336,31 +336,54 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   g3.K = cf.time_dim;
   launch_gemv(g3, DI_F16, c->stream);
 
-  auto act_alloc = [&](Scratch& s, uint32_t hh, uint32_t ww, uint32_t ch) {
-    return s.alloc(c, (uint64_t)B * hh * ww * ch * 2);
+  // An activation and, when its level allows (HW % 64 == 0), the GroupNorm
+  // statistics its producer wrote (every GN input here is the output of a
+  // GEMM epilogue, so no GN runs a separate statistics pass).
+  struct Act {
+    Scratch buf, st;
+    uint32_t c = 0;
+    StatsOut so;   // request / report of the producer's statistics
+    bool has_st = false;
   };
-  auto resnet = [&](const ResIdx& r, NhwcSrc x, uint32_t hh, uint32_t ww, f16* y) {
+  auto act_alloc = [&](Act& a, uint32_t hh, uint32_t ww, uint32_t ch) {
+    const uint64_t rows = (uint64_t)B * hh * ww;
+    a.c = ch;
+    a.has_st = false;
+    int r = a.buf.alloc(c, rows * ch * 2);
+    if (!r && (hh * ww) % 64 == 0) r = a.st.alloc(c, gn_stats_floats(rows, ch) * sizeof(float));
+    a.so = StatsOut{a.st.f(), false};
+    return r;
+  };
+  // statistics request for a's producer; has_st follows once it has run
+  auto st_out = [](Act& a) { return a.so.p ? &a.so : (StatsOut*)nullptr; };
+  auto st_done = [](Act& a) { a.has_st = a.so.done; };
+  auto st_of = [](const Act& a) { return GnStats{a.st.f(), a.st.f(), a.c, a.c, a.c}; };
+  auto resnet = [&](const ResIdx& r, NhwcSrc x, const GnStats* xs, uint32_t hh, uint32_t ww,
+                    Act& y) {
     ResnetShape s{B, hh, ww, r.cin, r.cout, G, cf.resnet_eps};
-    return resnet_forward(c, res_w(u, r), s, x, tproj.f() + r.temb_row, u.temb_rows, y);
+    const int r2 = resnet_forward(c, res_w(u, r), s, x, tproj.f() + r.temb_row, u.temb_rows,
+                                  y.buf.h(), xs, st_out(y));
+    st_done(y);
+    return r2;
   };
-  auto transformer = [&](const TfIdx& t, const f16* x, uint32_t hh, uint32_t ww, f16* y) {
+  auto transformer = [&](const TfIdx& t, const Act& x, uint32_t hh, uint32_t ww, Act& y) {
     TransformerShape s{B, hh, ww, t.c, Sctx, cf.cross_dim, G, cf.transformer_gn_eps, cf.ln_eps};
     TransformerW w = tf_w(u, t);
     w.kv_pre = kvall.h() + t.kv_row;
     w.kv_ld = u.kv_rows;
-    return transformer_forward(c, w, s, x, ctx16.h(), y);
+    const GnStats xs = st_of(x);
+    const int r2 = transformer_forward(c, w, s, x.buf.h(), ctx16.h(), y.buf.h(),
+                                       x.has_st ? &xs : nullptr, st_out(y));
+    st_done(y);
+    return r2;
   };
   auto one = [](const f16* p, uint32_t ch) { return NhwcSrc{p, p, ch, ch, ch}; };
 
   // conv_in
-  struct Skip {
-    Scratch buf;
-    uint32_t c;
-  };
-  std::vector<Skip> skips;  // diffusers' down_block_res_samples
+  std::vector<Act> skips;  // diffusers' down_block_res_samples
   uint32_t hh = H, ww = W;
   uint32_t ch = cf.block_channels[0];
-  Scratch hcur;
+  Act hcur;
   rc = act_alloc(hcur, hh, ww, ch);
   if (rc) return rc;
   {
@@ -373,9 +396,11 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
     cc.Cout = ch;
     cc.w = u.h(u.conv_in_w);
     cc.bias = u.f(u.conv_in_b);
-    cc.y = hcur.h();
+    cc.y = hcur.buf.h();
+    cc.stats = st_out(hcur);
     rc = conv_nhwc(c, cc);
     if (rc) return rc;
+    st_done(hcur);
   }
   // down path: conv_in's output, every resnet(+transformer) output and every
   // downsampler output become skips; the current tensor is always the last one
@@ -383,28 +408,29 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
     Level& lv = u.down[i];
     for (size_t j = 0; j < lv.res.size(); j++) {
       const ResIdx& r = lv.res[j];
-      Scratch nxt;
+      Act nxt;
+      const GnStats xs = st_of(hcur);
       rc = act_alloc(nxt, hh, ww, r.cout);
-      if (!rc) rc = resnet(r, one(hcur.h(), ch), hh, ww, nxt.h());
+      if (!rc) rc = resnet(r, one(hcur.buf.h(), ch), hcur.has_st ? &xs : nullptr, hh, ww, nxt);
       if (rc) return rc;
       if (!lv.tf.empty()) {
-        Scratch t2;
+        Act t2;
         rc = act_alloc(t2, hh, ww, r.cout);
-        if (!rc) rc = transformer(lv.tf[j], nxt.h(), hh, ww, t2.h());
+        if (!rc) rc = transformer(lv.tf[j], nxt, hh, ww, t2);
         if (rc) return rc;
         nxt = std::move(t2);
       }
-      skips.push_back(Skip{std::move(hcur), ch});
+      skips.push_back(std::move(hcur));
       hcur = std::move(nxt);
       ch = r.cout;
     }
     if (lv.sample_w >= 0) {
-      Scratch ds;
+      Act ds;
       const uint32_t h2 = (hh - 1) / 2 + 1, w2 = (ww - 1) / 2 + 1;
       rc = act_alloc(ds, h2, w2, ch);
       if (rc) return rc;
       ConvCall cc;
-      cc.x = one(hcur.h(), ch);
+      cc.x = one(hcur.buf.h(), ch);
       cc.B = B;
       cc.H = hh;
       cc.W = ww;
@@ -413,59 +439,67 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
       cc.stride = 2;
       cc.w = u.h(lv.sample_w);
       cc.bias = u.f(lv.sample_b);
-      cc.y = ds.h();
+      cc.y = ds.buf.h();
+      cc.stats = st_out(ds);
       rc = conv_nhwc(c, cc);
       if (rc) return rc;
-      skips.push_back(Skip{std::move(hcur), ch});
+      st_done(ds);
+      skips.push_back(std::move(hcur));
       hcur = std::move(ds);
       hh = h2;
       ww = w2;
     }
   }
-  skips.push_back(Skip{std::move(hcur), ch});
+  skips.push_back(std::move(hcur));
   // mid block on the last skip (which the first up resnet consumes again)
-  Scratch m1, m2, m3;
-  const f16* mid_in = skips.back().buf.h();
+  Act m1, m2, m3;
+  const Act& mid_in = skips.back();
+  const GnStats ms = st_of(mid_in);
   rc = act_alloc(m1, hh, ww, ch);
-  if (!rc) rc = resnet(u.mid_res[0], one(mid_in, ch), hh, ww, m1.h());
+  if (!rc) rc = resnet(u.mid_res[0], one(mid_in.buf.h(), ch), mid_in.has_st ? &ms : nullptr, hh, ww, m1);
   if (!rc) rc = act_alloc(m2, hh, ww, ch);
-  if (!rc) rc = transformer(u.mid_tf, m1.h(), hh, ww, m2.h());
+  if (!rc) rc = transformer(u.mid_tf, m1, hh, ww, m2);
+  const GnStats m2s = st_of(m2);
   if (!rc) rc = act_alloc(m3, hh, ww, ch);
-  if (!rc) rc = resnet(u.mid_res[1], one(m2.h(), ch), hh, ww, m3.h());
+  if (!rc) rc = resnet(u.mid_res[1], one(m2.buf.h(), ch), m2.has_st ? &m2s : nullptr, hh, ww, m3);
   if (rc) return rc;
-  m1.release();
-  m2.release();
+  m1.buf.release();
+  m1.st.release();
+  m2.buf.release();
+  m2.st.release();
   hcur = std::move(m3);
   // up path: each resnet takes cat(current, last skip)
   for (int i = 0; i < 4; i++) {
     Level& lv = u.up[i];
     for (size_t j = 0; j < lv.res.size(); j++) {
       const ResIdx& r = lv.res[j];
-      Skip sk = std::move(skips.back());
+      Act sk = std::move(skips.back());
       skips.pop_back();
-      Scratch nxt;
+      Act nxt;
       rc = act_alloc(nxt, hh, ww, r.cout);
       if (rc) return rc;
-      NhwcSrc cat{hcur.h(), sk.buf.h(), ch, ch, sk.c};
-      rc = resnet(r, cat, hh, ww, nxt.h());
+      NhwcSrc cat{hcur.buf.h(), sk.buf.h(), ch, ch, sk.c};
+      const GnStats cs{hcur.st.f(), sk.st.f(), ch, ch, sk.c};
+      rc = resnet(r, cat, hcur.has_st && sk.has_st ? &cs : nullptr, hh, ww, nxt);
       if (rc) return rc;
       sk.buf.release();
+      sk.st.release();
       ch = r.cout;
       if (!lv.tf.empty()) {
-        Scratch t2;
+        Act t2;
         rc = act_alloc(t2, hh, ww, ch);
-        if (!rc) rc = transformer(lv.tf[j], nxt.h(), hh, ww, t2.h());
+        if (!rc) rc = transformer(lv.tf[j], nxt, hh, ww, t2);
         if (rc) return rc;
         nxt = std::move(t2);
       }
       hcur = std::move(nxt);
     }
     if (lv.sample_w >= 0) {
-      Scratch us;
+      Act us;
       rc = act_alloc(us, hh * 2, ww * 2, ch);
       if (rc) return rc;
       ConvCall cc;
-      cc.x = one(hcur.h(), ch);
+      cc.x = one(hcur.buf.h(), ch);
       cc.B = B;
       cc.H = hh;
       cc.W = ww;
@@ -474,9 +508,11 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
       cc.up = 2;
       cc.w = u.h(lv.sample_w);
       cc.bias = u.f(lv.sample_b);
-      cc.y = us.h();
+      cc.y = us.buf.h();
+      cc.stats = st_out(us);
       rc = conv_nhwc(c, cc);
       if (rc) return rc;
+      st_done(us);
       hcur = std::move(us);
       hh *= 2;
       ww *= 2;
@@ -484,14 +520,19 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   }
   // conv_norm_out + SiLU -> conv_out (NCHW fp32 store)
   Scratch no;
-  rc = act_alloc(no, hh, ww, ch);
+  rc = no.alloc(c, (uint64_t)B * hh * ww * ch * 2);
   if (rc) return rc;
   {
-    void* ws = nullptr;
-    rc = workspace(c, gn_nhwc_ws_floats(B, ch, G, hh * ww) * sizeof(float), &ws);
-    if (rc) return rc;
-    launch_group_norm_nhwc(c->stream, one(hcur.h(), ch), u.f(u.nog), u.f(u.nob), no.h(), B, ch, G,
-                           hh * ww, cf.resnet_eps, true, (float*)ws);
+    const GnStats hs = st_of(hcur);
+    if (!hcur.has_st || !launch_group_norm_nhwc_st(c->stream, one(hcur.buf.h(), ch), hs, u.f(u.nog),
+                                                   u.f(u.nob), no.h(), B, ch, G, hh * ww,
+                                                   cf.resnet_eps, true)) {
+      void* ws = nullptr;
+      rc = workspace(c, gn_nhwc_ws_floats(B, ch, G, hh * ww) * sizeof(float), &ws);
+      if (rc) return rc;
+      launch_group_norm_nhwc(c->stream, one(hcur.buf.h(), ch), u.f(u.nog), u.f(u.nob), no.h(), B,
+                             ch, G, hh * ww, cf.resnet_eps, true, (float*)ws);
+    }
   }
   ConvCall co;
   co.x = one(no.h(), ch);
