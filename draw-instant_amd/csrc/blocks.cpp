@@ -23,15 +23,26 @@ namespace di {
 
 namespace {
 
-int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr) {
+int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rst = nullptr) {
   const GemmPlan plan = gemm_plan(g, DI_F16, c->num_cus);
   const int tile = plan.tile;
   g.splits = plan.splits;
   g.stats = nullptr;
+  g.rstats = nullptr;
   if (st && st->p) {
     st->done = gemm_stats_ok(g, DI_F16, a_mode, B_NK, tile);
     if (st->done) g.stats = st->p;
   }
+  if (rst && rst->p) {
+    rst->done = gemm_rstats_ok(g, DI_F16, a_mode, B_NK, tile);
+    if (rst->done) {
+      g.rstats = rst->p;
+      rst->nt = gemm_rstats_tiles(g, tile);
+    }
+  }
+  DI_REQUIRE(!g.ln_rows || gemm_lnfold_ok(g, DI_F16, tile), DI_EUNSUPPORTED,
+             "LayerNorm fold needs the vector epilogue (M=%u N=%u K=%u tile %d)", g.M, g.N, g.K,
+             tile);
   if (g.splits > 1) {
     void* ws = nullptr;
     int rc = workspace(c, gemm_ws_bytes(g), &ws);
@@ -102,7 +113,7 @@ int conv_nhwc(Ctx* c, const ConvCall& cc) {
 
 int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const f16* w,
                uint32_t N, const float* b, int act, const f16* res, uint64_t ldr, f16* y,
-               uint64_t ldy, StatsOut* stats) {
+               uint64_t ldy, StatsOut* stats, RowStatsOut* rstats, const LnFold* ln) {
   GemmArgs g;
   g.a = x;
   g.lda = ldx;
@@ -121,7 +132,13 @@ int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const
   g.b_vec_ok = K % 8 == 0;
   g.a_bytes = gemm_extent((uint64_t)M * ldx * 2);
   g.b_bytes = gemm_extent((uint64_t)N * K * 2);
-  return run(c, g, A_DENSE, stats);
+  if (ln) {
+    g.ln_rows = ln->rows;
+    g.ln_nt = ln->nt;
+    g.ln_s = ln->s;
+    g.ln_eps = ln->eps;
+  }
+  return run(c, g, A_DENSE, stats, rstats);
 }
 
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, const float* temb,
@@ -203,8 +220,11 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
                         const f16* context, f16* out, const GnStats* x_st, StatsOut* out_st) {
   const uint32_t HW = s.H * s.W, C = s.C;
   const uint64_t rows = (uint64_t)s.B * HW;
-  Scratch t, h, n, qkv, a, q, kv, gg;
+  Scratch t, h, n, qkv, a, q, kv, gg, rs;
   int rc = t.alloc(c, rows * C * 2);
+  // row statistics of h from the GEMM that wrote it: the next LayerNorm runs
+  // inside the consuming GEMM's A staging
+  if (!rc) rc = rs.alloc(c, rows * ((C + 63) / 64) * 2 * sizeof(float));
   if (!rc) rc = h.alloc(c, rows * C * 2);
   if (!rc) rc = n.alloc(c, rows * C * 2);
   if (!rc) rc = qkv.alloc(c, rows * 3 * C * 2);
@@ -215,11 +235,38 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
   // GN (eps 1e-6 in diffusers Transformer2DModel) -> proj_in
   rc = gn_nhwc(c, single(x, C), w.n_g, w.n_b, t.h(), s.B, C, s.groups, HW, s.gn_eps, false, x_st);
-  if (!rc) rc = linear_f16(c, t.h(), C, rows, C, w.pin_w, C, w.pin_b, ACT_NONE, nullptr, 0, h.h(), C);
+  // a producer of h writes its row statistics when the next LayerNorm is folded
+  RowStatsOut ro{rs.f()};
+  auto ro_for = [&](const float* fs) {
+    ro.done = false;
+    return fs ? &ro : nullptr;
+  };
+  if (!rc)
+    rc = linear_f16(c, t.h(), C, rows, C, w.pin_w, C, w.pin_b, ACT_NONE, nullptr, 0, h.h(), C,
+                    nullptr, ro_for(w.qkv_s));
   if (rc) return rc;
+  // y = LayerNorm(h) @ W^T (+ bias / act).  With folded weights (fs set)
+  // the LayerNorm is the GEMM epilogue's, from row statistics of h that its
+  // producer wrote (or a statistics pass); else a LayerNorm kernel into n.
+  auto ln_linear = [&](const float* lg, const float* lb, const f16* wt, const float* fs,
+                       const float* fc, uint32_t N, const float* bias, int act, f16* y,
+                       uint64_t ldy) {
+    if (fs) {
+      if (!ro.done) {
+        launch_row_stats(c->stream, h.h(), rs.f(), rows, C);
+        ro.nt = 1;
+        ro.done = true;
+      }
+      const LnFold ln{rs.f(), ro.nt, fs, s.ln_eps};
+      return linear_f16(c, h.h(), C, rows, C, wt, N, fc, act, nullptr, 0, y, ldy, nullptr,
+                        nullptr, &ln);
+    }
+    launch_layer_norm(c->stream, h.h(), lg, lb, n.h(), rows, C, s.ln_eps, DI_F16);
+    return linear_f16(c, n.h(), C, rows, C, wt, N, bias, act, nullptr, 0, y, ldy);
+  };
   // self-attention
-  launch_layer_norm(c->stream, h.h(), w.ln1_g, w.ln1_b, n.h(), rows, C, s.ln_eps, DI_F16);
-  rc = linear_f16(c, n.h(), C, rows, C, w.qkv_w, 3 * C, nullptr, ACT_NONE, nullptr, 0, qkv.h(), 3 * C);
+  rc = ln_linear(w.ln1_g, w.ln1_b, w.qkv_w, w.qkv_s, w.qkv_c, 3 * C, nullptr, ACT_NONE, qkv.h(),
+                 3 * C);
   if (rc) return rc;
   AttnArgs sa;
   sa.q = qkv.h();
@@ -237,11 +284,11 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   sa.scale_log2 = scale_log2;
   rc = run_attention(c, sa, s.B);
   if (rc) return rc;
-  rc = linear_f16(c, a.h(), C, rows, C, w.o1_w, C, w.o1_b, ACT_NONE, h.h(), C, h.h(), C);
+  rc = linear_f16(c, a.h(), C, rows, C, w.o1_w, C, w.o1_b, ACT_NONE, h.h(), C, h.h(), C, nullptr,
+                  ro_for(w.q2_s));
   if (rc) return rc;
   // cross-attention
-  launch_layer_norm(c->stream, h.h(), w.ln2_g, w.ln2_b, n.h(), rows, C, s.ln_eps, DI_F16);
-  rc = linear_f16(c, n.h(), C, rows, C, w.q2_w, C, nullptr, ACT_NONE, nullptr, 0, qkv.h(), C);
+  rc = ln_linear(w.ln2_g, w.ln2_b, w.q2_w, w.q2_s, w.q2_c, C, nullptr, ACT_NONE, qkv.h(), C);
   const f16* kvp = w.kv_pre;
   const uint64_t kvld = w.kv_pre ? w.kv_ld : 2 * C;
   if (!rc && !kvp) {
@@ -268,11 +315,12 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   ca.scale_log2 = scale_log2;
   rc = run_attention(c, ca, s.B);
   if (rc) return rc;
-  rc = linear_f16(c, a.h(), C, rows, C, w.o2_w, C, w.o2_b, ACT_NONE, h.h(), C, h.h(), C);
+  rc = linear_f16(c, a.h(), C, rows, C, w.o2_w, C, w.o2_b, ACT_NONE, h.h(), C, h.h(), C, nullptr,
+                  ro_for(w.ff1_s));
   if (rc) return rc;
   // GEGLU feed-forward
-  launch_layer_norm(c->stream, h.h(), w.ln3_g, w.ln3_b, n.h(), rows, C, s.ln_eps, DI_F16);
-  rc = linear_f16(c, n.h(), C, rows, C, w.ff1_w, 8 * C, w.ff1_b, ACT_GEGLU, nullptr, 0, gg.h(), 4 * C);
+  rc = ln_linear(w.ln3_g, w.ln3_b, w.ff1_w, w.ff1_s, w.ff1_c, 8 * C, w.ff1_b, ACT_GEGLU, gg.h(),
+                 4 * C);
   if (!rc)
     rc = linear_f16(c, gg.h(), 4 * C, rows, 4 * C, w.ff2_w, C, w.ff2_b, ACT_NONE, h.h(), C, h.h(), C);
   if (rc) return rc;

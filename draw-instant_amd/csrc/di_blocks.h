@@ -22,6 +22,23 @@ struct StatsOut {
   bool done = false;
 };
 
+// Request for a GEMM's row statistics (GemmArgs::rstats): p is the
+// destination ([rows][ceil(N/64)] pairs suffice); nt and done are reported.
+struct RowStatsOut {
+  float* p = nullptr;
+  uint32_t nt = 0;
+  bool done = false;
+};
+
+// LayerNorm of a GEMM's A rows folded into its epilogue (GemmArgs::ln_*):
+// the weights are W * gamma, the bias sum_k beta[k] W[n][k] + bias[n].
+struct LnFold {
+  const float* rows;  // row statistics of A (RowStatsOut layout)
+  uint32_t nt;
+  const float* s;  // [N] column sums of the scaled weights
+  float eps;
+};
+
 struct Scratch {
   Ctx* c = nullptr;
   void* p = nullptr;
@@ -100,6 +117,13 @@ struct TransformerW {
   const float *ln3_g = nullptr, *ln3_b = nullptr;
   const f16* ff1_w = nullptr;  // GEGLU proj [8C][C], rows in 32-groups [16 h | 16 gate]
   const float* ff1_b = nullptr;
+  // Optional LayerNorms folded into their projections (qkv / q2 / ff1): when
+  // *_s is set, *_w holds W * gamma (per input column, launch_ln_fold),
+  // *_s[n] its row sums and *_c[n] = sum_k beta[k] W[n][k] + bias[n]; the
+  // ln*_g / ln*_b and ff1_b fields are then unused.
+  const float *qkv_s = nullptr, *qkv_c = nullptr;
+  const float *q2_s = nullptr, *q2_c = nullptr;
+  const float *ff1_s = nullptr, *ff1_c = nullptr;
   const f16* ff2_w = nullptr;  // [C][4C]
   const float* ff2_b = nullptr;
   const f16* pout_w = nullptr;  // proj_out [C][C]
@@ -136,9 +160,12 @@ int conv_nhwc(Ctx* c, const ConvCall& cc);
 
 // Linear on token rows: y = act(x w^T + b) (+ res); fp16.  stats: optional
 // GroupNorm statistics of y (GemmArgs::stats).
+// rstats: optional row statistics of y; ln: optional LayerNorm of x's rows
+// folded into the epilogue (w and b are then the folded weights and bias).
 int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const f16* w,
                uint32_t N, const float* b, int act, const f16* res, uint64_t ldr, f16* y,
-               uint64_t ldy, StatsOut* stats = nullptr);
+               uint64_t ldy, StatsOut* stats = nullptr, RowStatsOut* rstats = nullptr,
+               const LnFold* ln = nullptr);
 
 // Floats of the GroupNorm statistics of a [rows][C] output (rows % 64 == 0).
 inline uint64_t gn_stats_floats(uint64_t rows, uint32_t C) { return rows / 64 * C * 2; }

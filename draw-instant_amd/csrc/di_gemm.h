@@ -68,6 +68,20 @@ struct GemmArgs {
   // per 64-row chunk of the M rows and per column, (sum, sum of squares) at
   // stats[((bz * ceil(M/64) + m/64) * N + n) * 2].
   float* stats = nullptr;
+  // Optional row statistics of the stored output (vector epilogue, no split):
+  // per row m and column tile t = n0 / BN, (sum, sum of squares) at
+  // rstats[(m * ceil(N / BN) + t) * 2].
+  float* rstats = nullptr;
+  // Optional LayerNorm of A folded into the epilogue (see gemm_lnfold_ok):
+  // with B = W * gamma (per k), ln_s[n] = sum_k B[n][k] and the bias holding
+  // sum_k beta[k] W[n][k] + bias[n], LayerNorm(A) W^T + bias equals
+  // rstd[m] * (acc[m][n] - mean[m] * ln_s[n]) + bias[n].  mean / rstd of row
+  // m come from ln_rows: ln_nt (sum, sum of squares) pairs per row over its K
+  // values (the rstats layout), eps ln_eps.
+  const float* ln_rows = nullptr;
+  uint32_t ln_nt = 0;
+  const float* ln_s = nullptr;
+  float ln_eps = 0.0f;
   // Set by launch_gemm: fp16 NHWC output whose rows, bias, temb bias and
   // residual allow 16-byte vectors (the C tile is then staged through LDS
   // and written 8 columns per thread).
@@ -88,6 +102,13 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
 // path with the vector epilogue, no GEGLU, batch 1, and N % 32 == 0 when
 // split-K is used.
 bool gemm_stats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile_cfg);
+// Whether launch_gemm can produce g.rstats (same path, no split-K); the
+// column-tile count of the layout is then gemm_rstats_tiles(g, tile_cfg).
+bool gemm_rstats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile_cfg);
+uint32_t gemm_rstats_tiles(const GemmArgs& g, int tile_cfg);
+// Whether launch_gemm applies the LayerNorm fold of g.ln_* (fp16 vector
+// epilogue, batch 1, no GroupNorm statistics; split-K included).
+bool gemm_lnfold_ok(const GemmArgs& g, int elem, int tile_cfg);
 // OIHW (any dtype) -> OHWI fp16 with optional zero channel padding Cin -> Cin_pad.
 void launch_repack_oihw_ohwi(hipStream_t s, const void* w, int wdt, void* out, uint32_t Cout,
                              uint32_t Cin, uint32_t ks, uint32_t Cin_pad);

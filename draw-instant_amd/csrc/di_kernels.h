@@ -67,5 +67,12 @@ void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const 
 void launch_layer_norm(hipStream_t s, const void* x, const float* gamma,
                        const float* beta, void* y, uint32_t rows, uint32_t inner,
                        float eps, int dt);
+// (sum, sum of squares) of each fp16 row into out[row * 2] (inner % 8 == 0).
+void launch_row_stats(hipStream_t s, const f16* x, float* out, uint32_t rows, uint32_t inner);
+// LayerNorm folded into the projection that consumes it: wf = w * gamma (per
+// input column k, fp16), sum[n] = sum_k wf[n][k], cst[n] = sum_k beta[k]
+// w[n][k] + bias[n] (bias optional).  w, wf: [N][K] fp16, K % 8 == 0.
+void launch_ln_fold(hipStream_t s, const f16* w, const float* gamma, const float* beta,
+                    const float* bias, f16* wf, float* sum, float* cst, uint32_t N, uint32_t K);
 
 }  // namespace di

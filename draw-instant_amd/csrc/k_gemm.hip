@@ -149,6 +149,52 @@ __device__ __forceinline__ void act8(int act, float* v) {
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; }
 
+// LayerNorm fold (g.ln_rows): mean and rstd of A row m from its row
+// statistics, summed in column-tile order.  The first kLnBatch pairs are
+// loaded together (indices clamped to the row), so one memory latency
+// covers rows of up to kLnBatch column tiles; ln_load issues them and
+// ln_reduce consumes them, which lets a caller overlap the latency.
+constexpr int kLnBatch = 8;
+
+__device__ __forceinline__ void ln_load(const GemmArgs& g, uint32_t m, float2* v) {
+  const float2* p = (const float2*)g.ln_rows + (uint64_t)m * g.ln_nt;
+#pragma unroll
+  for (int i = 0; i < kLnBatch; i++) v[i] = p[min((uint32_t)i, g.ln_nt - 1)];
+}
+
+__device__ __forceinline__ void ln_reduce(const GemmArgs& g, uint32_t m, const float2* v,
+                                          float& mean, float& rstd) {
+  float s = 0.0f, q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kLnBatch; i++) {
+    if ((uint32_t)i < g.ln_nt) {
+      s += v[i].x;
+      q += v[i].y;
+    }
+  }
+  const float2* p = (const float2*)g.ln_rows + (uint64_t)m * g.ln_nt;
+  for (uint32_t t = kLnBatch; t < g.ln_nt; t++) {
+    const float2 w = p[t];
+    s += w.x;
+    q += w.y;
+  }
+  mean = s / (float)g.K;
+  const float var = fmaxf(q / (float)g.K - mean * mean, 0.0f);
+  rstd = 1.0f / sqrtf(var + g.ln_eps);
+}
+
+__device__ __forceinline__ void ln_coef(const GemmArgs& g, uint32_t m, float& mean, float& rstd) {
+  float2 v[kLnBatch];
+  ln_load(g, m, v);
+  ln_reduce(g, m, v, mean, rstd);
+}
+
+// x[j] = rstd * (x[j] - mean * s[j]) for one 8-column vector.
+__device__ __forceinline__ void ln_fold8(float* x, float mean, float rstd, const f32x4* s) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) x[j] = rstd * (x[j] - mean * s[j >> 2][j & 3]);
+}
+
 // x = act(x*alpha + bias[n..n+8) + bias2[(m/rows_b2)*ld_b2 + n..]) for one
 // vector whose operand loads (bb = bias, tb = bias2) were issued earlier.
 __device__ __forceinline__ void epi_math8(const GemmArgs& g, float* x, const f32x4* bb,
@@ -163,11 +209,17 @@ __device__ __forceinline__ void epi_math8(const GemmArgs& g, float* x, const f32
   act8(g.act, x);
 }
 
+// Epilogue extras of the dense buffer-load kernels (template parameter EX):
+// EX_ROWSTATS writes g.rstats, EX_LNFOLD applies the LayerNorm fold of
+// g.ln_*.  Separate instantiations keep their registers out of every other
+// GEMM's allocation.
+enum { EX_NONE = 0, EX_ROWSTATS = 1, EX_LNFOLD = 2 };
+
 // Writes (GEGLU-combined when act == GEGLU) results for the rows/columns of
 // one C tile staged in LDS as fp32 sC[BM][LDC].  Split-K partials are
 // stored as fp32 vectors instead.  All operand loads of a batch of vectors
 // are issued before any is consumed.
-template <int BM, int BN, int LDC, int NT>
+template <int BM, int BN, int LDC, int NT, int EX>
 __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float* sC, uint32_t m0,
                                                   uint32_t n0, uint32_t bz, uint32_t split) {
   const int tid = threadIdx.x;
@@ -277,26 +329,51 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     }
 #pragma unroll
     for (int u = 0; u < CH; u++) {
-      if (!okv[u]) continue;
       const int idx = tid + (v0 + u) * NT;
       const int r = idx / VPR8, c8 = (idx % VPR8) * 8;
-      float x[8];
-      const f32x4 a0 = ld4(&sC[r * LDC + c8]), a1 = ld4(&sC[r * LDC + c8 + 4]);
+      float rs = 0.0f, rq = 0.0f;
+      if (okv[u]) {
+        float x[8];
+        const f32x4 a0 = ld4(&sC[r * LDC + c8]), a1 = ld4(&sC[r * LDC + c8 + 4]);
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        x[j] = a0[j];
-        x[j + 4] = a1[j];
+        for (int j = 0; j < 4; j++) {
+          x[j] = a0[j];
+          x[j + 4] = a1[j];
+        }
+        epi_math8(g, x, bb[u], tb[u]);
+        f16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rr[u][j] : x[j]);
+        *(f16x8*)(C + (uint64_t)mm[u] * g.ldc + nn[u]) = o;
+        if (g.stats) {
+          // the stored values, for the column statistics of the tile
+          float* w = const_cast<float*>(&sC[r * LDC + c8]);
+          *(f32x4*)w = f32x4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+          *(f32x4*)(w + 4) = f32x4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+        }
+        if (EX == EX_ROWSTATS) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float f = (float)o[j];
+            rs += f;
+            rq += f * f;
+          }
+        }
       }
-      epi_math8(g, x, bb[u], tb[u]);
-      f16x8 o;
+      if (EX == EX_ROWSTATS) {
+        // row statistics over the tile's columns: the VPR8 lanes holding
+        // one row are consecutive (VPR8 divides the wavefront)
+        static_assert(64 % VPR8 == 0 || BN == 160, "row groups inside a wavefront");
+        if constexpr (64 % VPR8 == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rr[u][j] : x[j]);
-      *(f16x8*)(C + (uint64_t)mm[u] * g.ldc + nn[u]) = o;
-      if (g.stats) {
-        // the stored values, for the per-channel statistics of the tile
-        float* w = const_cast<float*>(&sC[r * LDC + c8]);
-        *(f32x4*)w = f32x4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
-        *(f32x4*)(w + 4) = f32x4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+          for (int o = 1; o < VPR8; o <<= 1) {
+            rs += __shfl_xor(rs, o);
+            rq += __shfl_xor(rq, o);
+          }
+          if (c8 == 0 && v0 + u < NV && idx < BM * VPR8 && mm[u] < g.M)
+            *(float2*)(g.rstats + ((uint64_t)mm[u] * ((g.N + BN - 1) / BN) + n0 / BN) * 2) =
+                float2{rs, rq};
+        }
       }
     }
   }
@@ -330,8 +407,10 @@ __device__ __forceinline__ void gemm_tile_stats(const GemmArgs& g, const float* 
 }
 
 // ---- the GEMM kernel ----
-template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D, int KS>
+template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D, int KS,
+          int EX>
 __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
+  static_assert(EX == EX_NONE || (FAST && AM == A_DENSE), "epilogue extras: dense fast path");
   using MT = Mfma<T>;
   constexpr int KV = MT::KV;
   constexpr int BK = 128 / sizeof(T);  // k elements per stage (128 bytes per row)
@@ -360,6 +439,8 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
   constexpr int kSmemPipe = 2 * (BM + BN) * LDK;
   constexpr int kSmemC = BM * (BN + 4) * 4 / (int)sizeof(T);  // fp32 C tile of the vector epilogue
   __shared__ __attribute__((aligned(16))) T smem[kSmemPipe > kSmemC ? kSmemPipe : kSmemC];
+  // LayerNorm fold: (mean, rstd) of each tile row, then ln_s of each column
+  __shared__ __attribute__((aligned(8))) float sLn[EX == EX_LNFOLD ? 2 * BM + BN : 2];
   T (*sA)[BM * LDK] = reinterpret_cast<T (*)[BM * LDK]>(smem);
   T (*sB)[BN * LDK] = reinterpret_cast<T (*)[BN * LDK]>(smem + 2 * BM * LDK);
   // element offset of (row r, k element e) inside one buffer
@@ -658,6 +739,53 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
   // barrier.  Loads past the last stage read zeros (offsets out of range) and
   // stages past the end skip their MFMA work, so the loop body has no branches
   // around loads and the waitcnt pass keeps exact vmcnt counts.
+  // LayerNorm fold (no split): the LN_T = NT / BM consecutive threads of
+  // tile row r = tid / LN_T each fetch every LN_T-th (sum, sum of squares)
+  // pair of the row (LN_U at once, after the first stages' loads are
+  // issued), combine them with lane shuffles once stage 0 is in LDS and
+  // leave (mean, rstd) in sLn; threads < BN add the column sums ln_s[n0 + tid].
+  // The prologue barrier publishes both before the main loop.
+  constexpr int LN_T = NT / BM, LN_U = 3;
+  static_assert(LN_T >= 1 && LN_T <= 64 && (LN_T & (LN_T - 1)) == 0, "row groups in a wavefront");
+  float2 ln_v[EX == EX_LNFOLD ? LN_U : 1];
+  float ln_col = 0.0f;
+  const uint32_t ln_r = (uint32_t)tid / LN_T, ln_p = (uint32_t)tid % LN_T;
+  const float2* ln_row = (const float2*)g.ln_rows + (uint64_t)min(m0 + ln_r, g.M - 1) * g.ln_nt;
+  auto ln_issue = [&]() {
+    if constexpr (EX == EX_LNFOLD) {
+#pragma unroll
+      for (int i = 0; i < LN_U; i++) ln_v[i] = ln_row[min(ln_p + i * LN_T, g.ln_nt - 1)];
+      if (tid < BN) ln_col = g.ln_s[min(n0 + (uint32_t)tid, g.N - 1)];
+    }
+  };
+  auto ln_publish = [&]() {
+    if constexpr (EX == EX_LNFOLD) {
+      float sm = 0.0f, sq = 0.0f;
+#pragma unroll
+      for (int i = 0; i < LN_U; i++) {
+        if (ln_p + i * LN_T < g.ln_nt) {
+          sm += ln_v[i].x;
+          sq += ln_v[i].y;
+        }
+      }
+      for (uint32_t t = ln_p + LN_U * LN_T; t < g.ln_nt; t += LN_T) {
+        const float2 w = ln_row[t];
+        sm += w.x;
+        sq += w.y;
+      }
+#pragma unroll
+      for (int o = 1; o < LN_T; o <<= 1) {
+        sm += __shfl_xor(sm, o);
+        sq += __shfl_xor(sq, o);
+      }
+      if (ln_p == 0) {
+        const float mean = sm / (float)g.K;
+        const float var = fmaxf(sq / (float)g.K - mean * mean, 0.0f);
+        *(float2*)&sLn[2 * ln_r] = float2{mean, 1.0f / sqrtf(var + g.ln_eps)};
+      }
+      if (tid < BN) sLn[2 * BM + tid] = ln_col;
+    }
+  };
   Stage r0, r1;
   if constexpr (FAST) {
     static_assert(D % 2 == 0, "even ring depth: LDS buffer = stage parity");
@@ -665,8 +793,10 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
     if (n_stages > 0) {
 #pragma unroll
       for (int j = 0; j < D; j++) load(j, r[j]);
+      ln_issue();
       store_stage(0, r[0]);
       load(D, r[0]);
+      ln_publish();  // after stage D's loads are issued: its wait covers stage 1 only
       __syncthreads();
       // steady state: whole rounds of D stages, no conditions (a conditional
       // compute makes the compiler copy the accumulators around it)
@@ -723,6 +853,18 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
       static_assert(BM * LDC * 4 <= (int)sizeof(smem), "C tile fits the LDS allocation");
       float* sC = reinterpret_cast<float*>(smem);
       __syncthreads();  // every wave is done reading the last stage
+      // LayerNorm fold (EX_LNFOLD, launched without split-K): the (mean,
+      // rstd) of this thread's accumulator rows and ln_s of its columns
+      float2 lmr[EX == EX_LNFOLD ? TM : 1][4];
+      float lsc[EX == EX_LNFOLD ? TN : 1];
+      if constexpr (EX == EX_LNFOLD) {
+#pragma unroll
+        for (int a = 0; a < TM; a++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) lmr[a][i] = *(const float2*)&sLn[2 * (wm0 + a * 16 + rq + i)];
+#pragma unroll
+        for (int b = 0; b < TN; b++) lsc[b] = sLn[2 * BM + wn0 + b * 16 + fr];
+      }
       // k half 0 writes the C tile, k half 1 (same positions) adds to it
 #pragma unroll
       for (int h = 0; h < KS; h++) {
@@ -734,12 +876,17 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
 #pragma unroll
               for (int i = 0; i < 4; i++) {
                 float& c = sC[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr];
-                c = h == 0 ? acc[a][b][i] : c + acc[a][b][i];
+                float v = h == 0 ? acc[a][b][i] : c + acc[a][b][i];
+                // LayerNorm fold once the k halves are summed:
+                // rstd * (acc - mean * ln_s[n])
+                if constexpr (EX == EX_LNFOLD)
+                  if (h == KS - 1) v = lmr[a][i].y * (v - lmr[a][i].x * lsc[b]);
+                c = v;
               }
         }
         __syncthreads();
       }
-      gemm_epilogue_vec<BM, BN, LDC, NT>(g, sC, m0, n0, bz, split);
+      gemm_epilogue_vec<BM, BN, LDC, NT, EX>(g, sC, m0, n0, bz, split);
       if (g.stats && splits == 1) {
         __syncthreads();
         gemm_tile_stats<BM, BN, LDC, NT>(g, sC, m0, n0);
@@ -890,11 +1037,19 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
     f16* C = (f16*)g.c + (uint64_t)bz * g.sc + (uint64_t)m * g.ldc + c8;
     const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr + (uint64_t)m * g.ldr + c8;
     float x[8];
+    float mean = 0.0f, rstd = 0.0f;
+    if (g.ln_rows) ln_coef(g, m, mean, rstd);
     if (geglu) {
       const uint32_t nh = (c8 / 16) * 32 + c8 % 16;
       float gt[8];
       sum_splits8(g, bz, m, nh, x);
       sum_splits8(g, bz, m, nh + 16, gt);
+      if (g.ln_rows) {
+        const f32x4 sh[2] = {ld4(g.ln_s + nh), ld4(g.ln_s + nh + 4)};
+        const f32x4 sg[2] = {ld4(g.ln_s + nh + 16), ld4(g.ln_s + nh + 20)};
+        ln_fold8(x, mean, rstd, sh);
+        ln_fold8(gt, mean, rstd, sg);
+      }
 #pragma unroll
       for (int j = 0; j < 8; j++) {
         const float hv = x[j] * g.alpha + (g.bias ? g.bias[nh + j] : 0.0f);
@@ -913,6 +1068,10 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
         tb[1] = ld4(tp + 4);
       }
       sum_splits8(g, bz, m, c8, x);
+      if (g.ln_rows) {
+        const f32x4 ls[2] = {ld4(g.ln_s + c8), ld4(g.ln_s + c8 + 4)};
+        ln_fold8(x, mean, rstd, ls);
+      }
       epi_math8(g, x, bb, tb);
     }
     f16x8 rv = {};
@@ -979,10 +1138,10 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
 }
 
 template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D = 2,
-          int KS = 1>
+          int KS = 1, int EX = EX_NONE>
 void launch_cfg(const GemmArgs& g, hipStream_t s) {
   uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D, KS>
+  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D, KS, EX>
       <<<dim3(tiles, 1, g.batch * g.splits), 256 * KS, 0, s>>>(g);
 }
 
@@ -997,22 +1156,27 @@ void launch_slow(const GemmArgs& g, int tile_cfg, hipStream_t s) {
     launch_cfg<T, 128, 128, 2, 2, AM, BMD, false>(g, s);
 }
 
-// Buffer-load variants: every tile shape, ring depth D.
-template <int AM, int D>
+// Buffer-load variants: every tile shape, ring depth D, epilogue extras EX.
+template <int AM, int D, int EX = EX_NONE>
 void launch_fast_d(const GemmArgs& g, int tile_cfg, hipStream_t s) {
   switch (tile_cfg) {
-    case TILE_128x128: launch_cfg<f16, 128, 128, 2, 2, AM, B_NK, true, D>(g, s); break;
-    case TILE_128x64: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D>(g, s); break;
-    case TILE_64x160: launch_cfg<f16, 64, 160, 2, 2, AM, B_NK, true, D>(g, s); break;
-    case TILE_64x128: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D>(g, s); break;
-    case TILE_64x64_K2: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D, 2>(g, s); break;
-    case TILE_128x64_K2: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D, 2>(g, s); break;
-    case TILE_64x128_K2: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D, 2>(g, s); break;
-    default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D>(g, s); break;
+    case TILE_128x128: launch_cfg<f16, 128, 128, 2, 2, AM, B_NK, true, D, 1, EX>(g, s); break;
+    case TILE_128x64: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D, 1, EX>(g, s); break;
+    case TILE_64x160: launch_cfg<f16, 64, 160, 2, 2, AM, B_NK, true, D, 1, EX>(g, s); break;
+    case TILE_64x128: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D, 1, EX>(g, s); break;
+    case TILE_64x64_K2: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
+    case TILE_128x64_K2: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
+    case TILE_64x128_K2: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
+    default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D, 1, EX>(g, s); break;
   }
 }
 template <int AM>
 void launch_fast(const GemmArgs& g, int tile_cfg, int depth, hipStream_t s) {
+  if constexpr (AM == A_DENSE) {
+    // the extras only at ring depth 2 (depth 4 is a tuning option)
+    if (g.ln_rows && g.splits <= 1) return launch_fast_d<AM, 2, EX_LNFOLD>(g, tile_cfg, s);
+    if (g.rstats) return launch_fast_d<AM, 2, EX_ROWSTATS>(g, tile_cfg, s);
+  }
   if (depth >= 4) launch_fast_d<AM, 4>(g, tile_cfg, s);
   else launch_fast_d<AM, 2>(g, tile_cfg, s);
 }
@@ -1134,9 +1298,11 @@ uint64_t gemm_ws_bytes(const GemmArgs& g) {
 }
 
 bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode) {
+  // a2 == nullptr: single source (launch_gemm then sets a2 = a)
+  const uint32_t a2_bytes = g.a2 ? g.a2_bytes : g.a_bytes;
+  const bool single = !g.a2 || g.c1 == 0xffffffffu || g.a2 == g.a;
   if (elem != DI_F16 || b_mode != B_NK || !g.b_vec_ok) return false;
-  if (g.a_bytes == 0 || g.a2_bytes == 0 || g.b_bytes == 0) return false;  // extents unknown
-  const bool single = g.c1 == 0xffffffffu || g.a2 == g.a;
+  if (g.a_bytes == 0 || a2_bytes == 0 || g.b_bytes == 0) return false;  // extents unknown
   if (g.K % 64 != 0) return false;  // whole 64-element stages (no per-lane k bound)
   if (a_mode == A_DENSE) return g.a_vec_ok && single;
   if (a_mode == A_CONV_NHWC) return g.Cin % 64 == 0 && (single || g.c1 % 64 == 0) && (g.up == 1 || g.up == 2);
@@ -1155,15 +1321,28 @@ bool vec_epi_ok(const GemmArgs& g, int elem, int tile_cfg) {
 }  // namespace
 
 bool gemm_stats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile_cfg) {
-  GemmArgs h = g;
-  if (!h.a2) {
-    h.a2 = h.a;
-    h.lda2 = h.lda;
-    h.a2_bytes = h.a_bytes;
-    if (h.c1 == 0) h.c1 = 0xffffffffu;
-  }
-  return gemm_fast_ok(h, elem, a_mode, b_mode) && vec_epi_ok(g, elem, tile_cfg) &&
+  return gemm_fast_ok(g, elem, a_mode, b_mode) && vec_epi_ok(g, elem, tile_cfg) &&
          g.act != ACT_GEGLU && g.batch == 1 && (g.splits <= 1 || g.N % 32 == 0);
+}
+
+bool gemm_rstats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile_cfg) {
+  GemmArgs h = g;
+  h.splits = 1;
+  // row groups of the vector epilogue must divide a wavefront (not 160 wide)
+  return gemm_stats_ok(h, elem, a_mode, b_mode, tile_cfg) && g.splits <= 1 &&
+         64 % (kTileN[tile_cfg] / 8) == 0;
+}
+
+bool gemm_lnfold_ok(const GemmArgs& g, int elem, int tile_cfg) {
+  // without split-K the fold runs in the buffer-load kernel's epilogue, with
+  // it in the vector split-K reducer
+  return vec_epi_ok(g, elem, tile_cfg) && g.batch == 1 && !g.stats && !g.rstats && g.ln_s &&
+         ((uintptr_t)g.ln_s & 15) == 0 && ((uintptr_t)g.ln_rows & 7) == 0 && g.ln_nt > 0 && g.K > 0 &&
+         (g.splits > 1 || gemm_fast_ok(g, elem, A_DENSE, B_NK));
+}
+
+uint32_t gemm_rstats_tiles(const GemmArgs& g, int tile_cfg) {
+  return (g.N + kTileN[tile_cfg] - 1) / kTileN[tile_cfg];
 }
 
 void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s) {

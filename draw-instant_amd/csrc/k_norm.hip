@@ -845,6 +845,78 @@ void launch_layer_norm(hipStream_t s, const void* x, const float* gamma, const f
   }
 }
 
+// ---- LayerNorm folded into the consuming projection ----
+// Row statistics: (sum, sum of squares) of each fp16 row, one wavefront per
+// row (inner % 8 == 0).
+__global__ __launch_bounds__(256) void k_row_stats_f16(const f16* __restrict__ x,
+                                                       float* __restrict__ out, uint32_t rows,
+                                                       uint32_t inner) {
+  const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  const f16* xr = x + (uint64_t)row * inner;
+  float s = 0.0f, q = 0.0f;
+  for (uint32_t j = lane * 8; j < inner; j += kWave * 8) {
+    const f16x8 v = *(const f16x8*)(xr + j);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float f = (float)v[e];
+      s += f;
+      q += f * f;
+    }
+  }
+  s = wave_sum(s);
+  q = wave_sum(q);
+  if (lane == 0) *(float2*)(out + (uint64_t)row * 2) = float2{s, q};
+}
+
+void launch_row_stats(hipStream_t s, const f16* x, float* out, uint32_t rows, uint32_t inner) {
+  k_row_stats_f16<<<(rows + 3) / 4, 256, 0, s>>>(x, out, rows, inner);
+}
+
+// Weight fold, one wavefront per output row n (K % 8 == 0):
+// wf[n][k] = fp16(gamma[k] * w[n][k]), sum[n] = sum_k wf[n][k] (the rounded
+// values, so the epilogue's mean term matches what the GEMM multiplies) and
+// cst[n] = sum_k beta[k] * w[n][k] + bias[n].
+__global__ __launch_bounds__(256) void k_ln_fold(const f16* __restrict__ w,
+                                                 const float* __restrict__ gamma,
+                                                 const float* __restrict__ beta,
+                                                 const float* __restrict__ bias,
+                                                 f16* __restrict__ wf, float* __restrict__ sum,
+                                                 float* __restrict__ cst, uint32_t N, uint32_t K) {
+  const uint32_t n = blockIdx.x * 4 + threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  if (n >= N) return;
+  const f16* wr = w + (uint64_t)n * K;
+  f16* fr = wf + (uint64_t)n * K;
+  float sw = 0.0f, cb = 0.0f;
+  for (uint32_t k = lane * 8; k < K; k += kWave * 8) {
+    const f16x8 v = *(const f16x8*)(wr + k);
+    const f32x4 g[2] = {*(const f32x4*)(gamma + k), *(const f32x4*)(gamma + k + 4)};
+    const f32x4 b[2] = {*(const f32x4*)(beta + k), *(const f32x4*)(beta + k + 4)};
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float wv = (float)v[e];
+      o[e] = (f16)(wv * g[e >> 2][e & 3]);
+      sw += (float)o[e];
+      cb += b[e >> 2][e & 3] * wv;
+    }
+    *(f16x8*)(fr + k) = o;
+  }
+  sw = wave_sum(sw);
+  cb = wave_sum(cb);
+  if (lane == 0) {
+    sum[n] = sw;
+    cst[n] = cb + (bias ? bias[n] : 0.0f);
+  }
+}
+
+void launch_ln_fold(hipStream_t s, const f16* w, const float* gamma, const float* beta,
+                    const float* bias, f16* wf, float* sum, float* cst, uint32_t N, uint32_t K) {
+  k_ln_fold<<<(N + 3) / 4, 256, 0, s>>>(w, gamma, beta, bias, wf, sum, cst, N, K);
+}
+
 }  // namespace di
 
 using namespace di;

@@ -29,8 +29,20 @@ namespace di {
 
 namespace {
 
-// AR_TEMB16 / AR_TEMB32 / AR_KV16 hold stacked matrices (no gaps between tensors)
-enum Arena { AR_W16 = 0, AR_TEMB16 = 1, AR_F32 = 2, AR_TEMB32 = 3, AR_KV16 = 4, AR_COUNT = 5 };
+// AR_TEMB16 / AR_TEMB32 / AR_KV16 hold stacked matrices (no gaps between
+// tensors).  AR_LNW16 / AR_LN32 hold no parameters: they are derived from
+// them (the LayerNorm-folded attn1 qkv / attn2 to_q / GEGLU proj weights and
+// their column sums and constants, refreshed after any parameter upload).
+enum Arena {
+  AR_W16 = 0,
+  AR_TEMB16 = 1,
+  AR_F32 = 2,
+  AR_TEMB32 = 3,
+  AR_KV16 = 4,
+  AR_LNW16 = 5,
+  AR_LN32 = 6,
+  AR_COUNT = 7
+};
 
 struct Param {
   std::string name;
@@ -53,6 +65,9 @@ struct TfIdx {
   uint64_t kv_row;  // row offset inside the stacked attn2 to_kv matrix
   int ng, nb, piw, pib, l1g, l1b, qkv, o1w, o1b, l2g, l2b, q2, kv2, o2w, o2b, l3g, l3b, f1w, f1b,
       f2w, f2b, pow_, pob;
+  // folded projections: weights in AR_LNW16, column sums / constants in AR_LN32
+  uint64_t fw_qkv, fw_q2, fw_ff1;
+  uint64_t fs_qkv, fc_qkv, fs_q2, fc_q2, fs_ff1, fc_ff1;
 };
 
 struct Level {
@@ -77,6 +92,7 @@ struct UNet {
   TfIdx mid_tf;
   uint32_t temb_rows = 0;
   uint32_t kv_rows = 0;
+  bool ln_folded = false;  // AR_LNW16 / AR_LN32 match the parameters
   // captured step
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
@@ -174,6 +190,21 @@ TfIdx add_transformer(UNet& u, const std::string& p, uint32_t c) {
   t.f2b = u.add(tb + ".ff.net.2.bias", {c}, AR_F32, 0.0f, 0.01f, DI_PARAM_VECTOR);
   t.pow_ = add_linear_w(u, p + ".proj_out", c, c, DI_PARAM_LINEAR);
   t.pob = u.add(p + ".proj_out.bias", {c}, AR_F32, 0.0f, 0.01f, DI_PARAM_VECTOR);
+  auto derived = [&](int arena, uint64_t n) {
+    const uint64_t align = arena == AR_LN32 ? 4 : 8;
+    const uint64_t o = (u.arena_elems[arena] + align - 1) / align * align;
+    u.arena_elems[arena] = o + n;
+    return o;
+  };
+  t.fw_qkv = derived(AR_LNW16, 3ull * c * c);
+  t.fw_q2 = derived(AR_LNW16, (uint64_t)c * c);
+  t.fw_ff1 = derived(AR_LNW16, 8ull * c * c);
+  t.fs_qkv = derived(AR_LN32, 3 * c);
+  t.fc_qkv = derived(AR_LN32, 3 * c);
+  t.fs_q2 = derived(AR_LN32, c);
+  t.fc_q2 = derived(AR_LN32, c);
+  t.fs_ff1 = derived(AR_LN32, 8 * c);
+  t.fc_ff1 = derived(AR_LN32, 8 * c);
   return t;
 }
 
@@ -265,7 +296,39 @@ TransformerW tf_w(const UNet& u, const TfIdx& t) {
   w.ff2_b = u.f(t.f2b);
   w.pout_w = u.h(t.pow_);
   w.pout_b = u.f(t.pob);
+  // the three LayerNorms run in the epilogues of their projections
+  f16* fw = (f16*)u.arena[AR_LNW16];
+  float* ff = (float*)u.arena[AR_LN32];
+  w.qkv_w = fw + t.fw_qkv;
+  w.qkv_s = ff + t.fs_qkv;
+  w.qkv_c = ff + t.fc_qkv;
+  w.q2_w = fw + t.fw_q2;
+  w.q2_s = ff + t.fs_q2;
+  w.q2_c = ff + t.fc_q2;
+  w.ff1_w = fw + t.fw_ff1;
+  w.ff1_s = ff + t.fs_ff1;
+  w.ff1_c = ff + t.fc_ff1;
   return w;
+}
+
+// Derives every transformer's folded projections from the parameters.
+void fold_layer_norms(hipStream_t s, UNet& u) {
+  f16* fw = (f16*)u.arena[AR_LNW16];
+  float* ff = (float*)u.arena[AR_LN32];
+  auto one = [&](const TfIdx& t) {
+    const uint32_t c = t.c;
+    launch_ln_fold(s, u.h(t.qkv), u.f(t.l1g), u.f(t.l1b), nullptr, fw + t.fw_qkv, ff + t.fs_qkv,
+                   ff + t.fc_qkv, 3 * c, c);
+    launch_ln_fold(s, u.h(t.q2), u.f(t.l2g), u.f(t.l2b), nullptr, fw + t.fw_q2, ff + t.fs_q2,
+                   ff + t.fc_q2, c, c);
+    launch_ln_fold(s, u.h(t.f1w), u.f(t.l3g), u.f(t.l3b), u.f(t.f1b), fw + t.fw_ff1,
+                   ff + t.fs_ff1, ff + t.fc_ff1, 8 * c, c);
+  };
+  for (const Level& l : u.down)
+    for (const TfIdx& t : l.tf) one(t);
+  one(u.mid_tf);
+  for (const Level& l : u.up)
+    for (const TfIdx& t : l.tf) one(t);
 }
 
 // One denoise step (enqueue only).
@@ -614,7 +677,7 @@ int32_t di_unet_create(di_ctx* ctx, const di_unet_config* cfg, uint64_t seed, di
   auto* u = new di_unet();
   u->cfg = c;
   build_params(*u);
-  const size_t esz[AR_COUNT] = {2, 2, 4, 4, 2};
+  const size_t esz[AR_COUNT] = {2, 2, 4, 4, 2, 2, 4};
   for (int a = 0; a < AR_COUNT; a++) {
     int rc = pool_alloc(ctx, std::max<uint64_t>(u->arena_elems[a] * esz[a], 256), &u->arena[a],
                         &u->arena_cap[a]);
@@ -685,10 +748,12 @@ static int param_xfer(di_ctx* ctx, di_unet* u, uint32_t i, void* host, uint64_t 
              (unsigned long long)(p.numel * es), (unsigned long long)bytes);
   DI_REQUIRE(host != nullptr, DI_EINVAL, "null host pointer");
   void* dev = (char*)u->arena[p.arena] + p.offset * es;
-  if (down)
+  if (down) {
     DI_HIP(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
-  else
+  } else {
     DI_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    u->ln_folded = false;
+  }
   DI_HIP(hipStreamSynchronize(ctx->stream));
   return DI_OK;
 }
@@ -716,6 +781,12 @@ int32_t di_unet_forward(di_ctx* ctx, di_unet* u, di_handle sample, di_handle tim
   DI_BUF(ctx, timesteps, t, (uint64_t)B * 4);
   DI_BUF(ctx, context, cx, (uint64_t)B * Sctx * c.cross_dim * 4);
   DI_BUF(ctx, out, o, (uint64_t)B * c.out_channels * H * W * 4);
+  if (!u->ln_folded) {
+    // stream-ordered before the step (a captured graph reads the same arenas)
+    fold_layer_norms(ctx->stream, *u);
+    DI_LAUNCH_CHECK();
+    u->ln_folded = true;
+  }
   if (!(flags & DI_UNET_GRAPH)) {
     int rc = unet_step(ctx, *u, (const float*)s->ptr, (const float*)t->ptr, (const float*)cx->ptr,
                        (float*)o->ptr, B, H, W, Sctx);

@@ -57,6 +57,40 @@ def test_small_unet_vs_oracle(dev, rng):
         u.destroy()
 
 
+def test_layer_norm_fold_follows_uploads(dev, rng):
+    """The transformer LayerNorms (norm1/2/3) run inside their projections'
+    GEMMs, on weights derived from the parameters (W * gamma, beta . W + bias)
+    the first time the U-Net runs after a parameter upload.  Strong gammas /
+    betas uploaded after a first step (so the derived weights must be
+    refreshed) still give the oracle's result; with the near-identity
+    initial affines a dropped beta term or a stale derivation would pass."""
+    import re
+    from drawinstant.unet import UNet, UNetConfig
+    cfg = UNetConfig.small()
+    u = UNet(dev, cfg, seed=11)
+    try:
+        x, ctx = _inputs(rng, 1, 16, 16, 77, cfg.cross_dim)
+        first = u(x, 999.0, ctx)  # derives the folded weights
+        sd = u.state_dict(np.float32)
+        pat = re.compile(r"transformer_blocks\.0\.norm[123]\.(weight|bias)$")
+        for k in sd:
+            m = pat.search(k)
+            if m:
+                n = rng.standard_normal(sd[k].shape).astype(np.float32)
+                sd[k] = (1.0 + 0.5 * n) if m.group(1) == "weight" else 0.5 * n
+        u.load_state_dict(sd)
+        got = u(x, 999.0, ctx)
+        ref = unet_ref.unet_forward(unet_ref.OracleOps(), u.state_dict(), cfg.as_dict(), x,
+                                    np.array([999.0], np.float32), ctx)
+        err = rel_l2(got, ref)
+        print(f"[ln fold] rel-L2 {err:.2e}, change from the first step {rel_l2(got, first):.2e}",
+              flush=True)
+        assert np.isfinite(got).all() and err <= 1e-2
+        assert rel_l2(got, first) > 5e-2  # the new affines took effect
+    finally:
+        u.destroy()
+
+
 def _torch_ref(sd21, x, t, ctx):
     sd = sd21.state_dict(np.float32)
     out = unet_ref.unet_forward(unet_ref.TorchOps("cuda"), sd, sd21.config.as_dict(), x,
