@@ -22,7 +22,12 @@ enum TileCfg {
   TILE_64x64_K2 = 6,
   TILE_128x64_K2 = 7,
   TILE_64x128_K2 = 8,
-  TILE_COUNT = 9
+  // sixteen wavefronts: 2x4 (4x2) output wave tiles, two waves per tile
+  TILE_64x128_W16 = 9,
+  TILE_128x64_W16 = 10,
+  TILE_128x128_W16 = 11,
+  TILE_64x64_W16 = 12,
+  TILE_COUNT = 13
 };
 
 struct GemmPlan {

@@ -22,7 +22,7 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))  # draw-instant_amd/
 
-TILES = (0, 1, 2, 3, 5, 6, 7, 8)  # TILE_128x160 (4) is not built
+TILES = (0, 1, 2, 3, 5, 6, 7, 8, 9, 10, 11, 12)  # TILE_128x160 (4) is not built
 SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
 TRACE_RE = re.compile(r"\[di_gemm\] (.*)")
 

@@ -409,7 +409,7 @@ __device__ __forceinline__ void gemm_tile_stats(const GemmArgs& g, const float* 
 // ---- the GEMM kernel ----
 template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D, int KS,
           int EX>
-__global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
   static_assert(EX == EX_NONE || (FAST && AM == A_DENSE), "epilogue extras: dense fast path");
   using MT = Mfma<T>;
   constexpr int KV = MT::KV;
@@ -419,20 +419,27 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
   // chunk position XOR-swizzled by (row >> 1) & 7: the 8 lanes writing one row
   // and the 16 lanes reading one fragment column (16 rows) hit distinct banks.
   constexpr int LDK = BK;
-  // KS = 2: eight wavefronts, two per output wave tile, each computing half
-  // of every stage's k steps (the halves are summed through LDS at the end).
-  // A lone workgroup per CU then still has two waves per SIMD, which lets
-  // LDS reads of one overlap MFMAs of the other.
-  constexpr int NT = 256 * KS;         // threads
-  constexpr int NVA = BM * VPR / NT;   // A vectors per thread per stage
-  constexpr int NVB = BN * VPR / NT;
+  // WGM x WGN output wave tiles (4 or 8).  KS = 2: two wavefronts per output
+  // wave tile, each computing half of every stage's k steps (the halves are
+  // summed through LDS at the end).  A lone workgroup per CU then still has
+  // two (4 tiles) or four (8 tiles) waves per SIMD, so LDS reads and barrier
+  // waits of one wave overlap the MFMAs of another.
+  constexpr int NWQ = WGM * WGN;
+  constexpr int NT = 64 * NWQ * KS;    // threads
+  // A / B vectors per thread per stage; when a tile has fewer vectors than
+  // threads, the first BM * VPR (BN * VPR) threads - whole wavefronts - load
+  constexpr int NVA = (BM * VPR + NT - 1) / NT;
+  constexpr int NVB = (BN * VPR + NT - 1) / NT;
+  constexpr bool A_PART = NVA * NT != BM * VPR, B_PART = NVB * NT != BN * VPR;
   constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
   constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int KSTEPS = BK / MT::KM;  // MFMA k steps per stage
-  static_assert(WGM * WGN == 4, "4 wavefronts per k half");
+  static_assert(NWQ == 4 || NWQ == 8, "4 or 8 wavefronts per k half");
   static_assert(KS == 1 || (FAST && KSTEPS % KS == 0), "k halves: fast path, whole k steps");
   static_assert(NVA >= 1 && NVB >= 1 && TM >= 1 && TN >= 1, "tile too small");
-  static_assert(NVA * NT == BM * VPR && NVB * NT == BN * VPR, "whole vectors per thread");
+  static_assert((!A_PART || (FAST && NVA == 1 && BM * VPR % 64 == 0)) &&
+                    (!B_PART || (FAST && NVB == 1 && BN * VPR % 64 == 0)),
+                "partial vector loads: fast path, whole wavefronts");
 
   // Pipeline buffers sA[2][BM*LDK], sB[2][BN*LDK]; reused by the fp32 C tile
   // of the vector epilogue.
@@ -449,7 +456,8 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
   };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wq = wave & 3, kh = wave >> 2;  // output wave tile, k half
+  const int wq = wave % NWQ, kh = wave / NWQ;  // output wave tile, k half
+  const bool a_ld = !A_PART || tid < BM * VPR, b_ld = !B_PART || tid < BN * VPR;
   const int wm0 = (wq / WGN) * WM, wn0 = (wq % WGN) * WN;
 
   // Tile order: N fastest, so consecutive tiles share A rows.  Workgroups are
@@ -483,7 +491,7 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
   for (int i = 0; i < NVA; i++) {
     uint32_t r = (tid + i * NT) / VPR;
     uint32_t m = m0 + r;
-    a_row_ok[i] = m < g.M;
+    a_row_ok[i] = a_ld && m < g.M;
     if constexpr (AM == A_DENSE) {
       a_row_off[i] = (int64_t)m;
       a_iy0[i] = a_ix0[i] = 0;
@@ -525,14 +533,14 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
     for (int i = 0; i < NVA; i++) {
       const uint32_t m = m0 + (tid + i * NT) / VPR;
       // row base + this thread's k chunk at k_begin; stages add a scalar offset
-      fa1[i] = m < g.M ? m * (uint32_t)g.lda * 2u + (k_begin + kc * KV) * 2u : kInv;
-      fa2[i] = m < g.M ? m * (uint32_t)g.lda2 * 2u : kInv;
+      fa1[i] = a_row_ok[i] ? m * (uint32_t)g.lda * 2u + (k_begin + kc * KV) * 2u : kInv;
+      fa2[i] = a_row_ok[i] ? m * (uint32_t)g.lda2 * 2u : kInv;
       fimg[i] = (uint32_t)a_row_off[i] * g.H;
     }
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
       const uint32_t n = n0 + (tid + i * NT) / VPR;
-      fb[i] = n < g.N ? n * (uint32_t)g.ldb * 2u + (k_begin + kc * KV) * 2u : kInv;
+      fb[i] = b_ld && n < g.N ? n * (uint32_t)g.ldb * 2u + (k_begin + kc * KV) * 2u : kInv;
     }
     if constexpr (AM == A_CONV_NHWC) {
       const uint32_t tap0 = k_begin / g.Cin;
@@ -646,10 +654,11 @@ __global__ __launch_bounds__(256 * KS) void k_gemm(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < NVA; i++) {
       uint32_t r = (tid + i * NT) / VPR;
-      *(typename MT::vec*)&sA[buf][lds_at(r, kc * KV)] = st.a[i];
+      if (a_ld) *(typename MT::vec*)&sA[buf][lds_at(r, kc * KV)] = st.a[i];
     }
 #pragma unroll
     for (int i = 0; i < NVB; i++) {
+      if (!b_ld) break;
       if constexpr (BMD == B_NK) {
         uint32_t r = (tid + i * NT) / VPR;
         *(typename MT::vec*)&sB[buf][lds_at(r, kc * KV)] = st.b[i];
@@ -1142,7 +1151,7 @@ template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FA
 void launch_cfg(const GemmArgs& g, hipStream_t s) {
   uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D, KS, EX>
-      <<<dim3(tiles, 1, g.batch * g.splits), 256 * KS, 0, s>>>(g);
+      <<<dim3(tiles, 1, g.batch * g.splits), 64 * WGM * WGN * KS, 0, s>>>(g);
 }
 
 // Generic (bounds-checked) variants: two tile shapes.
@@ -1150,7 +1159,8 @@ template <typename T, int AM, int BMD>
 void launch_slow(const GemmArgs& g, int tile_cfg, hipStream_t s) {
   if (tile_cfg == TILE_64x64 || tile_cfg == TILE_128x64 || tile_cfg == TILE_64x128 ||
       tile_cfg == TILE_64x160 || tile_cfg == TILE_64x64_K2 || tile_cfg == TILE_128x64_K2 ||
-      tile_cfg == TILE_64x128_K2)
+      tile_cfg == TILE_64x128_K2 || tile_cfg == TILE_64x128_W16 || tile_cfg == TILE_128x64_W16 ||
+      tile_cfg == TILE_64x64_W16)
     launch_cfg<T, 64, 64, 2, 2, AM, BMD, false>(g, s);
   else
     launch_cfg<T, 128, 128, 2, 2, AM, BMD, false>(g, s);
@@ -1167,6 +1177,10 @@ void launch_fast_d(const GemmArgs& g, int tile_cfg, hipStream_t s) {
     case TILE_64x64_K2: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
     case TILE_128x64_K2: launch_cfg<f16, 128, 64, 2, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
     case TILE_64x128_K2: launch_cfg<f16, 64, 128, 2, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
+    case TILE_64x128_W16: launch_cfg<f16, 64, 128, 2, 4, AM, B_NK, true, D, 2, EX>(g, s); break;
+    case TILE_128x64_W16: launch_cfg<f16, 128, 64, 4, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
+    case TILE_128x128_W16: launch_cfg<f16, 128, 128, 2, 4, AM, B_NK, true, D, 2, EX>(g, s); break;
+    case TILE_64x64_W16: launch_cfg<f16, 64, 64, 2, 4, AM, B_NK, true, D, 2, EX>(g, s); break;
     default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D, 1, EX>(g, s); break;
   }
 }
@@ -1181,11 +1195,12 @@ void launch_fast(const GemmArgs& g, int tile_cfg, int depth, hipStream_t s) {
   else launch_fast_d<AM, 2>(g, tile_cfg, s);
 }
 
-const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64, 64, 128, 64};
-const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160, 64, 64, 128};
+const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64, 64, 128, 64, 64, 128, 128, 64};
+const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160, 64, 64, 128, 128, 64, 128, 64};
 // Relative per-CU MFMA efficiency of each tile shape (the 2x2 wavefront tile
 // sets LDS bytes per MFMA cycle); tuned by measurement.
-const double kTileEff[TILE_COUNT] = {0.35, 0.5, 0.5, 0.8, 0.85, 0.55, 0.35, 0.5, 0.5};
+const double kTileEff[TILE_COUNT] = {0.35, 0.5, 0.5, 0.8, 0.85, 0.55, 0.35, 0.5, 0.5,
+                                      0.5, 0.5, 0.8, 0.35};
 
 }  // namespace
 
@@ -1238,6 +1253,7 @@ GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
   double best_t = 1e300;
   for (int tc = 0; tc < TILE_COUNT; tc++) {
     if (tc == TILE_128x160) continue;  // spills registers: not built
+    if (tc >= TILE_64x128_W16) continue;  // sixteen-wave tiles: measured table only
     if (g.act == ACT_GEGLU && kTileN[tc] == 160) continue;  // GEGLU pairs need even TN
     const uint64_t mt = (g.M + kTileM[tc] - 1) / kTileM[tc], nt = (g.N + kTileN[tc] - 1) / kTileN[tc];
     const uint64_t T = mt * nt * g.batch;
