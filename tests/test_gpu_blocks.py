@@ -66,6 +66,7 @@ def _tf_sd(rng, p, c, cross):
     (1, 320, 640, 32, 32, True),    # cfg3: SD2.1 ResNet 320->640 @32x32 with temb + 1x1 skip
     (1, 1280, 1280, 16, 16, False), # fused-resnet.js SHAPE (no temb, identity skip)
     (2, 640, 640, 16, 16, True),    # batch 2
+    (1, 1280, 1280, 8, 8, True),    # 8x8: split-K conv1 with GroupNorm in the reducer
 ])
 def test_resnet_block(dev, rng, B, cin, cout, H, W, temb):
     from drawinstant import blocks
