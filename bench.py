@@ -21,6 +21,9 @@ HIP events on the library's stream over exactly K graph-replayed steps
   scaled by FLOPs to ms per step.  Skipped with --no-cpu.
 * `blocks` (unless --no-blocks): per-config figures (cfg1 GN+SiLU HBM GB/s,
   cfg2 conv / cfg3 ResNet / cfg4 transformer / self-attention MFMA %).
+* `denoise_loop`: the 4-step SD-Turbo loop (noise, scaleModelInput, U-Net,
+  Euler update) entirely on the device, host wall time including the final
+  wait.
 """
 import argparse
 import json
@@ -75,6 +78,31 @@ def bench_unet(dev, args):
     out = dev.download(bo, np.float32, x.shape)
     finite = bool(np.isfinite(out).all())
     return u, ms, wall, eager, finite, (x, ctx)
+
+
+def bench_denoise(dev, u, ctx, steps=4, reps=5):
+    """The SD-Turbo denoise loop (pipeline.js:274-288) on the device: noise,
+    then per step scaleModelInput -> U-Net (graph) -> Euler update (scheduler
+    kernels, no host round trip).  HIP events around each whole loop; median
+    of `reps`; `scheduler_us_per_step` = loop time per step minus the bare
+    graph step time of the headline measurement."""
+    from drawinstant import scheduler as S
+    bc = dev.storage(ctx)
+    lat = dev.create_buffer(4 * 64 * 64 * 4)
+    d = S.Denoiser(u, steps=steps)
+    d.run(bc, lat, seed=0)  # capture with these buffers
+    dev.sync()
+    ts = []
+    for _ in range(reps):
+        ts.append(timed(dev, lambda i: d.run(bc, lat, seed=0), 1))
+    out = dev.download(lat, np.float32)
+    d.destroy()
+    for b in (bc, lat):
+        b.destroy()
+    ts.sort()
+    ms = ts[len(ts) // 2]
+    return {"steps": steps, "ms": round(ms, 4), "ms_per_step": round(ms / steps, 4),
+            "final_latent_finite": bool(np.isfinite(out).all())}
 
 
 def bench_blocks(dev, num_rot=64):
@@ -292,7 +320,10 @@ def main():
         "output_finite": finite,
         "pcie_inclusive_eager_ms_per_step": round(pcie_inclusive(u, inputs), 3),
         "roofline": roofline_conv(dev),
+        "denoise_loop": bench_denoise(dev, u, inputs[1]),
     }
+    line["denoise_loop"]["scheduler_us_per_step"] = round(
+        (line["denoise_loop"]["ms_per_step"] - ms) * 1e3, 1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(u)
     if not args.no_blocks:

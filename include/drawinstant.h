@@ -387,6 +387,26 @@ int32_t di_unet_forward(di_ctx* ctx, di_unet* unet, di_handle sample, di_handle 
                         di_handle context, di_handle out, uint32_t B, uint32_t H,
                         uint32_t W, uint32_t Sctx, int32_t flags);
 
+/* ======================= Euler Discrete scheduler ======================= */
+/* The per-element halves of makeEulerScheduler / sampleNoiseLatent
+ * (scheduler.js:77-134) on the device; the schedule constants (timesteps,
+ * sigmas) stay host scalars, as in the reference.  fp32 tensors of n
+ * elements; each element is a double expression rounded once to fp32, as the
+ * reference's Float32Array stores are. */
+
+/* sampleNoiseLatent (scheduler.js:117-134): seeded LCG (s * 1664525 +
+ * 1013904223, from (seed | 0) || 1) + Box-Muller pairs, times sigma
+ * (initNoiseSigma); n = B * 4 * H * W. */
+int32_t di_noise_latent(di_ctx* ctx, di_handle out, uint64_t n, int32_t seed, double sigma);
+/* scaleModelInput (scheduler.js:95-101): out = latent * inv, inv =
+ * 1 / sqrt(sigma_i^2 + 1). */
+int32_t di_euler_scale(di_ctx* ctx, di_handle latent, di_handle out, uint64_t n, double inv);
+/* step (scheduler.js:105-110): out = latent + dt * pred, dt = sigma_{i+1} -
+ * sigma_i; out may be latent.  next_in != 0 also writes the next step's
+ * scaleModelInput of out with inv_next (fused: one pass per step). */
+int32_t di_euler_step(di_ctx* ctx, di_handle latent, di_handle pred, di_handle out,
+                      di_handle next_in, uint64_t n, double dt, double inv_next);
+
 #ifdef __cplusplus
 }
 #endif
