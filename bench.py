@@ -24,6 +24,9 @@ HIP events on the library's stream over exactly K graph-replayed steps
 * `denoise_loop`: the 4-step SD-Turbo loop (noise, scaleModelInput, U-Net,
   Euler update) entirely on the device, host wall time including the final
   wait.
+* `executor_rewrites` (unless --no-blocks): the op-by-op executor over the
+  exported cfg4 attention and LayerNorm + GELU subgraphs, unfused and after
+  optimize_graph, wall ms per run.
 """
 import argparse
 import json
@@ -195,6 +198,82 @@ def bench_block_chains(dev, u):
     return res
 
 
+def _export_subgraphs(S=4096, H=5, d=64, D=320, F=1280):
+    """The cfg4 (64x64 level) attention and LayerNorm + GELU chains as
+    torch.onnx exports them, for the executor-rewrite leg."""
+    from drawinstant.executor import Attr, Graph, Node, TensorProto
+
+    def tp(a):
+        a = np.ascontiguousarray(a, np.float32)
+        return TensorProto(list(a.shape), "float32", a.tobytes())
+
+    perm = [Attr("perm", ints=[0, 2, 1, 3])]
+    attn = Graph([
+        Node("Transpose", "tq", ["q"], ["qh"], perm),
+        Node("Transpose", "tk", ["k"], ["kh"], [Attr("perm", ints=[0, 2, 3, 1])]),
+        Node("Transpose", "tv", ["v"], ["vh"], perm), Node("MatMul", "qk", ["qh", "kh"], ["s"]),
+        Node("Mul", "sc", ["s", "scale"], ["ss"]),
+        Node("Softmax", "sm", ["ss"], ["p"], [Attr("axis", i=-1)]),
+        Node("MatMul", "pv", ["p", "vh"], ["o"]), Node("Transpose", "to", ["o"], ["y"], perm)],
+        outputs=[{"name": "y"}], tensors={"scale": tp(np.array([d ** -0.5]))})
+    rng = np.random.default_rng(3)
+    rm = [Attr("axes", ints=[-1])]
+    t = {"two": tp([2.0]), "eps": tp([1e-5]), "g": tp(1 + 0.02 * rng.standard_normal(D)),
+         "b": tp(0.02 * rng.standard_normal(D)), "sq2": tp([2 ** 0.5]), "one": tp([1.0]),
+         "half": tp([0.5]), "w": tp(0.03 * rng.standard_normal((D, F)))}
+    ln_gelu = Graph([
+        Node("ReduceMean", "rm1", ["x"], ["mu"], rm), Node("Sub", "sub", ["x", "mu"], ["xc"]),
+        Node("Pow", "pw", ["xc", "two"], ["x2"]), Node("ReduceMean", "rm2", ["x2"], ["var"], rm),
+        Node("Add", "ae", ["var", "eps"], ["ve"]), Node("Sqrt", "sq", ["ve"], ["sd"]),
+        Node("Div", "dv", ["xc", "sd"], ["xn"]), Node("Mul", "mg", ["xn", "g"], ["xg"]),
+        Node("Add", "ab", ["xg", "b"], ["ln"]), Node("MatMul", "ff", ["ln", "w"], ["h"]),
+        Node("Div", "d2", ["h", "sq2"], ["u"]), Node("Erf", "erf", ["u"], ["e"]),
+        Node("Add", "a1", ["e", "one"], ["e1"]), Node("Mul", "mx", ["h", "e1"], ["pg"]),
+        Node("Mul", "mh", ["pg", "half"], ["y"])], outputs=[{"name": "y"}], tensors=t)
+    feeds_attn = {n: rng.standard_normal((1, S, H, d)).astype(np.float32) for n in "qkv"}
+    feeds_ln = {"x": rng.standard_normal((1, S, D)).astype(np.float32)}
+    return (attn, feeds_attn), (ln_gelu, feeds_ln)
+
+
+def bench_executor_rewrites(dev, reps=7):
+    """The executor over exported subgraphs at the cfg4 shapes, op by op
+    (as the reference's executor dispatches them) and after optimize_graph:
+    wall ms per Executor.run (median of `reps`, device-synchronised)."""
+    import copy
+    from drawinstant.executor import Executor, Tensor, WeightCache, optimize_graph
+    res = {}
+    for key, (graph, feeds) in zip(("attention_64x64", "layer_norm_gelu_64x64"),
+                                   _export_subgraphs()):
+        inputs = {k: dev.storage(v) for k, v in feeds.items()}
+        seeds = {k: Tensor(b, list(feeds[k].shape)) for k, b in inputs.items()}
+        row = {}
+        for fused in (False, True):
+            g = copy.deepcopy(graph)
+            if fused:
+                row["rewrites"] = {k: v for k, v in optimize_graph(g).items() if v}
+            wc = WeightCache(dev, g.tensors)
+            ex = Executor(dev, g, wc)
+            ts = []
+            for r in range(reps + 1):
+                t0 = time.perf_counter()
+                outs = ex.run(seeds)
+                dt = (time.perf_counter() - t0) * 1e3
+                for o in outs.values():
+                    o.buf.destroy()
+                if r:
+                    ts.append(dt)
+            ts.sort()
+            row["fused_ms" if fused else "unfused_ms"] = round(ts[len(ts) // 2], 4)
+            row["fused_nodes" if fused else "unfused_nodes"] = len(g.nodes)
+            ex.destroy()
+            wc.destroy()
+        row["speedup"] = round(row["unfused_ms"] / row["fused_ms"], 2)
+        res[key] = row
+        for b in inputs.values():
+            b.destroy()
+    return res
+
+
 ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_gemm_conv3x3_64x64x320_pmc.md")
 
 
@@ -331,6 +410,7 @@ def main():
         blk.update(bench_block_chains(dev, u))
         line["blocks"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                               for kk, vv in v.items()} for k, v in blk.items()}
+        line["executor_rewrites"] = bench_executor_rewrites(dev)
     print(json.dumps(line), flush=True)
 
 

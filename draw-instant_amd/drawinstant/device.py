@@ -18,6 +18,8 @@ F32 = 0
 F16 = 1
 NCHW = 0
 NHWC = 1
+BSHD = 0  # attention layouts
+BHSD = 1
 
 _NP_DT = {F32: np.float32, F16: np.float16}
 _DT_OF = {np.dtype(np.float32): F32, np.dtype(np.float16): F16}

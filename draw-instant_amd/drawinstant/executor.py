@@ -10,10 +10,18 @@ Mirrors, name for name (snake_case), the reference's executor contract:
 * ``BufferPool`` (:62-94): acquire/release by 4 KiB-rounded size with
   live / peak / allocs statistics, over ``di_alloc`` / ``di_free``.
 * ``OPS`` (:96-1114): ``OPS[op_type](ctx, node, inputs) -> tensor`` for the
-  37 op types of the reference, each GPU op one C-ABI call (shapes as scalars
-  instead of uniform buffers).  Activations are fp32 NCHW, as in the reference.
+  37 op types of the reference (plus the three ops the fusing rewrites
+  insert), each GPU op one C-ABI call (shapes as scalars instead of uniform
+  buffers).  Activations are fp32 NCHW, as in the reference.
 * graph rewrites ``fuse_silu_pattern`` (:799-839), ``fuse_mul_add_pattern``
-  (:845-898), ``fuse_group_norm_pattern`` (:905-1008).
+  (:845-898), ``fuse_group_norm_pattern`` (:905-1008), and four that map
+  exported subgraphs onto the library's fused kernels, which the reference
+  runs op by op: ``fuse_group_norm_silu_pattern`` (GroupNorm -> SiLU, one
+  dispatch), ``fuse_layer_norm_pattern`` (the 8-9 op LayerNorm decomposition
+  -> ``LayerNormalization``), ``fuse_gelu_pattern`` (Div/Erf/Add/Mul/Mul ->
+  ``Gelu``) and ``fuse_attention_pattern`` (MatMul -> scale -> Softmax ->
+  MatMul, with its head-split Transposes, -> ``FusedAttention``, flash
+  attention without the score matrix); ``optimize_graph`` runs them all.
 * ``plan_execution`` (:1157-1170), ``create_dispatchers`` (:1174-1197),
   ``infer_graph_io`` (:1205-1221), ``Executor.run`` (:1223-1466) with the
   same input-seeding, CPU promotion, consumer counting, output snapshot and
@@ -38,7 +46,7 @@ from typing import Any, Callable, Dict, List, Optional
 
 import numpy as np
 
-from .device import F32, NCHW, Buffer, Device, call
+from .device import BHSD, BSHD, F32, NCHW, Buffer, Device, call
 
 # ---------------------------------------------------------------- logging --
 LOG = {"verbose": False, "node_count": 0, "op_hist": {}, "t0": 0.0, "profile": False,
@@ -238,7 +246,7 @@ class WeightCache:
 
 # ------------------------------------------------------------- dispatchers --
 UNARY_CODE = {"Sigmoid": 0, "Sqrt": 1, "Neg": 2, "Abs": 3, "Sin": 4, "Cos": 5, "Exp": 6, "Log": 7,
-              "SiLU": 8, "GELU": 9, "Erf": 10}
+              "SiLU": 8, "GELU": 9, "Erf": 10, "GELU_TANH": 11}
 BINARY_CODE = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Pow": 4, "Max": 5, "Min": 6}
 
 
@@ -298,6 +306,9 @@ class Dispatchers:
         self.slice = lambda x, y, rank, dims, strides, start, n: call(
             "di_slice", ctx, x.handle, y.handle, rank, _u32x4(dims), _u32x4(strides),
             _u32x4(start), n, F32)
+        self.attention = lambda q, k, v, o, b, h, sq, skv, d, layout, scale: call(
+            "di_attn_cross", ctx, q.handle, k.handle, v.handle, o.handle, b, h, sq, skv, d,
+            layout, scale, F32)
         self.affine_bcast = lambda x, g, b, y, rank, dims, sx, sg, n: call(
             "di_affine_bcast", ctx, x.handle, g.handle, b.handle, y.handle, rank, _u32x4(dims),
             _u32x4(sx), _u32x4(sg), n, F32)
@@ -782,8 +793,12 @@ def _group_norm(ctx, node, inputs):
     if C % G:
         raise ValueError(f"GroupNorm: C={C} not divisible by G={G}")
     eps = get_attr_float(node, "epsilon", 1e-5)
+    act = get_attr_string(node, "activation", "")
+    if act not in ("", "silu"):
+        raise ValueError(f"GroupNorm {node.name}: activation {act!r}")
     out = ctx.pool.acquire(N * C * HW * 4)
-    ctx.dispatchers.group_norm(x.buf, g.buf, b.buf, out, N, G, C // G, HW, eps)
+    ctx.dispatchers.group_norm(x.buf, g.buf, b.buf, out, N, G, C // G, HW, eps,
+                               1 if act == "silu" else 0)
     return Tensor(out, list(x.dims))
 
 
@@ -899,6 +914,132 @@ def _resize(ctx, node, inputs):
     out = ctx.pool.acquire(N * C * Ho * Wo * 4)
     ctx.dispatchers.resize_nearest(x.buf, out, N * C, H, W, Ho, Wo)
     return Tensor(out, [N, C, Ho, Wo])
+
+
+# --------------------------------------------- ops inserted by the rewrites --
+def _on_device(ctx, t):
+    return t if t is None or getattr(t, "buf", None) is not None else ctx.promote(t)
+
+
+@_op("Gelu")
+def _gelu(ctx, node, inputs):
+    """ONNX Gelu (inserted by fuse_gelu_pattern): the erf form through the
+    same Abramowitz-Stegun erf as OPS.Erf, or approximate="tanh"."""
+    x = _on_device(ctx, inputs[0])
+    approx = get_attr_string(node, "approximate", "none")
+    if approx not in ("none", "tanh"):
+        raise ValueError(f"Gelu: approximate={approx!r}")
+    out = ctx.pool.acquire(x.byte_length)
+    ctx.dispatchers.unary["GELU" if approx == "none" else "GELU_TANH"](x.buf, out, x.numel)
+    return Tensor(out, list(x.dims))
+
+
+@_op("LayerNormalization")
+def _layer_norm(ctx, node, inputs):
+    """ONNX LayerNormalization over the last axis (inserted by
+    fuse_layer_norm_pattern): one di_layer_norm dispatch (layerNorm,
+    wgsl-ops.js:772-812).  Absent gamma / beta mean 1 / 0."""
+    x = _on_device(ctx, inputs[0])
+    g = _on_device(ctx, inputs[1]) if len(inputs) > 1 else None
+    b = _on_device(ctx, inputs[2]) if len(inputs) > 2 else None
+    rank = len(x.dims)
+    axis = get_attr_int(node, "axis", -1)
+    if rank < 1 or (axis + rank if axis < 0 else axis) != rank - 1:
+        raise ValueError(f"LayerNormalization: only the last axis is supported, got axis={axis} "
+                         f"dims={x.dims}")
+    inner = x.dims[-1]
+    if g is None:
+        g = ctx.promote(CpuTensor(np.ones(inner, np.float32), [inner], "float32", False))
+    if b is None:
+        b = ctx.promote(CpuTensor(np.zeros(inner, np.float32), [inner], "float32", False))
+    if g.numel != inner or b.numel != inner:
+        raise ValueError(f"LayerNormalization: gamma {g.dims} / beta {b.dims} do not match the "
+                         f"normalised dim {inner}")
+    out = ctx.pool.acquire(x.byte_length)
+    ctx.dispatchers.layer_norm(x.buf, g.buf, b.buf, out, x.numel // inner, inner,
+                               get_attr_float(node, "epsilon", 1e-5))
+    return Tensor(out, list(x.dims))
+
+
+ATTN_HEAD_DIM = 64  # the flash kernel's head dim
+
+
+def _attention_unfused(ctx, q, k, v, scale, k_transposed, axis):
+    """The chain the rewrite replaced, op by op: MatMul(Q, K^T) -> * scale ->
+    Softmax -> MatMul(., V)."""
+    tmp = []
+    if not k_transposed:
+        perm = list(range(len(k.dims)))
+        perm[-2], perm[-1] = perm[-1], perm[-2]
+        k = OPS["Transpose"](ctx, Node("Transpose", "", [], [], [Attr("perm", ints=perm)]), [k])
+        tmp.append(k)
+    s = OPS["MatMul"](ctx, Node("MatMul"), [q, k])
+    tmp.append(s)
+    if scale != 1.0:
+        s = OPS["Mul"](ctx, Node("Mul"), [s, CpuTensor(np.array([scale], np.float32), [1],
+                                                          "float32", False)])
+        tmp.append(s)
+    p = OPS["Softmax"](ctx, Node("Softmax", "", [], [], [Attr("axis", i=axis)]), [s])
+    tmp.append(p)
+    o = OPS["MatMul"](ctx, Node("MatMul"), [p, v])
+    for t in tmp:  # the stream is in order: later work may reuse these at once
+        ctx.pool.release(t.buf)
+    return o
+
+
+@_op("FusedAttention")
+def _fused_attention(ctx, node, inputs):
+    """softmax(Q K^T * scale) V (inserted by fuse_attention_pattern) through
+    di_attn_cross (WGSL_FUSED_ATTN fused-attn.js:199-307, WGSL_FUSED
+    fused-cross-attn.js:112-173).  layout "bhsd": Q [.., Sq, 64], K
+    [.., Skv, 64] (K^T [.., 64, Skv] with k_transposed), V [.., Skv, 64] with
+    equal leading dims, which run as heads; layout "bshd": Q [B, Sq, H, 64],
+    K / V [B, Skv, H, 64].  Other shapes run the unfused chain."""
+    q, k, v = (_on_device(ctx, t) for t in inputs[:3])
+    scale = get_attr_float(node, "scale", 1.0)
+    kt = get_attr_int(node, "k_transposed", 1)
+    axis = get_attr_int(node, "softmax_axis", -1)
+    rank = len(q.dims)
+    last_axis = (axis + rank if axis < 0 else axis) == rank - 1
+    d = q.dims[-1] if rank else 0
+    if get_attr_string(node, "layout", "bhsd") == "bshd":
+        ok = kt == 0 and rank == 4 and len(k.dims) == 4 and len(v.dims) == 4 and last_axis and \
+            q.dims[0] == k.dims[0] == v.dims[0] and q.dims[2] == k.dims[2] == v.dims[2] and \
+            k.dims[1] == v.dims[1] and d == k.dims[3] == v.dims[3] == ATTN_HEAD_DIM and \
+            q.dims[1] > 0 and k.dims[1] > 0
+        if not ok:
+            heads = Node("Transpose", "", [], [], [Attr("perm", ints=[0, 2, 1, 3])])
+            qh, kh, vh = (OPS["Transpose"](ctx, heads, [t]) for t in (q, k, v))
+            oh = _attention_unfused(ctx, qh, kh, vh, scale, kt, axis)
+            out = OPS["Transpose"](ctx, heads, [oh])
+            for t in (qh, kh, vh, oh):
+                ctx.pool.release(t.buf)
+            return out
+        B, Sq, H, _ = q.dims
+        out = ctx.pool.acquire(q.numel * 4)
+        ctx.dispatchers.attention(q.buf, k.buf, v.buf, out, B, H, Sq, k.dims[1], d, BSHD, scale)
+        return Tensor(out, list(q.dims))
+    ok = rank >= 2 and len(k.dims) == rank and len(v.dims) == rank and \
+        q.dims[:-2] == k.dims[:-2] == v.dims[:-2] and last_axis
+    if ok:
+        Skv = k.dims[-1] if kt else k.dims[-2]
+        ok = d == ATTN_HEAD_DIM and (k.dims[-2] if kt else k.dims[-1]) == d and \
+            v.dims[-2] == Skv and v.dims[-1] == ATTN_HEAD_DIM and q.dims[-2] > 0 and Skv > 0
+    if not ok:
+        return _attention_unfused(ctx, q, k, v, scale, kt, axis)
+    heads = int(np.prod(q.dims[:-2])) if rank > 2 else 1
+    Sq = q.dims[-2]
+    k_buf, tmp = k.buf, None
+    if kt:
+        tmp = ctx.pool.acquire(heads * Skv * d * 4)
+        ctx.dispatchers.transpose(k.buf, tmp, 3, [heads, Skv, d, 1], [d * Skv, Skv, 1, 0],
+                                  [0, 2, 1, 0], heads * Skv * d)
+        k_buf = tmp
+    out = ctx.pool.acquire(heads * Sq * d * 4)
+    ctx.dispatchers.attention(q.buf, k_buf, v.buf, out, 1, heads, Sq, Skv, d, BHSD, scale)
+    if tmp is not None:
+        ctx.pool.release(tmp)
+    return Tensor(out, list(q.dims))
 
 
 # ---------------------------------------------------------- graph rewrites --
@@ -1069,6 +1210,367 @@ def fuse_group_norm_pattern(graph: Graph) -> dict:
     if fused:
         graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
     return {"fused": fused}
+
+
+def _const_value(graph: Graph, producer: dict, name: str) -> Optional[float]:
+    """The value of a one-element initializer or Constant-node output of rank
+    <= 1 (an exported scalar; larger constants could broadcast the result to
+    a bigger shape, which the fused ops do not reproduce)."""
+    init = graph.tensors.get(name) if graph.tensors else None
+    if init is None or init.data is None:
+        pi = producer.get(name)
+        if pi is None or graph.nodes[pi].op_type != "Constant":
+            return None
+        a = _attr(graph.nodes[pi], "value")
+        init = a.t if a is not None else None
+        if init is None or init.data is None:
+            return None
+    if len(init.dims) > 1 or int(np.prod(init.dims or [1])) != 1:
+        return None
+    return _uniform_value(init)
+
+
+def _scalar_operand(graph: Graph, producer: dict, node: Node):
+    """(other input, constant) when one of a binary node's two inputs is a
+    uniform constant; for Div only the divisor may be the constant."""
+    a, b = (node.inputs + [None, None])[:2]
+    if not a or not b:
+        return None
+    cb = _const_value(graph, producer, b)
+    if cb is not None:
+        return a, cb
+    if node.op_type in ("Add", "Mul"):
+        ca = _const_value(graph, producer, a)
+        if ca is not None:
+            return b, ca
+    return None
+
+
+def _near(v: Optional[float], want: float, tol: float = 1e-6) -> bool:
+    return v is not None and abs(v - want) <= tol * max(1.0, abs(want))
+
+
+def fuse_gelu_pattern(graph: Graph) -> dict:
+    """Div(X, sqrt 2) -> Erf -> Add(., 1) -> Mul(X, .) -> Mul(., 0.5) => Gelu(X),
+    the erf GELU as torch.onnx exports it and as the decomposition the
+    reference's executor runs op by op (OPS.Div/Erf/Add/Mul, wgsl-executor.js
+    :587-706; GELU = x * 0.5 * (1 + erf(x / sqrt 2)), wgsl-ops.js:77-81).  A
+    Mul by 1/sqrt 2 stands for the Div, and the 0.5 may instead scale X first
+    (Mul(Mul(X, 0.5), 1 + erf)).  Every intermediate must have the chain as its
+    only consumer."""
+    nodes = graph.nodes
+    consumers, producer = _consumers_and_producers(graph)
+
+    def only(name, op):
+        if consumers.get(name, 0) != 1:
+            return None
+        pi = producer.get(name)
+        return pi if pi is not None and nodes[pi].op_type == op else None
+
+    drop, fused = set(), 0
+    for i, last in enumerate(nodes):
+        if last.op_type != "Mul" or i in drop:
+            continue
+        cands = []  # (x, name of 1 + erf(...), index of the other Mul)
+        so = _scalar_operand(graph, producer, last)
+        if so is not None:
+            mi = only(so[0], "Mul") if _near(so[1], 0.5) else None
+            if mi is not None:
+                ma, mb = nodes[mi].inputs[:2]
+                cands = [(ma, mb, mi), (mb, ma, mi)]
+        else:
+            la, lb = last.inputs[:2]
+            for h, a_out in ((la, lb), (lb, la)):
+                hi = only(h, "Mul")
+                ho = _scalar_operand(graph, producer, nodes[hi]) if hi is not None else None
+                if ho is not None and _near(ho[1], 0.5):
+                    cands.append((ho[0], a_out, hi))
+        for x, a_out, mi in cands:
+            ai = only(a_out, "Add")
+            ao = _scalar_operand(graph, producer, nodes[ai]) if ai is not None else None
+            if ao is None or not _near(ao[1], 1.0):
+                continue
+            ei = only(ao[0], "Erf")
+            if ei is None:
+                continue
+            d_out = nodes[ei].inputs[0]
+            di = producer.get(d_out)
+            if di is None or consumers.get(d_out, 0) != 1:
+                continue
+            dn = nodes[di]
+            do = _scalar_operand(graph, producer, dn) if dn.op_type in ("Div", "Mul") else None
+            if do is None or do[0] != x:
+                continue
+            if not ((dn.op_type == "Div" and _near(do[1], math.sqrt(2.0))) or
+                    (dn.op_type == "Mul" and _near(do[1], 1.0 / math.sqrt(2.0)))):
+                continue
+            nodes[i] = Node("Gelu", (last.name or "") + "_gelu", [x], list(last.outputs),
+                            [Attr("approximate", s="none")])
+            drop.update((mi, ai, ei, di))
+            fused += 1
+            break
+    if fused:
+        graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
+    return {"fused": fused}
+
+
+def _last_axis_attr(node: Node) -> Optional[int]:
+    axes = get_attr_ints(node, "axes", None)
+    if axes is None or len(axes) != 1 or get_attr_int(node, "keepdims", 1) != 1:
+        return None
+    return int(axes[0])
+
+
+def fuse_layer_norm_pattern(graph: Graph) -> dict:
+    """The exported LayerNorm decomposition ReduceMean(X) -> Sub(X, mean) ->
+    Pow(., 2) -> ReduceMean -> Add(., eps) -> Sqrt -> Div(X - mean, .) [->
+    Mul(., gamma) -> Add(., beta) | AffineBcast(., gamma, beta)] =>
+    LayerNormalization(X, gamma, beta) over the last axis, one di_layer_norm
+    dispatch instead of the 8-9 the reference's executor issues
+    (OPS.ReduceMean/Sub/Pow/Add/Sqrt/Div, wgsl-executor.js:491-706; the
+    fused form is layerNorm, wgsl-ops.js:772-812).  Both ReduceMeans reduce
+    the same single axis with keepdims; gamma / beta must be initializers
+    whose dims are 1 except the last."""
+    nodes = graph.nodes
+    consumers, producer = _consumers_and_producers(graph)
+
+    def prod(name, op, uses=1):
+        if consumers.get(name, 0) != uses:
+            return None
+        pi = producer.get(name)
+        return pi if pi is not None and nodes[pi].op_type == op else None
+
+    def vec_param(name):
+        t = graph.tensors.get(name) if graph.tensors else None
+        return t is not None and t.data is not None and len(t.dims) >= 1 and \
+            all(d == 1 for d in t.dims[:-1])
+
+    drop, fused = set(), 0
+    for i, dv in enumerate(nodes):
+        if dv.op_type != "Div" or i in drop or len(dv.inputs) < 2:
+            continue
+        xc, sd = dv.inputs[:2]
+        si = prod(sd, "Sqrt")
+        if si is None:
+            continue
+        ai = prod(nodes[si].inputs[0], "Add")
+        if ai is None:
+            continue
+        ao = _scalar_operand(graph, producer, nodes[ai])
+        if ao is None or ao[1] < 0:
+            continue
+        v_out, eps = ao
+        r2 = prod(v_out, "ReduceMean")
+        if r2 is None:
+            continue
+        pw = prod(nodes[r2].inputs[0], "Pow")
+        if pw is None or nodes[pw].inputs[0] != xc:
+            continue
+        if not _near(_const_value(graph, producer, nodes[pw].inputs[1]), 2.0, 0.0):
+            continue
+        sb = prod(xc, "Sub", uses=2)
+        if sb is None:
+            continue
+        x, mu = nodes[sb].inputs[:2]
+        r1 = prod(mu, "ReduceMean")
+        if r1 is None or nodes[r1].inputs[0] != x:
+            continue
+        ax1, ax2 = _last_axis_attr(nodes[r1]), _last_axis_attr(nodes[r2])
+        if ax1 is None or ax1 != ax2:
+            continue
+        # optional affine tail
+        xn = dv.outputs[0]
+        tail, gamma, beta, out = [], None, None, xn
+        if consumers.get(xn, 0) == 1:
+            ci = next((k for k, n in enumerate(nodes) if xn in n.inputs), None)
+            cn = nodes[ci] if ci is not None else None
+            if cn is not None and cn.op_type == "AffineBcast" and cn.inputs[0] == xn and \
+                    vec_param(cn.inputs[1]) and vec_param(cn.inputs[2]):
+                tail, gamma, beta, out = [ci], cn.inputs[1], cn.inputs[2], cn.outputs[0]
+            elif cn is not None and cn.op_type == "Mul":
+                g = cn.inputs[1] if cn.inputs[0] == xn else cn.inputs[0]
+                mo = cn.outputs[0]
+                ad = next((k for k, n in enumerate(nodes) if mo in n.inputs), None) \
+                    if consumers.get(mo, 0) == 1 else None
+                if vec_param(g) and ad is not None and nodes[ad].op_type == "Add":
+                    an = nodes[ad]
+                    b = an.inputs[1] if an.inputs[0] == mo else an.inputs[0]
+                    if vec_param(b):
+                        tail, gamma, beta, out = [ci, ad], g, b, an.outputs[0]
+        ins = [x, gamma or "", beta or ""]
+        fused_node = Node("LayerNormalization", (dv.name or "") + "_ln", ins, [out],
+                          [Attr("axis", i=ax1), Attr("epsilon", f=float(eps))])
+        keep = tail[-1] if tail else i
+        nodes[keep] = fused_node
+        drop.update(k for k in (r1, sb, pw, r2, ai, si, i, *tail) if k != keep)
+        fused += 1
+    if fused:
+        graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
+    return {"fused": fused}
+
+
+def fuse_group_norm_silu_pattern(graph: Graph) -> dict:
+    """GroupNorm -> Silu => GroupNorm with the SiLU epilogue (the
+    WGSL_FUSED_GN_SILU kernel, fused-resnet.js:121-166, one dispatch instead
+    of two).  Run after fuse_silu_pattern and fuse_group_norm_pattern."""
+    nodes = graph.nodes
+    consumers, producer = _consumers_and_producers(graph)
+    drop, fused = set(), 0
+    for i, sl in enumerate(nodes):
+        if sl.op_type != "Silu":
+            continue
+        g_out = sl.inputs[0]
+        gi = producer.get(g_out)
+        if gi is None or consumers.get(g_out, 0) != 1 or nodes[gi].op_type != "GroupNorm" or \
+                get_attr_string(nodes[gi], "activation", "") == "silu":
+            continue
+        gn = nodes[gi]
+        nodes[i] = Node("GroupNorm", (gn.name or "") + "_silu", list(gn.inputs), list(sl.outputs),
+                        list(gn.attributes) + [Attr("activation", s="silu")])
+        drop.add(gi)
+        fused += 1
+    if fused:
+        graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
+    return {"fused": fused}
+
+
+def fuse_attention_pattern(graph: Graph) -> dict:
+    """MatMul(Q, K^T) [-> Mul / Div by a constant] -> Softmax(last axis) ->
+    MatMul(., V) => FusedAttention(Q, K, V): flash attention through
+    di_attn_cross, so the [.., Sq, Skv] score matrix the reference's executor
+    materialises (OPS.MatMul + OPS.Softmax, wgsl-executor.js:1027-1054) is
+    never written.  Scalar Muls on Q or on K^T (torch's SDPA export splits
+    the scale over both) fold into the scale attribute, and a single-use
+    Transpose producing K^T gets its last two perm entries swapped so it
+    yields K directly.  When Q, K and V come from [B, S, H, d] through
+    single-use head-split Transposes (perm 0,2,1,3; for K^T composed with the
+    last-axes swap) and the output goes through the inverse one, those
+    Transposes go too and the node reads and writes [B, S, H, d]
+    (layout="bshd", the fused-attn.js layout).
+
+    The fused node runs head dim 64 with fp16 MFMA operands (fp32 softmax
+    state and accumulation), so its outputs agree with the fp32 chain to
+    about 1e-3 relative RMS, not bit for bit; other shapes run the unfused
+    chain (MatMul, scale, Softmax, MatMul) inside the node."""
+    nodes = graph.nodes
+    consumers, producer = _consumers_and_producers(graph)
+
+    def single(name, ops):
+        if consumers.get(name, 0) != 1:
+            return None
+        pi = producer.get(name)
+        return pi if pi is not None and nodes[pi].op_type in ops else None
+
+    def trace_transposes(name):
+        """(source, composed perm or None, node indices) of the chain of
+        single-use Transposes producing `name`."""
+        perm, idx = None, []
+        while True:
+            ti = single(name, ("Transpose",))
+            p = get_attr_ints(nodes[ti], "perm", None) if ti is not None else None
+            if not p or len(p) != 4:
+                return name, perm, idx
+            perm = list(p) if perm is None else [p[j] for j in perm]
+            idx.append(ti)
+            name = nodes[ti].inputs[0]
+
+    def consumer_of(name):
+        if consumers.get(name, 0) != 1:
+            return None
+        return next((k for k, n in enumerate(nodes) if name in n.inputs), None)
+
+    HEADS = [0, 2, 1, 3]
+    drop, fused = set(), 0
+    for i, sm in enumerate(nodes):
+        if sm.op_type != "Softmax" or i in drop:
+            continue
+        p = sm.outputs[0]
+        if consumers.get(p, 0) != 1:
+            continue
+        pv = next((k for k, n in enumerate(nodes) if n.op_type == "MatMul" and n.inputs and
+                   n.inputs[0] == p), None)
+        if pv is None:
+            continue
+        scale, s_in, used = 1.0, sm.inputs[0], [i]
+        si = single(s_in, ("Mul", "Div"))
+        if si is not None:
+            so = _scalar_operand(graph, producer, nodes[si])
+            if so is None or so[1] == 0:
+                continue
+            scale *= so[1] if nodes[si].op_type == "Mul" else 1.0 / so[1]
+            s_in = so[0]
+            used.append(si)
+        qk = single(s_in, ("MatMul",))
+        if qk is None:
+            continue
+        used.append(qk)
+        q, kt = nodes[qk].inputs[:2]
+        for which in (0, 1):
+            name = q if which == 0 else kt
+            mi = single(name, ("Mul",))
+            if mi is None:
+                continue
+            so = _scalar_operand(graph, producer, nodes[mi])
+            if so is None:
+                continue
+            scale *= so[1]
+            used.append(mi)
+            if which == 0:
+                q = so[0]
+            else:
+                kt = so[0]
+        if not scale > 0:
+            continue
+        v = nodes[pv].inputs[1]
+        attrs = [Attr("scale", f=float(scale)),
+                 Attr("softmax_axis", i=get_attr_int(sm, "axis", -1))]
+        o_name = nodes[pv].outputs[0]
+        # [B,S,H,d] in and out: every head split / merge Transpose goes
+        qs, cq, tq = trace_transposes(q)
+        ks, ck, tk = trace_transposes(kt)
+        vs, cv, tv = trace_transposes(v)
+        oc = consumer_of(o_name)
+        if cq == HEADS and ck is not None and ck[:2] + [ck[3], ck[2]] == HEADS and \
+                cv == HEADS and oc is not None and nodes[oc].op_type == "Transpose" and \
+                get_attr_ints(nodes[oc], "perm", None) == HEADS:
+            nodes[oc] = Node("FusedAttention", (nodes[pv].name or "") + "_attn", [qs, ks, vs],
+                             list(nodes[oc].outputs),
+                             attrs + [Attr("k_transposed", i=0), Attr("layout", s="bshd")])
+            used += tq + tk + tv + [pv]
+        else:
+            k_transposed = 1
+            ti = single(kt, ("Transpose",))
+            if ti is not None:
+                perm = get_attr_ints(nodes[ti], "perm", None)
+                if perm and len(perm) >= 2:
+                    perm = list(perm[:-2]) + [perm[-1], perm[-2]]
+                    tn = nodes[ti]
+                    nodes[ti] = Node("Transpose", tn.name, list(tn.inputs), list(tn.outputs),
+                                     [Attr("perm", ints=perm)])
+                    k_transposed = 0
+            nodes[pv] = Node("FusedAttention", (nodes[pv].name or "") + "_attn", [q, kt, v],
+                             [o_name], attrs + [Attr("k_transposed", i=k_transposed)])
+        drop.update(used)
+        fused += 1
+    if fused:
+        graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
+    return {"fused": fused}
+
+
+def optimize_graph(graph: Graph, attention: bool = True) -> dict:
+    """Every rewrite, in dependency order: the reference's three
+    (unet-wgsl.js:103-107) and then GN+SiLU, LayerNorm, GELU and (unless
+    ``attention`` is False) flash attention.  Returns the per-rewrite
+    counts."""
+    stats = {"silu": fuse_silu_pattern(graph)["fused"],
+             "mul_add": fuse_mul_add_pattern(graph)["fused"],
+             "group_norm": fuse_group_norm_pattern(graph)["fused"],
+             "group_norm_silu": fuse_group_norm_silu_pattern(graph)["fused"],
+             "layer_norm": fuse_layer_norm_pattern(graph)["fused"],
+             "gelu": fuse_gelu_pattern(graph)["fused"]}
+    if attention:
+        stats["attention"] = fuse_attention_pattern(graph)["fused"]
+    return stats
 
 
 # ---------------------------------------------------------------- planning --

@@ -117,7 +117,9 @@ def test_plan_and_infer_io():
     assert p["unsupported_ops"] == [("FancyOp", 2)]
     io = infer_graph_io(nodes, {"w", "b"})
     assert io == {"inputs": [{"name": "x"}], "outputs": [{"name": "z"}]}
-    assert len(OPS) == 37
+    # the reference's 37 op types plus the three the fusing rewrites insert
+    assert len(OPS) == 40
+    assert {"Gelu", "LayerNormalization", "FusedAttention"} <= set(OPS)
 
 
 class _FakeBuf:

@@ -16,7 +16,10 @@ import pytest
 import oracle
 from conftest import max_rel, rel_l2
 from drawinstant.executor import (Attr, Executor, Graph, Node, TensorProto, WeightCache,
-                                  fuse_group_norm_pattern, fuse_mul_add_pattern, fuse_silu_pattern)
+                                  fuse_attention_pattern, fuse_gelu_pattern,
+                                  fuse_group_norm_pattern, fuse_layer_norm_pattern,
+                                  fuse_mul_add_pattern, fuse_silu_pattern, get_attr_int,
+                                  get_attr_string, optimize_graph)
 
 pytestmark = pytest.mark.gpu
 
@@ -92,9 +95,11 @@ def test_silu_subgraph(dev, fused):
     assert max_rel(out["y"], oracle.unary("SiLU", x)) <= 1e-5
 
 
-def test_decomposed_layernorm_and_gelu_subgraphs(dev):
+@pytest.mark.parametrize("fused", [False, True])
+def test_decomposed_layernorm_and_gelu_subgraphs(dev, fused):
     """LN as exported (ReduceMean, Sub, Pow 2, ReduceMean, Add eps, Sqrt, Div,
-    Mul, Add) and erf-GELU (Div sqrt2, Erf, Add 1, Mul x, Mul 0.5)."""
+    Mul, Add) and erf-GELU (Div sqrt2, Erf, Add 1, Mul x, Mul 0.5), op by op
+    and after fuse_layer_norm_pattern + fuse_gelu_pattern (two dispatches)."""
     rng = np.random.default_rng(13)
     S, D = 256, 320
     x = rng.standard_normal((1, S, D)).astype(np.float32)
@@ -112,32 +117,83 @@ def test_decomposed_layernorm_and_gelu_subgraphs(dev):
              mk("Div", "d2", ["ln", "sq2"], ["u"]), mk("Erf", "erf", ["u"], ["e"]),
              mk("Add", "a1", ["e", "one"], ["e1"]), mk("Mul", "mx", ["ln", "e1"], ["p"]),
              mk("Mul", "mh", ["p", "half"], ["y"])]
-    out, ex = run_graph(dev, Graph(nodes, outputs=[{"name": "ln"}, {"name": "y"}], tensors=t),
-                        {"x": x})
+    g = Graph(nodes, outputs=[{"name": "ln"}, {"name": "y"}], tensors=t)
+    fuse = (fuse_layer_norm_pattern, fuse_gelu_pattern) if fused else ()
+    out, ex = run_graph(dev, g, {"x": x}, fuse)
+    if fused:
+        assert [n.op_type for n in g.nodes] == ["LayerNormalization", "Gelu"]
     ln_ref = oracle.layer_norm(x.reshape(S, D), gam, bet, eps=1e-5).reshape(1, S, D)
     assert max_rel(out["ln"], ln_ref) <= 1e-4
     assert max_rel(out["y"], oracle.unary("GELU", ln_ref)) <= 1e-4
 
 
-def test_attention_subgraph(dev):
-    """Exported attention: Transpose heads, MatMul Q.K^T, Mul scale, Softmax,
+def attention_graph(scale_op="Mul", shared_kt=False, merge=True):
+    """Exported attention: Transpose heads, MatMul Q.K^T, scale, Softmax,
     MatMul P.V, Transpose back (the materialised-score path flash attention
-    replaces)."""
-    rng = np.random.default_rng(14)
-    B, S, H, d = 1, 256, 5, 64
-    q, k, v = (rng.standard_normal((B, S, H, d)).astype(np.float32) for _ in range(3))
-    t = {"scale": tp(np.array([1 / 8], np.float32))}
+    replaces).  shared_kt also outputs K^T, so its Transpose cannot be
+    folded; merge=False leaves the output in [B, H, S, d]."""
+    t = {"scale": tp(np.array([1 / 8 if scale_op == "Mul" else 8.0], np.float32))}
     perm = [Attr("perm", ints=[0, 2, 1, 3])]
     nodes = [mk("Transpose", "tq", ["q"], ["qh"], perm), mk("Transpose", "tk", ["k"], ["kh"],
                                                             [Attr("perm", ints=[0, 2, 3, 1])]),
              mk("Transpose", "tv", ["v"], ["vh"], perm), mk("MatMul", "qk", ["qh", "kh"], ["s"]),
-             mk("Mul", "sc", ["s", "scale"], ["ss"]), mk("Softmax", "sm", ["ss"], ["p"],
-                                                         [Attr("axis", i=-1)]),
-             mk("MatMul", "pv", ["p", "vh"], ["o"]), mk("Transpose", "to", ["o"], ["y"], perm)]
-    out, _ = run_graph(dev, Graph(nodes, outputs=[{"name": "y"}], tensors=t),
-                       {"q": q, "k": k, "v": v})
+             mk(scale_op, "sc", ["s", "scale"], ["ss"]), mk("Softmax", "sm", ["ss"], ["p"],
+                                                            [Attr("axis", i=-1)]),
+             mk("MatMul", "pv", ["p", "vh"], ["o" if merge else "y"])]
+    if merge:
+        nodes.append(mk("Transpose", "to", ["o"], ["y"], perm))
+    outs = [{"name": "y"}] + ([{"name": "kh"}] if shared_kt else [])
+    return Graph(nodes, outputs=outs, tensors=t)
+
+
+@pytest.mark.parametrize("fused,Sq,Skv,d,scale_op,shared_kt,merge", [
+    (False, 256, 256, 64, "Mul", False, True),
+    (True, 256, 256, 64, "Mul", False, True),   # self, [B,S,H,d] in and out (BSHD)
+    (True, 256, 77, 64, "Div", False, True),    # cross: 77 keys, Div scale
+    (True, 256, 77, 64, "Mul", False, False),   # [B,H,S,d] out: BHSD, K transpose turned
+    (True, 200, 77, 64, "Mul", True, True),     # shared K^T: transposed on the device
+    (True, 96, 40, 32, "Mul", False, True),     # head dim 32: unfused chain inside the node
+    (True, 96, 40, 32, "Mul", False, False),    # same, BHSD with the turned K transpose
+])
+def test_attention_subgraph(dev, fused, Sq, Skv, d, scale_op, shared_kt, merge):
+    """The exported attention chain, op by op and after fuse_attention_pattern.
+    The flash path computes with fp16 MFMA operands: rel-L2 <= 2e-3 against
+    the fp64-accumulated oracle; the unfused fp32 chains keep max-rel 1e-4."""
+    rng = np.random.default_rng(14)
+    B, H = 1, 5
+    q = rng.standard_normal((B, Sq, H, d)).astype(np.float32)
+    k, v = (rng.standard_normal((B, Skv, H, d)).astype(np.float32) for _ in range(2))
+    g = attention_graph(scale_op, shared_kt, merge)
+    out, _ = run_graph(dev, g, {"q": q, "k": k, "v": v}, (fuse_attention_pattern,) if fused else ())
     ref = oracle.attention(q.transpose(0, 2, 1, 3).copy(), k.transpose(0, 2, 1, 3).copy(),
-                           v.transpose(0, 2, 1, 3).copy(), scale=1 / 8).transpose(0, 2, 1, 3)
+                           v.transpose(0, 2, 1, 3).copy(), scale=1 / 8)
+    if merge:
+        ref = ref.transpose(0, 2, 1, 3)
+    if fused:
+        fa = [n for n in g.nodes if n.op_type == "FusedAttention"]
+        assert len(fa) == 1 and "Softmax" not in [n.op_type for n in g.nodes]
+        assert get_attr_int(fa[0], "k_transposed", -1) == (1 if shared_kt else 0)
+        assert get_attr_string(fa[0], "layout", "bhsd") == \
+            ("bshd" if merge and not shared_kt else "bhsd")
+    if fused and d == 64:
+        assert rel_l2(out["y"], ref) <= 2e-3
+    else:
+        assert max_rel(out["y"], ref) <= 1e-4
+    if shared_kt:
+        assert max_rel(out["kh"], k.transpose(0, 2, 3, 1)) == 0
+
+
+def test_optimized_gn_silu_subgraph(dev):
+    """torch.onnx GroupNorm + Sigmoid*x SiLU through optimize_graph: one
+    GroupNorm dispatch with the SiLU epilogue (DI_NORM_SILU)."""
+    N, C, H, W, G, eps = 1, 64, 16, 16, 32, 1e-6
+    g, gamma, beta = gn_export_graph(N, C, H, W, G, eps)
+    g.nodes[-1].outputs = ["h"]
+    g.nodes += [mk("Sigmoid", "sg", ["h"], ["s"]), mk("Mul", "ms", ["h", "s"], ["y"])]
+    x = np.random.default_rng(15).standard_normal((N, C, H, W)).astype(np.float32)
+    out, _ = run_graph(dev, g, {"x": x}, (optimize_graph,))
+    assert [n.op_type for n in g.nodes if n.op_type != "Constant"] == ["GroupNorm"]
+    ref = oracle.group_norm(x, gamma.reshape(-1), beta.reshape(-1), G, eps, silu=True)
     assert max_rel(out["y"], ref) <= 1e-4
 
 
