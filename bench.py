@@ -27,6 +27,8 @@ HIP events on the library's stream over exactly K graph-replayed steps
 * `executor_rewrites` (unless --no-blocks): the op-by-op executor over the
   exported cfg4 attention and LayerNorm + GELU subgraphs, unfused and after
   optimize_graph, wall ms per run.
+* `executor_onnx_cfg4` (unless --no-blocks): the same for a real ONNX file,
+  torch.onnx's export of the cfg4 transformer block, through the parser.
 """
 import argparse
 import json
@@ -274,6 +276,49 @@ def bench_executor_rewrites(dev, reps=7):
     return res
 
 
+def bench_executor_onnx(dev, reps=5):
+    """A real ONNX graph: torch.onnx's opset-14 export of the cfg4 block (the
+    SD2.1 64x64 Transformer2D: C 320, 5 heads x 64, context [1,77,1024],
+    scaled_dot_product_attention), written by the test fixture generator,
+    parsed by drawinstant.onnx_parser and run by Executor op by op and after
+    optimize_graph; wall ms per run (median of `reps`)."""
+    import copy
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from golden import onnx_export
+    from drawinstant.executor import Executor, Tensor, WeightCache, optimize_graph
+    from drawinstant.onnx_parser import parse_onnx_graph
+    data, feeds, _ = onnx_export.transformer_case(C=320, heads=5, head_dim=64, H=64, W=64,
+                                                  Sctx=77, ctx_dim=1024)
+    graph = parse_onnx_graph(data)
+    inputs = {k: dev.storage(v) for k, v in feeds.items()}
+    seeds = {k: Tensor(b, list(feeds[k].shape)) for k, b in inputs.items()}
+    row = {"onnx_bytes": len(data), "exported_nodes": len(graph.nodes)}
+    for fused in (False, True):
+        g = copy.deepcopy(graph)
+        if fused:
+            row["rewrites"] = {k: v for k, v in optimize_graph(g).items() if v}
+        wc = WeightCache(dev, g.tensors)
+        ex = Executor(dev, g, wc)
+        ts = []
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            outs = ex.run(seeds)
+            dt = (time.perf_counter() - t0) * 1e3
+            for o in outs.values():
+                o.buf.destroy()
+            if r:
+                ts.append(dt)
+        ts.sort()
+        row["fused_ms" if fused else "unfused_ms"] = round(ts[len(ts) // 2], 3)
+        row["fused_nodes" if fused else "unfused_nodes"] = len(g.nodes)
+        ex.destroy()
+        wc.destroy()
+    row["speedup"] = round(row["unfused_ms"] / row["fused_ms"], 2)
+    for b in inputs.values():
+        b.destroy()
+    return row
+
+
 ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_gemm_conv3x3_64x64x320_pmc.md")
 
 
@@ -411,6 +456,7 @@ def main():
         line["blocks"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                               for kk, vv in v.items()} for k, v in blk.items()}
         line["executor_rewrites"] = bench_executor_rewrites(dev)
+        line["executor_onnx_cfg4"] = bench_executor_onnx(dev)
     print(json.dumps(line), flush=True)
 
 

@@ -69,10 +69,12 @@ class TensorProto:
     dims: List[int]
     dtype: str = "float32"
     data: Any = None  # bytes-like or numpy array
+    name: str = ""
 
     def array(self) -> np.ndarray:
         dt = {"float32": np.float32, "float16": np.float16, "int64": np.int64,
-              "int32": np.int32, "bool": np.uint8}[self.dtype]
+              "int32": np.int32, "bool": np.uint8, "float64": np.float64, "uint8": np.uint8,
+              "int8": np.int8, "int16": np.int16, "uint16": np.uint16}[self.dtype]
         if isinstance(self.data, np.ndarray):
             return np.ascontiguousarray(self.data, dt).reshape(-1)
         return np.frombuffer(bytes(self.data or b""), dt).copy()
@@ -87,6 +89,7 @@ class Attr:
     floats: Optional[List[float]] = None
     s: Optional[Any] = None
     t: Optional[TensorProto] = None
+    strings: Optional[List[str]] = None
 
 
 @dataclass
@@ -96,6 +99,7 @@ class Node:
     inputs: List[str] = field(default_factory=list)
     outputs: List[str] = field(default_factory=list)
     attributes: List[Attr] = field(default_factory=list)
+    domain: str = ""
 
 
 @dataclass
@@ -452,8 +456,20 @@ def _reshape(ctx, node, inputs):
 
 @_op("Shape")
 def _shape(ctx, node, inputs):
-    x = inputs[0]
-    return CpuTensor(np.array(x.dims, np.int64), [len(x.dims)], "int64", True)
+    """Dims as an int64 host tensor, with opset-15 start / end; a ``perm``
+    attribute (set by fuse_attention_pattern on Shape nodes whose Transpose
+    input it removed) permutes the dims first."""
+    dims = list(inputs[0].dims or [])
+    perm = get_attr_ints(node, "perm", None)
+    if perm:
+        dims = [dims[j] for j in perm]
+    r = len(dims)
+    start = get_attr_int(node, "start", 0)
+    end = get_attr_int(node, "end", r)
+    start = min(max(start + r if start < 0 else start, 0), r)
+    end = min(max(end + r if end < 0 else end, 0), r)
+    dims = dims[start:end] if end > start else []
+    return CpuTensor(np.array(dims, np.int64), [len(dims)], "int64", True)
 
 
 @_op("Unsqueeze")
@@ -740,10 +756,18 @@ def _where(ctx, node, inputs):
     raise ValueError(f"Where {node.name}: GPU path not implemented")
 
 
+def _host_small(t) -> bool:
+    """A tensor whose values are also on the host and few (scalars, shape
+    vectors): binary ops between two of them run on the host."""
+    d = getattr(t, "cpu_data", None) if t is not None else None
+    return d is not None and np.asarray(d).size <= 16 and \
+        int(np.prod(t.dims or [1])) == np.asarray(d).size
+
+
 def _binary(op):
     def fn(ctx, node, inputs):
         a, b = inputs
-        if _is_cpu(a) and _is_cpu(b):
+        if (_is_cpu(a) and _is_cpu(b)) or (_host_small(a) and _host_small(b)):
             dims = broadcast_shape(list(a.dims), list(b.dims))
             big = a.cpu_data.dtype == np.int64 or b.cpu_data.dtype == np.int64
             av = a.cpu_data.reshape(a.dims) if a.dims else a.cpu_data.reshape(())
@@ -964,14 +988,28 @@ def _layer_norm(ctx, node, inputs):
 ATTN_HEAD_DIM = 64  # the flash kernel's head dim
 
 
-def _attention_unfused(ctx, q, k, v, scale, k_transposed, axis):
-    """The chain the rewrite replaced, op by op: MatMul(Q, K^T) -> * scale ->
-    Softmax -> MatMul(., V)."""
+def _host_scalar(t) -> Optional[float]:
+    """The value of a one-element tensor known on the host, else None."""
+    d = getattr(t, "cpu_data", None) if t is not None else None
+    if d is None or np.asarray(d).size != 1:
+        return None
+    return float(np.asarray(d, np.float64).reshape(-1)[0])
+
+
+def _attention_unfused(ctx, q, k, v, scale, k_transposed, axis, q_fac=None, k_fac=None):
+    """The chain the rewrite replaced, op by op: [Q * q_fac], MatMul(Q, K^T
+    [* k_fac]) -> * scale -> Softmax -> MatMul(., V)."""
     tmp = []
+    if q_fac is not None:
+        q = OPS["Mul"](ctx, Node("Mul"), [q, q_fac])
+        tmp.append(q)
     if not k_transposed:
         perm = list(range(len(k.dims)))
         perm[-2], perm[-1] = perm[-1], perm[-2]
         k = OPS["Transpose"](ctx, Node("Transpose", "", [], [], [Attr("perm", ints=perm)]), [k])
+        tmp.append(k)
+    if k_fac is not None:
+        k = OPS["Mul"](ctx, Node("Mul"), [k, k_fac])
         tmp.append(k)
     s = OPS["MatMul"](ctx, Node("MatMul"), [q, k])
     tmp.append(s)
@@ -994,23 +1032,36 @@ def _fused_attention(ctx, node, inputs):
     fused-cross-attn.js:112-173).  layout "bhsd": Q [.., Sq, 64], K
     [.., Skv, 64] (K^T [.., 64, Skv] with k_transposed), V [.., Skv, 64] with
     equal leading dims, which run as heads; layout "bshd": Q [B, Sq, H, 64],
-    K / V [B, Skv, H, 64].  Other shapes run the unfused chain."""
+    K / V [B, Skv, H, 64].  Optional inputs 3 / 4 are factors on Q and on
+    K^T, folded into the scale when they are host scalars.  Other shapes or
+    factors run the unfused chain."""
     q, k, v = (_on_device(ctx, t) for t in inputs[:3])
+    q_fac = inputs[3] if len(inputs) > 3 and inputs[3] is not None else None
+    k_fac = inputs[4] if len(inputs) > 4 and inputs[4] is not None else None
     scale = get_attr_float(node, "scale", 1.0)
     kt = get_attr_int(node, "k_transposed", 1)
     axis = get_attr_int(node, "softmax_axis", -1)
+    facs_ok = True
+    for f in (q_fac, k_fac):
+        if f is not None:
+            hv = _host_scalar(f)
+            facs_ok = facs_ok and hv is not None and hv > 0
+            scale *= hv if hv is not None else 1.0
+    if not facs_ok:
+        scale = get_attr_float(node, "scale", 1.0)
     rank = len(q.dims)
     last_axis = (axis + rank if axis < 0 else axis) == rank - 1
     d = q.dims[-1] if rank else 0
     if get_attr_string(node, "layout", "bhsd") == "bshd":
-        ok = kt == 0 and rank == 4 and len(k.dims) == 4 and len(v.dims) == 4 and last_axis and \
-            q.dims[0] == k.dims[0] == v.dims[0] and q.dims[2] == k.dims[2] == v.dims[2] and \
-            k.dims[1] == v.dims[1] and d == k.dims[3] == v.dims[3] == ATTN_HEAD_DIM and \
-            q.dims[1] > 0 and k.dims[1] > 0
+        ok = facs_ok and kt == 0 and rank == 4 and len(k.dims) == 4 and len(v.dims) == 4 and \
+            last_axis and q.dims[0] == k.dims[0] == v.dims[0] and \
+            q.dims[2] == k.dims[2] == v.dims[2] and k.dims[1] == v.dims[1] and \
+            d == k.dims[3] == v.dims[3] == ATTN_HEAD_DIM and q.dims[1] > 0 and k.dims[1] > 0
         if not ok:
             heads = Node("Transpose", "", [], [], [Attr("perm", ints=[0, 2, 1, 3])])
             qh, kh, vh = (OPS["Transpose"](ctx, heads, [t]) for t in (q, k, v))
-            oh = _attention_unfused(ctx, qh, kh, vh, scale, kt, axis)
+            oh = _attention_unfused(ctx, qh, kh, vh, scale, kt, axis,
+                                    None if facs_ok else q_fac, None if facs_ok else k_fac)
             out = OPS["Transpose"](ctx, heads, [oh])
             for t in (qh, kh, vh, oh):
                 ctx.pool.release(t.buf)
@@ -1019,14 +1070,15 @@ def _fused_attention(ctx, node, inputs):
         out = ctx.pool.acquire(q.numel * 4)
         ctx.dispatchers.attention(q.buf, k.buf, v.buf, out, B, H, Sq, k.dims[1], d, BSHD, scale)
         return Tensor(out, list(q.dims))
-    ok = rank >= 2 and len(k.dims) == rank and len(v.dims) == rank and \
+    ok = facs_ok and rank >= 2 and len(k.dims) == rank and len(v.dims) == rank and \
         q.dims[:-2] == k.dims[:-2] == v.dims[:-2] and last_axis
     if ok:
         Skv = k.dims[-1] if kt else k.dims[-2]
         ok = d == ATTN_HEAD_DIM and (k.dims[-2] if kt else k.dims[-1]) == d and \
             v.dims[-2] == Skv and v.dims[-1] == ATTN_HEAD_DIM and q.dims[-2] > 0 and Skv > 0
     if not ok:
-        return _attention_unfused(ctx, q, k, v, scale, kt, axis)
+        return _attention_unfused(ctx, q, k, v, scale, kt, axis, None if facs_ok else q_fac,
+                                  None if facs_ok else k_fac)
     heads = int(np.prod(q.dims[:-2])) if rank > 2 else 1
     Sq = q.dims[-2]
     k_buf, tmp = k.buf, None
@@ -1439,21 +1491,32 @@ def fuse_attention_pattern(graph: Graph) -> dict:
     MatMul(., V) => FusedAttention(Q, K, V): flash attention through
     di_attn_cross, so the [.., Sq, Skv] score matrix the reference's executor
     materialises (OPS.MatMul + OPS.Softmax, wgsl-executor.js:1027-1054) is
-    never written.  Scalar Muls on Q or on K^T (torch's SDPA export splits
-    the scale over both) fold into the scale attribute, and a single-use
-    Transpose producing K^T gets its last two perm entries swapped so it
-    yields K directly.  When Q, K and V come from [B, S, H, d] through
-    single-use head-split Transposes (perm 0,2,1,3; for K^T composed with the
-    last-axes swap) and the output goes through the inverse one, those
-    Transposes go too and the node reads and writes [B, S, H, d]
-    (layout="bshd", the fused-attn.js layout).
+    never written.
+
+    * Muls on Q or on K^T (torch's scaled_dot_product_attention export
+      splits the scale as sqrt(scale) over both) fold away: by constants into
+      the scale attribute; by a computed factor (SDPA derives it from
+      Shape(Q)) as extra inputs 3 / 4, multiplied into the scale at run time
+      when they are one-element host values.
+    * A single-use Transpose producing K^T gets its last two perm entries
+      swapped so it yields K directly.
+    * When Q, K and V come from [B, S, H, d] through head-split Transposes
+      (perm 0,2,1,3; for K^T composed with the last-axes swap) and the output
+      goes through the inverse one, those Transposes go too and the node
+      reads and writes [B, S, H, d] (layout="bshd", the fused-attn.js
+      layout).  Shape nodes reading a dropped Transpose read its source with
+      a ``perm`` attribute instead.
 
     The fused node runs head dim 64 with fp16 MFMA operands (fp32 softmax
     state and accumulation), so its outputs agree with the fp32 chain to
-    about 1e-3 relative RMS, not bit for bit; other shapes run the unfused
-    chain (MatMul, scale, Softmax, MatMul) inside the node."""
+    about 1e-3 relative RMS, not bit for bit; other shapes (or scale inputs
+    that are not host scalars) run the unfused chain inside the node."""
     nodes = graph.nodes
     consumers, producer = _consumers_and_producers(graph)
+    shape_readers: Dict[str, List[int]] = {}
+    for k, n in enumerate(nodes):
+        if n.op_type == "Shape" and n.inputs:
+            shape_readers.setdefault(n.inputs[0], []).append(k)
 
     def single(name, ops):
         if consumers.get(name, 0) != 1:
@@ -1462,17 +1525,26 @@ def fuse_attention_pattern(graph: Graph) -> dict:
         return pi if pi is not None and nodes[pi].op_type in ops else None
 
     def trace_transposes(name):
-        """(source, composed perm or None, node indices) of the chain of
-        single-use Transposes producing `name`."""
-        perm, idx = None, []
+        """(source, composed perm from the source or None, Transpose
+        indices, Shape fix-ups) of the chain of rank-4 Transposes producing
+        `name` whose outputs are read by nothing else but Shape nodes."""
+        chain = []
         while True:
-            ti = single(name, ("Transpose",))
-            p = get_attr_ints(nodes[ti], "perm", None) if ti is not None else None
+            ti = producer.get(name)
+            if ti is None or nodes[ti].op_type != "Transpose" or \
+                    consumers.get(name, 0) - len(shape_readers.get(name, [])) != 1:
+                break
+            p = get_attr_ints(nodes[ti], "perm", None)
             if not p or len(p) != 4:
-                return name, perm, idx
-            perm = list(p) if perm is None else [p[j] for j in perm]
-            idx.append(ti)
+                break
+            chain.append(ti)
             name = nodes[ti].inputs[0]
+        perm, fix = None, []
+        for ti in reversed(chain):  # forward from the source
+            p = get_attr_ints(nodes[ti], "perm", None)
+            perm = list(p) if perm is None else [perm[j] for j in p]
+            fix += [(si, list(perm)) for si in shape_readers.get(nodes[ti].outputs[0], [])]
+        return name, perm, chain, fix
 
     def consumer_of(name):
         if consumers.get(name, 0) != 1:
@@ -1505,38 +1577,58 @@ def fuse_attention_pattern(graph: Graph) -> dict:
             continue
         used.append(qk)
         q, kt = nodes[qk].inputs[:2]
+        extra = ["", ""]  # computed factors on Q and on K^T
         for which in (0, 1):
             name = q if which == 0 else kt
             mi = single(name, ("Mul",))
             if mi is None:
                 continue
             so = _scalar_operand(graph, producer, nodes[mi])
-            if so is None:
-                continue
-            scale *= so[1]
+            if so is not None:
+                scale *= so[1]
+                data = so[0]
+            else:
+                a, b = nodes[mi].inputs[:2]
+                # the factor is the operand that is not the head-split data
+                data, fac = (b, a) if trace_transposes(b)[2] and not trace_transposes(a)[2] \
+                    else (a, b)
+                if not fac or fac in (q, kt):
+                    continue
+                extra[which] = fac
             used.append(mi)
             if which == 0:
-                q = so[0]
+                q = data
             else:
-                kt = so[0]
+                kt = data
         if not scale > 0:
             continue
         v = nodes[pv].inputs[1]
         attrs = [Attr("scale", f=float(scale)),
                  Attr("softmax_axis", i=get_attr_int(sm, "axis", -1))]
+        tail = extra if any(extra) else []
         o_name = nodes[pv].outputs[0]
         # [B,S,H,d] in and out: every head split / merge Transpose goes
-        qs, cq, tq = trace_transposes(q)
-        ks, ck, tk = trace_transposes(kt)
-        vs, cv, tv = trace_transposes(v)
+        qs, cq, tq, fq = trace_transposes(q)
+        ks, ck, tk, fk = trace_transposes(kt)
+        vs, cv, tv, fv = trace_transposes(v)
         oc = consumer_of(o_name)
         if cq == HEADS and ck is not None and ck[:2] + [ck[3], ck[2]] == HEADS and \
                 cv == HEADS and oc is not None and nodes[oc].op_type == "Transpose" and \
-                get_attr_ints(nodes[oc], "perm", None) == HEADS:
-            nodes[oc] = Node("FusedAttention", (nodes[pv].name or "") + "_attn", [qs, ks, vs],
-                             list(nodes[oc].outputs),
+                get_attr_ints(nodes[oc], "perm", None) == HEADS and \
+                not shape_readers.get(o_name):
+            nodes[oc] = Node("FusedAttention", (nodes[pv].name or "") + "_attn",
+                             [qs, ks, vs] + tail, list(nodes[oc].outputs),
                              attrs + [Attr("k_transposed", i=0), Attr("layout", s="bshd")])
             used += tq + tk + tv + [pv]
+            for sidx, perm in fq + fk + fv:
+                sn = nodes[sidx]
+                src = qs if (sidx, perm) in fq else ks if (sidx, perm) in fk else vs
+                old = get_attr_ints(sn, "perm", None)
+                if old:
+                    perm = [perm[j] for j in old]
+                nodes[sidx] = Node("Shape", sn.name, [src], list(sn.outputs),
+                                   [a for a in sn.attributes if a.name != "perm"] +
+                                   [Attr("perm", ints=perm)])
         else:
             k_transposed = 1
             ti = single(kt, ("Transpose",))
@@ -1548,8 +1640,9 @@ def fuse_attention_pattern(graph: Graph) -> dict:
                     nodes[ti] = Node("Transpose", tn.name, list(tn.inputs), list(tn.outputs),
                                      [Attr("perm", ints=perm)])
                     k_transposed = 0
-            nodes[pv] = Node("FusedAttention", (nodes[pv].name or "") + "_attn", [q, kt, v],
-                             [o_name], attrs + [Attr("k_transposed", i=k_transposed)])
+            nodes[pv] = Node("FusedAttention", (nodes[pv].name or "") + "_attn",
+                             [q, kt, v] + tail, [o_name],
+                             attrs + [Attr("k_transposed", i=k_transposed)])
         drop.update(used)
         fused += 1
     if fused:

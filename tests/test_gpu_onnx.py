@@ -1,0 +1,61 @@
+"""GPU: real ONNX graphs through the parser and the executor.
+
+torch.onnx exports (opset 14) of a diffusers-style Transformer2D block
+(scaled_dot_product_attention and eager attention) and a ResnetBlock2D are
+parsed by drawinstant.onnx_parser and run by Executor, op by op as the
+reference's executor would and after optimize_graph, against the modules'
+float64 outputs.  Tolerances: the op-by-op fp32 path rel-L2 <= 1e-5 and
+max-rel <= 1e-4; the optimized graph the same except where flash attention
+(fp16 MFMA operands) is in the path: rel-L2 <= 2e-3.
+"""
+import copy
+
+import numpy as np
+import pytest
+
+from conftest import max_rel, rel_l2
+from drawinstant.executor import Executor, WeightCache, optimize_graph
+from drawinstant.onnx_parser import parse_onnx_graph
+from golden import onnx_export
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cases():
+    return {"sdpa": onnx_export.transformer_case(), "eager": onnx_export.transformer_case(eager=True),
+            "resnet": onnx_export.resnet_case()}
+
+
+def run(dev, g, feeds, reps=1):
+    wc = WeightCache(dev, g.tensors)
+    ex = Executor(dev, g, wc)
+    try:
+        res = []
+        for _ in range(reps):
+            outs = ex.run(feeds)
+            t = outs["y"]
+            res.append(dev.download(t.buf, np.float32, tuple(t.dims)))
+            t.buf.destroy()
+        return res
+    finally:
+        ex.destroy()
+        wc.destroy()
+
+
+@pytest.mark.parametrize("key", ["sdpa", "eager", "resnet"])
+@pytest.mark.parametrize("fused", [False, True])
+def test_exported_block(dev, cases, key, fused):
+    data, feeds, y = cases[key]
+    g = parse_onnx_graph(data)
+    if fused:
+        g = copy.deepcopy(g)
+        optimize_graph(g)
+    out = run(dev, g, feeds, reps=2)
+    print(f"[onnx] {key} fused={fused} nodes={len(g.nodes)} rel_l2={rel_l2(out[0], y):.2e} "
+          f"max_rel={max_rel(out[0], y):.2e}", flush=True)
+    assert np.array_equal(out[0], out[1])  # a second run through the reused pool
+    if fused and key != "resnet":
+        assert rel_l2(out[0], y) <= 2e-3
+    else:
+        assert rel_l2(out[0], y) <= 1e-5 and max_rel(out[0], y) <= 1e-4
