@@ -50,7 +50,10 @@ struct GemmArgs {
   // ---- problem ----
   uint32_t M = 0, N = 0, K = 0, batch = 1;
   uint32_t splits = 1, k_split = 0;
-  uint32_t a_vec_ok = 1, b_vec_ok = 1;  // 16-byte vector loads legal
+  uint32_t a_vec_ok = 1, b_vec_ok = 1;  // whole-vector (KV element) loads legal
+  // fp32 problem (elem DI_F32) whose B is stored in fp16 and widened exactly
+  // as it loads (fp16-resident weights); bounds-checked kernels only
+  int b_f16 = 0;
   // Byte extents of A, A2 (per batch entry) and B for buffer-load range
   // checks; 0 = unknown (generic path).  Must stay below 2 GiB.
   uint32_t a_bytes = 0, a2_bytes = 0, b_bytes = 0;

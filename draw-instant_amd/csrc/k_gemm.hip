@@ -27,6 +27,8 @@
 #include <cstdio>
 #include <cstdlib>
 
+#include <type_traits>
+
 #include "di_device.h"
 #include "di_gemm.h"
 #include "di_kernels.h"
@@ -407,10 +409,15 @@ __device__ __forceinline__ void gemm_tile_stats(const GemmArgs& g, const float* 
 }
 
 // ---- the GEMM kernel ----
+// TB: storage type of B.  The fp32 kernels also take fp16 B (weights kept
+// in fp16), widened exactly to fp32 as each vector is loaded.
 template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D, int KS,
-          int EX>
+          int EX, typename TB = T>
 __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
   static_assert(EX == EX_NONE || (FAST && AM == A_DENSE), "epilogue extras: dense fast path");
+  static_assert(std::is_same<TB, T>::value || (!FAST && std::is_same<T, float>::value &&
+                                               std::is_same<TB, f16>::value),
+                "fp16 B with fp32 A: bounds-checked fp32 kernels only");
   using MT = Mfma<T>;
   constexpr int KV = MT::KV;
   constexpr int BK = 128 / sizeof(T);  // k elements per stage (128 bytes per row)
@@ -480,7 +487,15 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
 
   const T* A = (const T*)g.a + (uint64_t)bz * g.sa;
   const T* A2 = (const T*)g.a2 + (uint64_t)bz * g.sa2;
-  const T* B = (const T*)g.b + (uint64_t)bz * g.sb;
+  const TB* B = (const TB*)g.b + (uint64_t)bz * g.sb;
+  // one vector of B: KV elements of TB (widened to T)
+  auto ld_bvec = [](const TB* p) -> typename MT::vec {
+    if constexpr (std::is_same<TB, T>::value) {
+      return *(const typename MT::vec*)p;
+    } else {
+      return __builtin_convertvector(*(const f16x4*)p, f32x4);
+    }
+  };
 
   // ---- per-thread A addressing (rows fixed for the whole K loop) ----
   const int kc = tid % VPR;  // same k-vector slot for all of this thread's vectors
@@ -625,7 +640,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
         uint32_t n = n0 + r, k = kbase + kc * KV;
         if (n < g.N) {
           if (b_fast && k + KV <= k_end) {
-            v = *(const typename MT::vec*)(B + (uint64_t)n * g.ldb + k);
+            v = ld_bvec(B + (uint64_t)n * g.ldb + k);
           } else {
 #pragma unroll
             for (int j = 0; j < KV; j++)
@@ -638,7 +653,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
         uint32_t k = kbase + kr, n = n0 + nc * KV;
         if (k < k_end) {
           if (b_fast && n + KV <= g.N) {
-            v = *(const typename MT::vec*)(B + (uint64_t)k * g.ldb + n);
+            v = ld_bvec(B + (uint64_t)k * g.ldb + n);
           } else {
 #pragma unroll
             for (int j = 0; j < KV; j++)
@@ -1147,23 +1162,23 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
 }
 
 template <typename T, int BM, int BN, int WGM, int WGN, int AM, int BMD, bool FAST, int D = 2,
-          int KS = 1, int EX = EX_NONE>
+          int KS = 1, int EX = EX_NONE, typename TB = T>
 void launch_cfg(const GemmArgs& g, hipStream_t s) {
   uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D, KS, EX>
+  k_gemm<T, BM, BN, WGM, WGN, AM, BMD, FAST, D, KS, EX, TB>
       <<<dim3(tiles, 1, g.batch * g.splits), 64 * WGM * WGN * KS, 0, s>>>(g);
 }
 
 // Generic (bounds-checked) variants: two tile shapes.
-template <typename T, int AM, int BMD>
+template <typename T, int AM, int BMD, typename TB = T>
 void launch_slow(const GemmArgs& g, int tile_cfg, hipStream_t s) {
   if (tile_cfg == TILE_64x64 || tile_cfg == TILE_128x64 || tile_cfg == TILE_64x128 ||
       tile_cfg == TILE_64x160 || tile_cfg == TILE_64x64_K2 || tile_cfg == TILE_128x64_K2 ||
       tile_cfg == TILE_64x128_K2 || tile_cfg == TILE_64x128_W16 || tile_cfg == TILE_128x64_W16 ||
       tile_cfg == TILE_64x64_W16)
-    launch_cfg<T, 64, 64, 2, 2, AM, BMD, false>(g, s);
+    launch_cfg<T, 64, 64, 2, 2, AM, BMD, false, 2, 1, EX_NONE, TB>(g, s);
   else
-    launch_cfg<T, 128, 128, 2, 2, AM, BMD, false>(g, s);
+    launch_cfg<T, 128, 128, 2, 2, AM, BMD, false, 2, 1, EX_NONE, TB>(g, s);
 }
 
 // Buffer-load variants: every tile shape, ring depth D, epilogue extras EX.
@@ -1399,6 +1414,12 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
     DI_GEMM_CASE(f16, A_DENSE, B_NK)
     else DI_GEMM_CASE(f16, A_DENSE, B_KN)
     else DI_GEMM_CASE(f16, A_CONV_NHWC, B_NK)
+  } else if (g.b_f16) {
+    if (a_mode == A_DENSE && b_mode == B_NK) launch_slow<float, A_DENSE, B_NK, f16>(g, tile_cfg, s);
+    else if (a_mode == A_DENSE && b_mode == B_KN)
+      launch_slow<float, A_DENSE, B_KN, f16>(g, tile_cfg, s);
+    else if (a_mode == A_CONV_NCHW && b_mode == B_NK)
+      launch_slow<float, A_CONV_NCHW, B_NK, f16>(g, tile_cfg, s);
   } else {
     DI_GEMM_CASE(float, A_DENSE, B_NK)
     else DI_GEMM_CASE(float, A_DENSE, B_KN)

@@ -24,6 +24,22 @@ int run_gemm(di_ctx* ctx, GemmArgs& g, int elem, int a_mode, int b_mode, int til
   return DI_OK;
 }
 
+// dtype of the activations / outputs and element size of B for the
+// contractions that take DI_F32W16 (fp32 with fp16-resident weights).
+struct Dts {
+  int act;
+  size_t es, esb;
+  bool w16;
+};
+Dts contraction_dts(int dt) {
+  const bool w16 = dt == DI_F32W16;
+  const int act = w16 ? DI_F32 : dt;
+  return Dts{act, dtype_size(act), w16 ? 2 : dtype_size(act), w16};
+}
+#define DI_DTYPE_W16(dt)                                                                    \
+  DI_REQUIRE(::di::dtype_ok(dt) || (dt) == DI_F32W16, DI_EINVAL, "unsupported dtype %d", \
+             (int)(dt))
+
 // Optional fp32 per-channel parameter buffer (0 = absent).
 int opt_f32(di_ctx* ctx, di_handle h, uint64_t n, const float** out) {
   *out = nullptr;
@@ -53,14 +69,16 @@ struct Tmp {
 extern "C" {
 
 int32_t di_matmul(di_ctx* ctx, di_handle A, di_handle B, di_handle Y, uint32_t M, uint32_t N,
-                  uint32_t K, uint32_t batch, int32_t b_batched, int32_t dt) {
+                  uint32_t K, uint32_t batch, int32_t b_batched, int32_t dtype) {
   DI_CTX(ctx);
-  DI_DTYPE(dt);
+  DI_DTYPE_W16(dtype);
   DI_REQUIRE(M && N && K && batch, DI_EINVAL, "di_matmul: zero dimension (M=%u N=%u K=%u batch=%u)",
              M, N, K, batch);
-  const size_t es = dtype_size(dt);
+  const Dts d = contraction_dts(dtype);
+  const int dt = d.act;
+  const size_t es = d.es;
   DI_BUF(ctx, A, a, (uint64_t)batch * M * K * es);
-  DI_BUF(ctx, B, b, (uint64_t)(b_batched ? batch : 1) * K * N * es);
+  DI_BUF(ctx, B, b, (uint64_t)(b_batched ? batch : 1) * K * N * d.esb);
   DI_BUF(ctx, Y, y, (uint64_t)batch * M * N * es);
   GemmArgs g;
   g.a = a->ptr;
@@ -80,17 +98,20 @@ int32_t di_matmul(di_ctx* ctx, di_handle A, di_handle B, di_handle Y, uint32_t M
   const uint32_t kv = dt == DI_F32 ? 4 : 8;
   g.a_vec_ok = K % kv == 0;
   g.b_vec_ok = N % kv == 0;
+  g.b_f16 = d.w16;
   return run_gemm(ctx, g, dt, A_DENSE, B_KN);
 }
 
 int32_t di_gemm(di_ctx* ctx, di_handle A, di_handle B, di_handle C, di_handle Y, uint32_t M,
-                uint32_t N, uint32_t K, int32_t trans_b, int32_t dt) {
+                uint32_t N, uint32_t K, int32_t trans_b, int32_t dtype) {
   DI_CTX(ctx);
-  DI_DTYPE(dt);
+  DI_DTYPE_W16(dtype);
   DI_REQUIRE(M && N && K, DI_EINVAL, "di_gemm: zero dimension (M=%u N=%u K=%u)", M, N, K);
-  const size_t es = dtype_size(dt);
+  const Dts d = contraction_dts(dtype);
+  const int dt = d.act;
+  const size_t es = d.es;
   DI_BUF(ctx, A, a, (uint64_t)M * K * es);
-  DI_BUF(ctx, B, b, (uint64_t)K * N * es);
+  DI_BUF(ctx, B, b, (uint64_t)K * N * d.esb);
   DI_BUF(ctx, Y, y, (uint64_t)M * N * es);
   const float* bias = nullptr;
   int rc = opt_f32(ctx, C, N, &bias);
@@ -110,8 +131,9 @@ int32_t di_gemm(di_ctx* ctx, di_handle A, di_handle B, di_handle C, di_handle Y,
   const uint32_t kv = dt == DI_F32 ? 4 : 8;
   g.a_vec_ok = K % kv == 0;
   g.b_vec_ok = (trans_b ? K : N) % kv == 0;
+  g.b_f16 = d.w16;
   g.a_bytes = gemm_extent((uint64_t)M * K * es);
-  g.b_bytes = gemm_extent((uint64_t)K * N * es);
+  g.b_bytes = gemm_extent((uint64_t)K * N * d.esb);
   return run_gemm(ctx, g, dt, A_DENSE, trans_b ? B_NK : B_KN);
 }
 
@@ -159,9 +181,13 @@ int32_t di_linear(di_ctx* ctx, di_handle X, di_handle W, di_handle bias, di_hand
 
 int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_handle R, di_handle Y,
                   uint32_t N, uint32_t Cin, uint32_t Cout, uint32_t H, uint32_t W, uint32_t K,
-                  uint32_t S, uint32_t pad, int32_t flags, int32_t dt, int32_t layout) {
+                  uint32_t S, uint32_t pad, int32_t flags, int32_t dtype, int32_t layout) {
   DI_CTX(ctx);
-  DI_DTYPE(dt);
+  DI_DTYPE_W16(dtype);
+  const Dts d = contraction_dts(dtype);
+  const int dt = d.act;
+  DI_REQUIRE(!d.w16 || layout == DI_NCHW, DI_EUNSUPPORTED,
+             "di_conv2d: DI_F32W16 is for the NCHW fp32 path");
   DI_REQUIRE(N && Cin && Cout && H && W && K && S, DI_EINVAL, "di_conv2d: zero dimension");
   DI_REQUIRE((flags & ~(DI_CONV_F16_COMPUTE | DI_CONV_UPSAMPLE2X | DI_CONV_SILU)) == 0, DI_EINVAL,
              "di_conv2d: unknown flags 0x%x", flags);
@@ -173,7 +199,7 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_han
   const size_t es = dtype_size(dt);
   const uint64_t nx = (uint64_t)N * Cin * H * W, ny = (uint64_t)N * Cout * Ho * Wo;
   DI_BUF(ctx, X, x, nx * es);
-  DI_BUF(ctx, Wt, w, (uint64_t)Cout * Cin * K * K * es);
+  DI_BUF(ctx, Wt, w, (uint64_t)Cout * Cin * K * K * d.esb);
   DI_BUF(ctx, Y, y, ny * es);
   const float* b = nullptr;
   int rc = opt_f32(ctx, bias, Cout, &b);
@@ -229,6 +255,7 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_han
     g.b = w->ptr;
     g.ldb = g.K;
     g.b_vec_ok = g.K % (dt == DI_F32 ? 4 : 8) == 0;
+    g.b_f16 = d.w16;
     DI_REQUIRE(dt == DI_F32, DI_EUNSUPPORTED,
                "di_conv2d: NCHW fp16 needs DI_CONV_F16_COMPUTE or the NHWC layout");
     return run_gemm(ctx, g, DI_F32, A_CONV_NCHW, B_NK);
@@ -243,7 +270,7 @@ int32_t di_conv2d(di_ctx* ctx, di_handle X, di_handle Wt, di_handle bias, di_han
   rc = tw.alloc((uint64_t)Cout * K * K * Cp * 2);
   if (rc) return rc;
   launch_layout(ctx->stream, x->ptr, dt, DI_NCHW, tx.p, DI_F16, DI_NHWC, N, Cin, H, W, Cp);
-  launch_repack_oihw_ohwi(ctx->stream, w->ptr, dt, tw.p, Cout, Cin, K, Cp);
+  launch_repack_oihw_ohwi(ctx->stream, w->ptr, d.w16 ? DI_F16 : dt, tw.p, Cout, Cin, K, Cp);
   DI_LAUNCH_CHECK();
   g.a = tx.p;
   g.lda = Cp;

@@ -16,6 +16,7 @@ from . import _lib
 
 F32 = 0
 F16 = 1
+F32W16 = 2  # fp32 activations, fp16-resident weights (matmul / gemm / conv2d)
 NCHW = 0
 NHWC = 1
 BSHD = 0  # attention layouts

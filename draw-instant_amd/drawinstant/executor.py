@@ -46,7 +46,7 @@ from typing import Any, Callable, Dict, List, Optional
 
 import numpy as np
 
-from .device import BHSD, BSHD, F32, NCHW, Buffer, Device, call
+from .device import BHSD, BSHD, F16, F32, F32W16, NCHW, Buffer, Device, call
 
 # ---------------------------------------------------------------- logging --
 LOG = {"verbose": False, "node_count": 0, "op_hist": {}, "t0": 0.0, "profile": False,
@@ -122,11 +122,11 @@ class Tensor:
         self.consumers = consumers
         self.cpu_data = cpu_data  # CPU mirror for scalar fast paths (Pow exponent, scales)
         self.numel = int(np.prod(self.dims)) if self.dims else 1
-        self.byte_length = self.numel * 4
+        self.byte_length = self.numel * (2 if dtype == "float16" else 4)
         self.is_shape = False
 
     def __repr__(self):
-        return f"Tensor(GPU{self.dims})"
+        return f"Tensor(GPU{self.dims}{':f16' if self.dtype == 'float16' else ''})"
 
 
 class CpuTensor:
@@ -212,12 +212,24 @@ class BufferPool:
 class WeightCache:
     """Initializers uploaded once on first use (wgsl-unet.js:55-104): floats
     (fp16 widened to fp32) on the device, int64/int32/bool kept on the CPU as
-    shape tensors; scalar floats also expose ``cpu_data``."""
+    shape tensors; scalar floats also expose ``cpu_data``.
 
-    def __init__(self, device: Device, tensors: Dict[str, TensorProto]):
+    ``keep_f16``: fp16 initializers of rank >= 2 (the MatMul / Gemm / Conv
+    weights of an fp16 ONNX file) stay fp16 on the device, half the bytes;
+    the contractions read them through DI_F32W16 (widened exactly as they
+    load, so results are unchanged) and any other consumer gets an fp32 copy
+    for the run."""
+
+    def __init__(self, device: Device, tensors: Dict[str, TensorProto], keep_f16: bool = False):
         self.device = device
         self.tensors = tensors
+        self.keep_f16 = keep_f16
         self.gpu: Dict[str, Any] = {}
+
+    @property
+    def device_bytes(self) -> int:
+        """Bytes of the initializers uploaded so far."""
+        return sum(v.byte_length for v in self.gpu.values() if isinstance(v, Tensor))
 
     def get(self, name: str):
         if name in self.gpu:
@@ -228,6 +240,8 @@ class WeightCache:
         a = t.array()
         if t.dtype in ("int64", "int32", "bool"):
             entry = CpuTensor(a, t.dims, t.dtype, is_shape=t.dtype != "bool")
+        elif self.keep_f16 and t.dtype == "float16" and len(t.dims) >= 2:
+            entry = Tensor(self.device.storage(a), t.dims, "float16")
         else:
             f = a.astype(np.float32)
             entry = Tensor(self.device.storage(f if f.size else np.zeros(1, np.float32)), t.dims,
@@ -288,14 +302,17 @@ class Dispatchers:
             F32, NCHW)
         self.layer_norm = lambda x, g, b, y, rows, inner, eps: call(
             "di_layer_norm", ctx, x.handle, g.handle, b.handle, y.handle, rows, inner, eps, F32)
-        self.matmul = lambda a, b, y, M, N, K, batch, bb: call(
-            "di_matmul", ctx, a.handle, b.handle, y.handle, M, N, K, batch, bb, F32)
-        self.gemm = lambda a, b, c, y, M, N, K, tb: call(
+        # dt F32W16: the weight operand (b / w) is fp16-resident
+        self.matmul = lambda a, b, y, M, N, K, batch, bb, dt=F32: call(
+            "di_matmul", ctx, a.handle, b.handle, y.handle, M, N, K, batch, bb, dt)
+        self.gemm = lambda a, b, c, y, M, N, K, tb, dt=F32: call(
             "di_gemm", ctx, a.handle, b.handle, c.handle if c is not None else 0, y.handle, M, N,
-            K, tb, F32)
-        self.conv_mm = lambda x, w, bias, y, n, cin, cout, h, wd, k, s, pad, flags=0: call(
+            K, tb, dt)
+        self.conv_mm = lambda x, w, bias, y, n, cin, cout, h, wd, k, s, pad, flags=0, dt=F32: call(
             "di_conv2d", ctx, x.handle, w.handle, bias.handle if bias is not None else 0, 0,
-            y.handle, n, cin, cout, h, wd, k, s, pad, flags, F32, NCHW)
+            y.handle, n, cin, cout, h, wd, k, s, pad, flags, dt, NCHW)
+        self.convert = lambda x, sdt, y, ddt, n: call("di_convert", ctx, x.handle, sdt, y.handle,
+                                                      ddt, n)
         self.resize_nearest = lambda x, y, planes, hi, wi, ho, wo: call(
             "di_resize_nearest", ctx, x.handle, y.handle, planes, hi, wi, ho, wo, F32)
         self.reduce_mean = lambda x, y, inner, rows: call("di_reduce_mean", ctx, x.handle, y.handle,
@@ -395,7 +412,7 @@ def _passthrough_with_dims(x, new_dims):
             dtype = x.dtype or _dtype_of(x.cpu_data)
             is_shape = x.is_shape if x.is_shape is not None else dtype in ("int64", "int32")
             return CpuTensor(x.cpu_data, new_dims, dtype, is_shape)
-    return Tensor(x.buf, new_dims)
+    return Tensor(x.buf, new_dims, getattr(x, "dtype", "float32"))
 
 
 def _trunc_div(a: np.ndarray, b: np.ndarray) -> np.ndarray:
@@ -882,7 +899,8 @@ def _matmul(ctx, node, inputs):
     if batch == 1 and b_batch > 1:
         raise ValueError("MatMul: batched B with unbatched A not supported")
     out = ctx.pool.acquire(batch * M * N * 4)
-    ctx.dispatchers.matmul(a.buf, b.buf, out, M, N, K, batch, 1 if b_batch > 1 else 0)
+    ctx.dispatchers.matmul(a.buf, b.buf, out, M, N, K, batch, 1 if b_batch > 1 else 0,
+                           F32W16 if b.dtype == "float16" else F32)
     return Tensor(out, list(a.dims[:-2]) + [M, N])
 
 
@@ -894,7 +912,8 @@ def _gemm(ctx, node, inputs):
     M, K = a.dims
     N = b.dims[0] if tb else b.dims[1]
     out = ctx.pool.acquire(M * N * 4)
-    ctx.dispatchers.gemm(a.buf, b.buf, c.buf if c is not None else None, out, M, N, K, tb)
+    ctx.dispatchers.gemm(a.buf, b.buf, c.buf if c is not None else None, out, M, N, K, tb,
+                         F32W16 if b.dtype == "float16" else F32)
     return Tensor(out, [M, N])
 
 
@@ -919,7 +938,7 @@ def _conv(ctx, node, inputs):
     Ho, Wo = (H + 2 * P - K) // S + 1, (W + 2 * P - K) // S + 1
     out = ctx.pool.acquire(N * Cout * Ho * Wo * 4)
     ctx.dispatchers.conv_mm(x.buf, w.buf, bias.buf if bias is not None else None, out, N, Cin,
-                            Cout, H, W, K, S, P)
+                            Cout, H, W, K, S, P, 0, F32W16 if w.dtype == "float16" else F32)
     return Tensor(out, [N, Cout, Ho, Wo])
 
 
@@ -1702,6 +1721,10 @@ def infer_graph_io(nodes: List[Node], weight_names) -> dict:
 # ---------------------------------------------------------------- executor --
 METADATA_OPS = {"Reshape", "Shape", "Unsqueeze", "Squeeze", "Gather", "Slice", "Concat", "Constant",
                 "ConstantOfShape", "Cast", "Expand", "Equal", "Where", "Identity", "Transpose"}
+# fp16-resident weights: (op, input index) pairs that read them as they are;
+# relabelling ops pass the dtype on; every other consumer gets an fp32 copy
+F16_WEIGHT_INPUTS = {("MatMul", 1), ("Gemm", 1), ("Conv", 1)}
+F16_PASSTHROUGH = {"Reshape", "Unsqueeze", "Squeeze", "Identity", "Expand", "Shape"}
 BINARY_SHAPE_AWARE = {"Add", "Sub", "Mul", "Div"}
 
 
@@ -1755,6 +1778,14 @@ class Executor:
         self._temps.append(buf)
         return Tensor(buf, list(t.dims) if t.dims is not None else [f.size])
 
+    def _widen(self, t):
+        """fp16 device tensor -> fp32 copy (a pool buffer released at the end
+        of the run)."""
+        buf = self.pool.acquire(max(t.numel * 4, 4))
+        self.dispatchers.convert(t.buf, F16, buf, F32, t.numel)
+        self._temps.append(buf)
+        return Tensor(buf, list(t.dims))
+
     def run(self, inputs: Dict[str, Any]) -> Dict[str, Tensor]:
         """One forward pass.  ``inputs``: name -> Tensor | CpuTensor | numpy
         array (uploaded as fp32; float arrays keep their shape, int arrays
@@ -1795,6 +1826,11 @@ class Executor:
                     ins.append(self.weights.get(name))
                 else:
                     raise ExecutorError(f"tensor not found @{ni} {node.op_type}: {name}")
+            if node.op_type not in F16_PASSTHROUGH:
+                ins = [self._widen(t) if getattr(t, "dtype", None) == "float16" and
+                       getattr(t, "buf", None) is not None and
+                       (node.op_type, k) not in F16_WEIGHT_INPUTS else t
+                       for k, t in enumerate(ins)]
             if node.op_type not in METADATA_OPS:
                 keep_int = node.op_type in BINARY_SHAPE_AWARE
                 promoted = []

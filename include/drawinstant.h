@@ -40,6 +40,11 @@ typedef uint64_t di_handle;
 /* ---- dtypes (per tensor argument unless stated) ---- */
 #define DI_F32 0
 #define DI_F16 1
+/* di_matmul / di_gemm / di_conv2d (NCHW) only: fp32 activations, outputs and
+ * biases with the B operand (the weights) stored in fp16 and widened exactly
+ * to fp32 as it loads, so results equal DI_F32 on the widened weights while
+ * the weights keep half the bytes (the executor's fp16-resident weights). */
+#define DI_F32W16 2
 
 /* ---- activation layouts ---- */
 #define DI_NCHW 0 /* reference layout (wgsl-executor.js Tensor dims) */

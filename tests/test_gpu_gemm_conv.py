@@ -271,3 +271,86 @@ def test_conv_nchw_f32_via_f16_compute_cfg2(dev, rng):
     err = rel_l2(got, ref)
     print(f"   cfg2 rel-L2 {err:.2e} max-abs {np.max(np.abs(got - ref)):.2e}", flush=True)
     assert err <= 1e-2
+
+
+# ---------------- fp32 with fp16-resident weights (DI_F32W16) ----------------
+F32W16 = 2
+
+
+def _run_pair(dev, fn, make_args, w16):
+    """Run `fn` with the weight operand fp16 (DI_F32W16) and, on the same
+    fp16 values widened on the host, with DI_F32; both outputs."""
+    w32 = w16.astype(np.float32)
+    outs = []
+    for dt, w in ((F32W16, w16), (F32, w32)):
+        y, n, args = make_args(dev.storage(w))
+        _call(dev, fn, *args(dt))
+        outs.append(dev.download(y, np.float32, (n,)))
+    return outs
+
+
+@pytest.mark.parametrize("M,N,K,bb", [(77, 1280, 1024, 0), (4096, 320, 320, 0), (33, 45, 27, 0),
+                                      (64, 96, 64, 1), (1, 1280, 320, 0)])
+def test_matmul_w16_equals_widened(dev, rng, M, N, K, bb):
+    """Same plan and summation order: bit-identical to DI_F32 on the widened
+    weights, aligned and ragged (per-element B loads) shapes, shared and
+    batched B."""
+    batch = 3 if bb else 1
+    a = rng.standard_normal((batch, M, K)).astype(np.float32)
+    w = (rng.standard_normal(((batch if bb else 1), K, N)) / math.sqrt(K)).astype(np.float16)
+    ba = dev.storage(a)
+
+    def make(bw):
+        y = dev.create_buffer(batch * M * N * 4)
+        return y, batch * M * N, lambda dt: (ba.handle, bw.handle, y.handle, M, N, K, batch, bb,
+                                             dt)
+    w16, w32 = _run_pair(dev, "di_matmul", make, w)
+    assert np.array_equal(w16, w32)
+    ref = oracle.matmul(a, w.astype(np.float32), batched_b=bool(bb))
+    assert max_rel(w16.reshape(ref.shape), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("trans_b", [0, 1])
+def test_gemm_w16_equals_widened(dev, rng, trans_b):
+    M, N, K = 2, 1280, 320  # the time-embedding linear
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K) if trans_b else (K, N)) * 0.05).astype(np.float16)
+    c = rng.standard_normal(N).astype(np.float32)
+    ba, bc = dev.storage(a), dev.storage(c)
+
+    def make(bw):
+        y = dev.create_buffer(M * N * 4)
+        return y, M * N, lambda dt: (ba.handle, bw.handle, bc.handle, y.handle, M, N, K, trans_b,
+                                     dt)
+    w16, w32 = _run_pair(dev, "di_gemm", make, w)
+    assert np.array_equal(w16, w32)
+
+
+@pytest.mark.parametrize("cin,cout,h,k,s", [(320, 320, 16, 3, 1), (4, 320, 16, 3, 1),
+                                            (64, 128, 8, 1, 1), (128, 128, 16, 3, 2)])
+def test_conv_nchw_w16_equals_widened(dev, rng, cin, cout, h, k, s):
+    x = rng.standard_normal((1, cin, h, h)).astype(np.float32)
+    w = (rng.standard_normal((cout, cin, k, k)) / math.sqrt(cin * k * k)).astype(np.float16)
+    bias = rng.standard_normal(cout).astype(np.float32) * 0.1
+    pad = k // 2
+    ho = (h + 2 * pad - k) // s + 1
+    bx, bbias = dev.storage(x), dev.storage(bias)
+
+    def make(bw):
+        y = dev.create_buffer(cout * ho * ho * 4)
+        return y, cout * ho * ho, lambda dt: (bx.handle, bw.handle, bbias.handle, 0, y.handle, 1,
+                                              cin, cout, h, h, k, s, pad, 0, dt, NCHW)
+    w16, w32 = _run_pair(dev, "di_conv2d", make, w)
+    assert np.array_equal(w16, w32)
+    ref = oracle.conv2d(x, w.astype(np.float32), bias, stride=s, pad=pad)
+    assert max_rel(w16.reshape(ref.shape), ref) <= 1e-4
+
+
+def test_w16_rejected_outside_contractions(dev):
+    import drawinstant
+    x = dev.create_buffer(64)
+    with pytest.raises(drawinstant.DiError):
+        _call(dev, "di_unary", 0, x.handle, x.handle, 16, F32W16)
+    with pytest.raises(drawinstant.DiError):  # NHWC conv is fp16 already
+        _call(dev, "di_conv2d", x.handle, x.handle, 0, 0, x.handle, 1, 8, 8, 1, 1, 1, 1, 0, 0,
+              F32W16, NHWC)

@@ -59,3 +59,43 @@ def test_exported_block(dev, cases, key, fused):
         assert rel_l2(out[0], y) <= 2e-3
     else:
         assert rel_l2(out[0], y) <= 1e-5 and max_rel(out[0], y) <= 1e-4
+
+
+def as_fp16_file(g):
+    """The same graph as an fp16 ONNX file would carry it (float initializers
+    in fp16), like the SD-Turbo U-Net's."""
+    g = copy.deepcopy(g)
+    for t in g.tensors.values():
+        if t.dtype == "float32":
+            t.data = t.array().astype(np.float16).tobytes()
+            t.dtype = "float16"
+    return g
+
+
+@pytest.mark.parametrize("key", ["sdpa", "resnet"])
+@pytest.mark.parametrize("fused", [False, True])
+def test_fp16_resident_weights(dev, cases, key, fused):
+    """WeightCache(keep_f16=True): MatMul / Gemm / Conv weights stay fp16 on
+    the device (DI_F32W16) and the run is bit-identical to the reference's
+    widen-on-upload path, with the weight bytes nearly halved."""
+    data, feeds, y = cases[key]
+    g = as_fp16_file(parse_onnx_graph(data))
+    if fused:
+        optimize_graph(g)
+    outs, nbytes = [], []
+    for keep in (False, True):
+        wc = WeightCache(dev, g.tensors, keep_f16=keep)
+        ex = Executor(dev, g, wc)
+        try:
+            t = ex.run(feeds)["y"]
+            outs.append(dev.download(t.buf, np.float32, tuple(t.dims)))
+            t.buf.destroy()
+            nbytes.append(wc.device_bytes)
+        finally:
+            ex.destroy()
+            wc.destroy()
+    print(f"[onnx-f16] {key} fused={fused} weight bytes {nbytes[0]} -> {nbytes[1]} "
+          f"rel_l2 vs fp64 {rel_l2(outs[1], y):.2e}", flush=True)
+    assert np.array_equal(outs[0], outs[1])
+    assert nbytes[1] < 0.56 * nbytes[0]
+    assert rel_l2(outs[1], y) <= 5e-3  # fp16-rounded weights
