@@ -29,6 +29,10 @@ HIP events on the library's stream over exactly K graph-replayed steps
   optimize_graph, wall ms per run.
 * `executor_onnx_cfg4` (unless --no-blocks): the same for a real ONNX file,
   torch.onnx's export of the cfg4 transformer block, through the parser.
+* `vae_decode_512` (unless --no-blocks): SD's VAE decoder as the native
+  di_vae object, [1,4,64,64] -> [1,3,512,512], graph replay, TFLOP/s over
+  the decode's 2.51 TFLOP; `executor_vae_decode_512`: the same decode the
+  way vae-wgsl.js runs it, the exported decoder through parser + executor.
 """
 import argparse
 import json
@@ -327,6 +331,80 @@ def bench_executor_onnx(dev, reps=5):
     return row
 
 
+def bench_vae(dev, iters=10):
+    """SD's VAE decoder as one native object (di_vae_decode): latent
+    [1,4,64,64] -> image [1,3,512,512], seeded weights, graph replay; HIP
+    events on the library stream."""
+    from drawinstant import perf
+    from drawinstant.vae import VAE
+    v = VAE(dev, seed=0)
+    z = dev.create_buffer(4 * 64 * 64 * 4)
+    dev.fill_normal(z, 4 * 64 * 64, 11)
+    img = dev.create_buffer(3 * 512 * 512 * 4)
+    try:
+        run = lambda i: v.decode(z, img, 1, 64, 64, graph=True)
+        run(0)
+        run(0)
+        ms = timed(dev, run, iters)
+        out = dev.download(img, np.float32, (3 * 512 * 512,))
+        fl = perf.vae_work().total
+        return {"ms": round(ms, 3), "gflop": round(fl / 1e9, 1),
+                "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                "mfma_frac": round(fl / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, 4),
+                "image_finite": bool(np.isfinite(out).all())}
+    finally:
+        z.destroy()
+        img.destroy()
+        v.destroy()
+
+
+def bench_executor_vae(dev, reps=3):
+    """The VAE decode of vae-wgsl.js: torch.onnx's export of SD's VAE decoder
+    (post_quant_conv + Decoder, channels 128/256/512/512, seeded weights,
+    latent [1,4,64,64] -> image [1,3,512,512]) parsed and run by Executor op
+    by op, after optimize_graph, and with fp16-resident weights; wall ms per
+    decode (median of `reps`)."""
+    import copy
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from golden import onnx_export
+    from drawinstant.executor import Executor, Tensor, WeightCache, optimize_graph
+    from drawinstant.onnx_parser import parse_onnx_graph
+    data, feeds, _ = onnx_export.vae_case(channels=(128, 256, 512, 512), latent_hw=64,
+                                          expected=False)
+    graph = parse_onnx_graph(data)
+    del data
+    z = dev.storage(feeds["latent"] / 0.18215)  # vae-wgsl.js scaling
+    seeds = {"latent": Tensor(z, [1, 4, 64, 64])}
+    row = {"exported_nodes": len(graph.nodes), "weights_mb": round(graph.bytes / 2 ** 20, 1)}
+    for key in ("unfused", "fused", "fused_f16_resident"):
+        g = copy.deepcopy(graph)
+        if key != "unfused":
+            row.setdefault("rewrites", {k: v for k, v in optimize_graph(g).items() if v})
+        if "f16" in key:
+            for t in g.tensors.values():
+                if t.dtype == "float32":
+                    t.data, t.dtype = t.array().astype(np.float16).tobytes(), "float16"
+        wc = WeightCache(dev, g.tensors, keep_f16="f16" in key)
+        ex = Executor(dev, g, wc)
+        ts = []
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            outs = ex.run(seeds)
+            dt = (time.perf_counter() - t0) * 1e3
+            for o in outs.values():
+                if o.buf is not None:
+                    o.buf.destroy()
+            if r:
+                ts.append(dt)
+        ts.sort()
+        row[key] = {"ms": round(ts[len(ts) // 2], 2), "nodes": len(g.nodes),
+                    "pool_peak_buffers": ex.pool.peak}
+        ex.destroy()
+        wc.destroy()
+    z.destroy()
+    return row
+
+
 ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_gemm_conv3x3_64x64x320_pmc.md")
 
 
@@ -465,6 +543,8 @@ def main():
                               for kk, vv in v.items()} for k, v in blk.items()}
         line["executor_rewrites"] = bench_executor_rewrites(dev)
         line["executor_onnx_cfg4"] = bench_executor_onnx(dev)
+        line["vae_decode_512"] = bench_vae(dev)
+        line["executor_vae_decode_512"] = bench_executor_vae(dev)
     print(json.dumps(line), flush=True)
 
 

@@ -22,6 +22,17 @@ void launch_layout(hipStream_t s, const void* src, int sdt, int slay, void* dst,
 void launch_fill_normal(hipStream_t s, void* dst, int dt, uint64_t n, uint64_t seed,
                         float mean, float std);
 void launch_fill_const(hipStream_t s, void* dst, int dt, uint64_t n, float v);
+// Row softmax of [rows][inner] (in place allowed).
+void launch_softmax(hipStream_t s, const void* x, void* y, uint32_t inner, uint32_t rows, int dt);
+// fp16 per-batch matrix transpose: y[b][c][r] = x[b * sx + r * ldx + c] for
+// r < rows, c < cols (strides below 2^32).
+void launch_transpose_f16(hipStream_t s, const f16* x, uint32_t ldx, uint32_t sx, f16* y,
+                          uint32_t batch, uint32_t rows, uint32_t cols);
+// VAE decoder input: y[b][p][c] (NHWC fp16, cpad channels, zeros past C) =
+// bias[c] + sum_ci w[c][ci] * scale * z[b][ci][p] (post_quant_conv, 1x1).
+void launch_vae_latent_in(hipStream_t s, const float* z, const float* w, const float* bias,
+                          float scale, f16* y, uint32_t B, uint32_t C, uint32_t HW,
+                          uint32_t cpad);
 
 // ---- normalisation (k_norm.hip) ----
 // NCHW group norm (single pass with a cross-workgroup barrier when the group

@@ -392,6 +392,27 @@ uint64_t max_offset(const Idx4& c, const uint32_t* extra_start) {
 
 }  // namespace
 
+namespace di {
+
+void launch_softmax(hipStream_t s, const void* x, void* y, uint32_t inner, uint32_t rows,
+                    int dt) {
+  if (rows == 0) return;
+  const unsigned g = (rows + 3) / 4;
+  if (dt == DI_F32) k_softmax<float><<<g, 256, 0, s>>>((const float*)x, (float*)y, inner, rows);
+  else k_softmax<f16><<<g, 256, 0, s>>>((const f16*)x, (f16*)y, inner, rows);
+}
+
+void launch_transpose_f16(hipStream_t s, const f16* x, uint32_t ldx, uint32_t sx, f16* y,
+                          uint32_t batch, uint32_t rows, uint32_t cols) {
+  Idx4 c;
+  const uint32_t dim[3] = {batch, cols, rows}, s0[3] = {sx, ldx, 1}, perm[3] = {0, 2, 1};
+  (void)fill_idx4(&c, 3, dim, s0, perm, "launch_transpose_f16");
+  const uint64_t n = (uint64_t)batch * rows * cols;
+  if (n) k_transpose<f16><<<grid_for(n), kBlock, 0, s>>>(x, y, c, n);
+}
+
+}  // namespace di
+
 extern "C" {
 
 int32_t di_convert(di_ctx* ctx, di_handle src, int32_t sdt, di_handle dst, int32_t ddt,

@@ -84,3 +84,27 @@ def unet_work(B=1, H=64, W=64, ch=(320, 640, 1280, 1280), xattn=(1, 1, 1, 0), L=
 def gn_silu_bytes(N, C, HW, elem=4):
     """cfg1 algorithmic traffic: read x, write y, read gamma/beta."""
     return 2 * N * C * HW * elem + 2 * C * 4
+
+
+def vae_work(B=1, H=64, W=64, ch=(128, 256, 512, 512), L=2, latent=4, out=3) -> Work:
+    """Dense FLOPs of SD's VAE decode (post_quant_conv + Decoder) for a
+    [B, latent, H, W] latent: convs, the mid attention (QKV, scores, PV,
+    out projection); norms and element-wise work are not counted."""
+    w = Work()
+    rev = list(reversed(ch))
+    w.add("conv", conv_flops(B, latent, latent, H, W, 1) + conv_flops(B, latent, rev[0], H, W, 3))
+    hh, ww = H, W
+    for _ in range(2):
+        resnet_flops(w, B, rev[0], rev[0], hh, ww, temb_dim=0)
+    S, C = hh * ww, rev[0]
+    w.add("attention", 2.0 * B * S * C * 3 * C + 4.0 * B * S * S * C + 2.0 * B * S * C * C)
+    prev = rev[0]
+    for i, c in enumerate(rev):
+        for j in range(L + 1):
+            resnet_flops(w, B, prev if j == 0 else c, c, hh, ww, temb_dim=0)
+        prev = c
+        if i < 3:
+            hh, ww = hh * 2, ww * 2
+            w.add("upsample_conv", conv_flops(B, c, c, hh, ww, 3))
+    w.add("conv", conv_flops(B, rev[-1], out, hh, ww, 3))
+    return w

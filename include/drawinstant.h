@@ -392,6 +392,46 @@ int32_t di_unet_forward(di_ctx* ctx, di_unet* unet, di_handle sample, di_handle 
                         di_handle context, di_handle out, uint32_t B, uint32_t H,
                         uint32_t W, uint32_t Sctx, int32_t flags);
 
+/* ======================= VAE decoder ======================= */
+
+/* SD's AutoencoderKL decode path (post_quant_conv + Decoder): the model
+ * vae-wgsl.js runs through the executor (vae_decoder/model.onnx,
+ * vae-wgsl.js:28-140), here as one native object on NHWC fp16 activations. */
+typedef struct {
+  uint32_t latent_channels;   /* 4 */
+  uint32_t out_channels;      /* 3 */
+  uint32_t block_channels[4]; /* 128, 256, 512, 512 (encoder order; the decoder runs them reversed) */
+  uint32_t layers_per_block;  /* 2: each decoder up block has layers_per_block + 1 ResNets */
+  uint32_t groups;            /* 32 */
+  float eps;                  /* 1e-6 (every GroupNorm) */
+} di_vae_config;
+
+typedef struct di_vae di_vae;
+
+#define DI_VAE_GRAPH 1 /* capture the decode in a HIP graph once, replay after */
+
+int32_t di_vae_default_config(di_vae_config* cfg);
+/* Build the decoder with seeded random weights; cfg = NULL selects SD's.
+ * Replaces loadVAEWGSL (vae-wgsl.js:28-72). */
+int32_t di_vae_create(di_ctx* ctx, const di_vae_config* cfg, uint64_t seed, di_vae** out);
+int32_t di_vae_destroy(di_ctx* ctx, di_vae* vae);
+int32_t di_vae_num_params(di_ctx* ctx, di_vae* vae, uint32_t* n_tensors, uint64_t* n_elements);
+/* Same layout tags as di_unet_param_info (convs OHWI fp16, conv_in's input
+ * channels padded to 8, attention to_q/to_k/to_v stacked [3C][C] with a [3C]
+ * bias; post_quant_conv fp32 [C][C]). */
+int32_t di_vae_param_info(di_ctx* ctx, di_vae* vae, uint32_t index, char* name,
+                          uint32_t name_cap, uint32_t* dims, uint32_t* ndims, int32_t* dtype,
+                          int32_t* layout);
+int32_t di_vae_param_download(di_ctx* ctx, di_vae* vae, uint32_t index, void* dst,
+                              uint64_t bytes);
+int32_t di_vae_param_upload(di_ctx* ctx, di_vae* vae, uint32_t index, const void* src,
+                            uint64_t bytes);
+/* vaeDecodeWGSL (vae-wgsl.js:94-140): latent fp32 [B][4][H][W] times `scale`
+ * (the caller's 1 / 0.18215) -> image fp32 [B][3][8H][8W] (NCHW).  Enqueues
+ * only; DI_VAE_GRAPH replays a captured graph. */
+int32_t di_vae_decode(di_ctx* ctx, di_vae* vae, di_handle latent, di_handle image,
+                      uint32_t B, uint32_t H, uint32_t W, float scale, int32_t flags);
+
 /* ======================= Euler Discrete scheduler ======================= */
 /* The per-element halves of makeEulerScheduler / sampleNoiseLatent
  * (scheduler.js:77-134) on the device; the schedule constants (timesteps,

@@ -120,6 +120,78 @@ class ResnetBlock2D(nn.Module):
         return self.conv_shortcut(x) + h
 
 
+class VAEResnet(nn.Module):
+    """The VAE decoder's ResnetBlock2D: no time embedding, eps 1e-6."""
+
+    def __init__(self, cin, cout):
+        super().__init__()
+        self.norm1 = nn.GroupNorm(32, cin, eps=1e-6)
+        self.conv1 = nn.Conv2d(cin, cout, 3, padding=1)
+        self.norm2 = nn.GroupNorm(32, cout, eps=1e-6)
+        self.conv2 = nn.Conv2d(cout, cout, 3, padding=1)
+        self.conv_shortcut = nn.Conv2d(cin, cout, 1) if cin != cout else None
+
+    def forward(self, x):
+        h = self.conv1(F.silu(self.norm1(x)))
+        h = self.conv2(F.silu(self.norm2(h)))
+        return (x if self.conv_shortcut is None else self.conv_shortcut(x)) + h
+
+
+class VAEAttention(nn.Module):
+    """The mid-block attention: GroupNorm, one head over all channels,
+    residual."""
+
+    def __init__(self, C):
+        super().__init__()
+        self.group_norm = nn.GroupNorm(32, C, eps=1e-6)
+        self.to_q, self.to_k, self.to_v = nn.Linear(C, C), nn.Linear(C, C), nn.Linear(C, C)
+        self.to_out = nn.Linear(C, C)
+
+    def forward(self, x):
+        b, c, h, w = x.shape
+        t = self.group_norm(x).reshape(b, c, h * w).transpose(1, 2)
+        q, k, v = (f(t).unsqueeze(1) for f in (self.to_q, self.to_k, self.to_v))
+        o = F.scaled_dot_product_attention(q, k, v).squeeze(1)
+        return self.to_out(o).transpose(1, 2).reshape(b, c, h, w) + x
+
+
+class VAEDecoder(nn.Module):
+    """AutoencoderKL's post_quant_conv + Decoder as SD uses them: conv_in,
+    mid (ResNet, attention, ResNet), four up blocks of three ResNets with a
+    nearest-x2 + conv3x3 upsampler on all but the last, GroupNorm, SiLU,
+    conv_out to RGB.  channels = block_out_channels (SD: 128, 256, 512,
+    512)."""
+
+    def __init__(self, channels=(128, 256, 512, 512), latent=4):
+        super().__init__()
+        rev = list(reversed(channels))
+        self.post_quant_conv = nn.Conv2d(latent, latent, 1)
+        self.conv_in = nn.Conv2d(latent, rev[0], 3, padding=1)
+        self.mid = nn.ModuleList([VAEResnet(rev[0], rev[0]), VAEAttention(rev[0]),
+                                  VAEResnet(rev[0], rev[0])])
+        self.ups = nn.ModuleList()
+        self.upconvs = nn.ModuleList()
+        prev = rev[0]
+        for i, c in enumerate(rev):
+            self.ups.append(nn.ModuleList([VAEResnet(prev if j == 0 else c, c) for j in range(3)]))
+            self.upconvs.append(nn.Conv2d(c, c, 3, padding=1) if i < len(rev) - 1 else
+                                nn.Identity())
+            prev = c
+        self.norm_out = nn.GroupNorm(32, rev[-1], eps=1e-6)
+        self.conv_out = nn.Conv2d(rev[-1], 3, 3, padding=1)
+
+    def forward(self, z):
+        h = self.conv_in(self.post_quant_conv(z))
+        for m in self.mid:
+            h = m(h)
+        for i, blocks in enumerate(self.ups):
+            for m in blocks:
+                h = m(h)
+            if i < len(self.ups) - 1:
+                h = self.upconvs[i](F.interpolate(h, scale_factor=2.0, mode="nearest"))
+        return self.conv_out(F.silu(self.norm_out(h)))
+
+
 def _seeded(module: nn.Module, seed: int) -> nn.Module:
     g = torch.Generator().manual_seed(seed)
     with torch.no_grad():
@@ -176,3 +248,13 @@ def resnet_case(cin=64, cout=128, H=8, W=8, temb_dim=256, seed=0):
     t = torch.randn(1, temb_dim, generator=g)
     data = export(m, (x, t), ("x", "temb"))
     return data, {"x": x.numpy(), "temb": t.numpy()}, _expected(m, (x, t))
+
+
+def vae_case(channels=(32, 32, 64, 64), latent_hw=8, seed=0, expected=True):
+    """(onnx bytes, {"latent": array}, expected image or None) for the VAE
+    decoder; SD's decoder is channels (128, 256, 512, 512) at latent 64x64."""
+    m = _seeded(VAEDecoder(channels), seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    z = torch.randn(1, 4, latent_hw, latent_hw, generator=g)
+    data = export(m, (z,), ("latent",), output_name="sample")
+    return data, {"latent": z.numpy()}, (_expected(m, (z,)) if expected else None)

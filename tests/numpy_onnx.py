@@ -113,6 +113,16 @@ def _fused_attention(n, i):
     return o.reshape(q.shape[:-1] + (v.shape[-1],))
 
 
+def _resize_nearest(n, i):
+    """Resize, mode nearest with asymmetric coordinates and floor rounding:
+    out[o] = in[floor(o / scale)] on each axis."""
+    assert get_attr_string(n, "mode", "nearest") == "nearest"
+    x, scales = i[0], np.asarray(i[2], np.float64)
+    idx = [np.minimum(np.floor(np.arange(int(np.floor(d * sc))) / sc).astype(np.int64), d - 1)
+           for d, sc in zip(x.shape, scales)]
+    return x[np.ix_(*idx)]
+
+
 def _constant(n, i):
     t = next(a for a in n.attributes if a.name == "value").t
     return t.array().reshape(t.dims) if t.dims else t.array().reshape(())
@@ -141,6 +151,10 @@ OPS = {
     "Unsqueeze": lambda n, i: np.expand_dims(i[0], tuple(
         int(a) for a in (i[1] if len(i) > 1 and i[1] is not None else
                          get_attr_ints(n, "axes", None)))),
+    "Squeeze": lambda n, i: np.squeeze(i[0], tuple(
+        int(a) for a in (i[1] if len(i) > 1 and i[1] is not None else
+                         get_attr_ints(n, "axes", None)))),
+    "Resize": lambda n, i: _resize_nearest(n, i),
     "Gather": lambda n, i: np.take(i[0], i[1], axis=get_attr_int(n, "axis", 0)),
     "Concat": lambda n, i: np.concatenate(i, axis=get_attr_int(n, "axis", 0)),
     "InstanceNormalization": _instance_norm, "Conv": _conv, "Gemm": _gemm,

@@ -1,11 +1,12 @@
 """GPU: real ONNX graphs through the parser and the executor.
 
 torch.onnx exports (opset 14) of a diffusers-style Transformer2D block
-(scaled_dot_product_attention and eager attention) and a ResnetBlock2D are
+(scaled_dot_product_attention and eager attention), a ResnetBlock2D and a
+reduced-width VAE decoder (channels 32/32/64/64, latent 8x8) are
 parsed by drawinstant.onnx_parser and run by Executor, op by op as the
 reference's executor would and after optimize_graph, against the modules'
-float64 outputs.  Tolerances: the op-by-op fp32 path rel-L2 <= 1e-5 and
-max-rel <= 1e-4; the optimized graph the same except where flash attention
+float64 outputs.  Tolerances: the op-by-op fp32 path rel-L2 <= 1e-5 (1e-4
+for the 35-convolution VAE) and max-rel <= 1e-4; the optimized graph the same except where flash attention
 (fp16 MFMA operands) is in the path: rel-L2 <= 2e-3.
 """
 import copy
@@ -24,7 +25,7 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module")
 def cases():
     return {"sdpa": onnx_export.transformer_case(), "eager": onnx_export.transformer_case(eager=True),
-            "resnet": onnx_export.resnet_case()}
+            "resnet": onnx_export.resnet_case(), "vae": onnx_export.vae_case()}
 
 
 def run(dev, g, feeds, reps=1):
@@ -34,7 +35,7 @@ def run(dev, g, feeds, reps=1):
         res = []
         for _ in range(reps):
             outs = ex.run(feeds)
-            t = outs["y"]
+            t = outs["sample" if "sample" in outs else "y"]
             res.append(dev.download(t.buf, np.float32, tuple(t.dims)))
             t.buf.destroy()
         return res
@@ -43,7 +44,7 @@ def run(dev, g, feeds, reps=1):
         wc.destroy()
 
 
-@pytest.mark.parametrize("key", ["sdpa", "eager", "resnet"])
+@pytest.mark.parametrize("key", ["sdpa", "eager", "resnet", "vae"])
 @pytest.mark.parametrize("fused", [False, True])
 def test_exported_block(dev, cases, key, fused):
     data, feeds, y = cases[key]
@@ -58,7 +59,10 @@ def test_exported_block(dev, cases, key, fused):
     if fused and key != "resnet":
         assert rel_l2(out[0], y) <= 2e-3
     else:
-        assert rel_l2(out[0], y) <= 1e-5 and max_rel(out[0], y) <= 1e-4
+        # the VAE chains 35 fp32 convolutions and 30 GroupNorms (variance as
+        # E[x^2] - E[x]^2, the reference's formula): rel-L2 1e-4 there
+        assert rel_l2(out[0], y) <= (1e-4 if key == "vae" else 1e-5)
+        assert max_rel(out[0], y) <= 1e-4
 
 
 def as_fp16_file(g):
@@ -72,7 +76,7 @@ def as_fp16_file(g):
     return g
 
 
-@pytest.mark.parametrize("key", ["sdpa", "resnet"])
+@pytest.mark.parametrize("key", ["sdpa", "resnet", "vae"])
 @pytest.mark.parametrize("fused", [False, True])
 def test_fp16_resident_weights(dev, cases, key, fused):
     """WeightCache(keep_f16=True): MatMul / Gemm / Conv weights stay fp16 on
@@ -87,7 +91,8 @@ def test_fp16_resident_weights(dev, cases, key, fused):
         wc = WeightCache(dev, g.tensors, keep_f16=keep)
         ex = Executor(dev, g, wc)
         try:
-            t = ex.run(feeds)["y"]
+            outs_run = ex.run(feeds)
+            t = outs_run["sample" if "sample" in outs_run else "y"]
             outs.append(dev.download(t.buf, np.float32, tuple(t.dims)))
             t.buf.destroy()
             nbytes.append(wc.device_bytes)

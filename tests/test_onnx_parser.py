@@ -9,7 +9,7 @@ rewrites on real exported graphs.
   float_data, negative int64 attributes as 10-byte varints) and its
   recovery paths (a garbage prefix, a truncated file).
 * torch.onnx exports of a diffusers-style Transformer2D block (SDPA and eager
-  attention) and ResnetBlock2D: parsed initializers equal the module's
+  attention), ResnetBlock2D and a reduced-width VAE decoder: parsed initializers equal the module's
   parameters, the graph evaluated by the numpy interpreter equals torch's
   float64 output, and so does the graph after optimize_graph, whose rewrite
   counts are checked.
@@ -153,7 +153,7 @@ def test_recovery_paths():
 @pytest.fixture(scope="module")
 def cases():
     return {"sdpa": onnx_export.transformer_case(), "eager": onnx_export.transformer_case(eager=True),
-            "resnet": onnx_export.resnet_case()}
+            "resnet": onnx_export.resnet_case(), "vae": onnx_export.vae_case()}
 
 
 def max_rel(a, b):
@@ -184,19 +184,21 @@ def test_exported_transformer_parses(cases, tmp_path):
     ("sdpa", {"mul_add": 4, "group_norm": 1, "layer_norm": 3, "gelu": 1, "attention": 2}),
     ("eager", {"mul_add": 4, "group_norm": 1, "layer_norm": 3, "gelu": 1, "attention": 2}),
     ("resnet", {"silu": 3, "mul_add": 2, "group_norm": 2, "group_norm_silu": 2}),
+    ("vae", {"silu": 29, "mul_add": 30, "group_norm": 30, "group_norm_silu": 29, "attention": 1}),
 ])
 def test_exported_graphs_rewrite_and_evaluate(cases, key, want):
     """torch's float64 output = the parsed graph's = the rewritten graph's."""
     data, feeds, y = cases[key]
+    out = "sample" if key == "vae" else "y"
     g = parse_onnx_graph(data)
-    assert max_rel(numpy_onnx.run(g, feeds)["y"], y) <= 1e-5
+    assert max_rel(numpy_onnx.run(g, feeds)[out], y) <= 1e-5
     g2 = copy.deepcopy(g)
     st = optimize_graph(g2)
     assert {k: v for k, v in st.items() if v} == want
-    assert max_rel(numpy_onnx.run(g2, feeds)["y"], y) <= 1e-5
+    assert max_rel(numpy_onnx.run(g2, feeds)[out], y) <= 1e-5
     ops = [n.op_type for n in g2.nodes]
     assert "Softmax" not in ops and "Erf" not in ops and "InstanceNormalization" not in ops
-    if key != "resnet":
+    if key in ("sdpa", "eager"):
         fa = [n for n in g2.nodes if n.op_type == "FusedAttention"]
         # head split / merge Transposes folded: [B, S, H, d] in and out
         assert all(get_attr_string(n, "layout", "") == "bshd" for n in fa)
