@@ -55,8 +55,17 @@ int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rs
 
 int gn_nhwc(Ctx* c, NhwcSrc x, const float* g, const float* b, f16* y, uint32_t N, uint32_t C,
             uint32_t G, uint32_t HW, float eps, bool silu, const GnStats* st = nullptr) {
-  if (st && launch_group_norm_nhwc_st(c->stream, x, *st, g, b, y, N, C, G, HW, eps, silu))
-    return DI_OK;
+  if (st) {
+    float* fold = nullptr;
+    if (const uint64_t nf = gn_fold_ws_floats(N, C, HW)) {
+      void* ws = nullptr;
+      int rc = workspace(c, nf * sizeof(float), &ws);
+      if (rc) return rc;
+      fold = (float*)ws;
+    }
+    if (launch_group_norm_nhwc_st(c->stream, x, *st, g, b, y, N, C, G, HW, eps, silu, fold))
+      return DI_OK;
+  }
   void* ws = nullptr;
   int rc = workspace(c, gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float), &ws);
   if (rc) return rc;

@@ -71,7 +71,11 @@ struct GnStats {
 // launch_group_norm_nhwc).
 bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st, const float* gamma,
                                const float* beta, void* y, uint32_t N, uint32_t C, uint32_t G,
-                               uint32_t HW, float eps, bool silu);
+                               uint32_t HW, float eps, bool silu, float* fold_ws = nullptr);
+// Floats of fold_ws for an [N][HW][C] input (0: no pre-fold at this size).
+// With fold_ws, statistics of large images are first summed to ~128 chunks
+// per image, so the apply workgroups do not each re-read all HW / 64.
+uint64_t gn_fold_ws_floats(uint32_t N, uint32_t C, uint32_t HW);
 void launch_group_norm_nhwc(hipStream_t s, NhwcSrc x, const float* gamma, const float* beta,
                             void* y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW,
                             float eps, bool silu, float* ws);

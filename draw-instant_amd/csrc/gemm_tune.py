@@ -1,11 +1,15 @@
 """Measure the best GEMM tile / split-K choice for every GEMM shape of one
-SD2.1 U-Net step and write them as gemm_tuned.inc (the table gemm_plan
-consults before its cost model).
+SD2.1 U-Net step (or one 512x512 VAE decode) and write them as
+gemm_tuned.inc (the table gemm_plan consults before its cost model).
 
-    python draw-instant_amd/csrc/gemm_tune.py [--out PATH] [--iters N]
+    python draw-instant_amd/csrc/gemm_tune.py [--model unet|vae] [--append]
+                                              [--out PATH] [--iters N]
 
-Needs the GPU and a built libdrawinstant_hip.so.  Steps:
-  1. one eager U-Net step with DI_TRACE_GEMM=1 lists its GEMM calls;
+--append keeps the table's existing rows and adds the shapes it lacks (so
+the VAE's shapes join the U-Net's).  Needs the GPU and a built
+libdrawinstant_hip.so.  Steps:
+  1. one eager U-Net step (VAE decode) with DI_TRACE_GEMM=1 lists its GEMM
+     calls;
   2. each distinct shape (M, N, K, conv geometry, GEGLU) is re-issued as a
      di_linear / di_conv2d call and timed for every (tile, splits) pair with
      DI_GEMM_TILE / DI_GEMM_SPLITS forcing the plan;
@@ -27,24 +31,31 @@ SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
 TRACE_RE = re.compile(r"\[di_gemm\] (.*)")
 
 
-def trace_step():
-    """GEMM calls of one eager 512x512 step (trace lines go to fd 2)."""
+def trace_step(model="unet"):
+    """GEMM calls of one eager 512x512 step / decode (trace lines go to fd 2)."""
     import numpy as np
     os.environ["DI_TRACE_GEMM"] = "1"
     import drawinstant
     from drawinstant.unet import UNet
+    from drawinstant.vae import VAE
     fd, path = tempfile.mkstemp(suffix=".log")
     saved = os.dup(2)
     os.dup2(fd, 2)
     try:
         dev = drawinstant.Device(0)
-        u = UNet(dev, seed=1)
         rng = np.random.default_rng(0)
         x = rng.standard_normal((1, 4, 64, 64)).astype(np.float32)
-        ctx = rng.standard_normal((1, 77, 1024)).astype(np.float32)
-        u(x, 999.0, ctx, graph=False)
-        dev.sync()
-        u.destroy()
+        if model == "vae":
+            v = VAE(dev, seed=1)
+            v(x, graph=False)
+            dev.sync()
+            v.destroy()
+        else:
+            u = UNet(dev, seed=1)
+            ctx = rng.standard_normal((1, 77, 1024)).astype(np.float32)
+            u(x, 999.0, ctx, graph=False)
+            dev.sync()
+            u.destroy()
         dev.destroy()
     finally:
         os.dup2(saved, 2)
@@ -70,14 +81,22 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=os.path.join(HERE, "gemm_tuned.inc"))
     ap.add_argument("--iters", type=int, default=10)
+    ap.add_argument("--model", choices=("unet", "vae"), default="unet")
+    ap.add_argument("--append", action="store_true")
     args = ap.parse_args()
-    calls = trace_step()
+    kept = []
+    if args.append and os.path.exists(args.out):
+        kept = [ln for ln in open(args.out) if ln.startswith("{")]
+    have = {tuple(int(v) for v in ln[1:ln.index("}")].split(",")[:8]) for ln in kept}
+    calls = trace_step(args.model)
     os.environ.pop("DI_TRACE_GEMM", None)
     shapes = {}
     for c in calls:
         if c["elem"] != "1" or c["fast"] != "1":
             continue
         k = key_of(c)
+        if k in have:
+            continue
         shapes.setdefault(k, [c, 0])[1] += 1
     print(f"[tune] {len(calls)} GEMM calls, {len(shapes)} distinct fast fp16 shapes", flush=True)
 
@@ -148,6 +167,8 @@ def main():
             for sp in SPLITS:
                 if sp > 1 and ((K + sp - 1) // sp + 63) // 64 * 64 < 256:
                     break
+                if sp > 2 and M >= 65536:  # thousands of tiles already
+                    break
                 os.environ["DI_GEMM_TILE"] = str(tile)
                 os.environ["DI_GEMM_SPLITS"] = str(sp)
                 us = t_us(fn, args.iters)
@@ -163,10 +184,13 @@ def main():
             b.destroy()
 
     with open(args.out, "w") as f:
-        f.write("// Measured GEMM plans for the SD2.1 U-Net step shapes (MI355X), written by\n")
-        f.write("//   python draw-instant_amd/csrc/gemm_tune.py\n")
+        f.write("// Measured GEMM plans for the SD2.1 U-Net step and VAE decode shapes (MI355X),\n")
+        f.write("// written by\n")
+        f.write("//   python draw-instant_amd/csrc/gemm_tune.py [--model vae --append]\n")
         f.write("// {M, N, K, conv, ks, stride, up, geglu, tile, splits},"
                 "  // best us / cost-model us, calls per step\n")
+        for ln in kept:
+            f.write(ln)
         for (M, N, K, conv, ks, stride, up, geglu), tile, sp, us, auto, count in rows:
             f.write(f"{{{M}, {N}, {K}, {conv}, {ks}, {stride}, {up}, {geglu}, {tile}, {sp}}},"
                     f"  // {us:.2f} / {auto:.2f} us, x{count}\n")

@@ -294,6 +294,46 @@ __global__ void k_softmax(const T* __restrict__ x, T* __restrict__ y, uint32_t i
   for (uint32_t j = lane; j < inner; j += kWave) yr[j] = (T)(__expf((float)xr[j] - m) * inv);
 }
 
+// fp16 rows of inner = 512 * NV elements (NV <= 8): one wavefront per row
+// holding the row in registers (NV 16-byte vectors per lane), so the row is
+// read once and written once.
+template <int NV>
+__global__ __launch_bounds__(256) void k_softmax_f16_reg(const f16* __restrict__ x,
+                                                         f16* __restrict__ y, uint32_t rows) {
+  const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  constexpr uint32_t inner = 512 * NV;
+  const f16* xr = x + (uint64_t)row * inner;
+  f16x8 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; i++) v[i] = *(const f16x8*)(xr + (i * kWave + lane) * 8);
+  float m = -3.0e38f;
+#pragma unroll
+  for (int i = 0; i < NV; i++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) m = fmaxf(m, (float)v[i][e]);
+  m = wave_max(m);
+  float ex[NV][8], s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; i++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      ex[i][e] = __expf((float)v[i][e] - m);
+      s += ex[i][e];
+    }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+  f16* yr = y + (uint64_t)row * inner;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = (f16)(ex[i][e] * inv);
+    *(f16x8*)(yr + (i * kWave + lane) * 8) = o;
+  }
+}
+
 template <typename T>
 __global__ void k_reduce_mean(const T* __restrict__ x, T* __restrict__ y, uint32_t inner,
                               uint32_t rows) {
@@ -398,6 +438,18 @@ void launch_softmax(hipStream_t s, const void* x, void* y, uint32_t inner, uint3
                     int dt) {
   if (rows == 0) return;
   const unsigned g = (rows + 3) / 4;
+  const bool al16 = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
+  if (dt == DI_F16 && al16 && inner % 512 == 0 && inner <= 4096) {
+    const f16* xp = (const f16*)x;
+    f16* yp = (f16*)y;
+    switch (inner / 512) {
+      case 1: k_softmax_f16_reg<1><<<g, 256, 0, s>>>(xp, yp, rows); return;
+      case 2: k_softmax_f16_reg<2><<<g, 256, 0, s>>>(xp, yp, rows); return;
+      case 4: k_softmax_f16_reg<4><<<g, 256, 0, s>>>(xp, yp, rows); return;
+      case 8: k_softmax_f16_reg<8><<<g, 256, 0, s>>>(xp, yp, rows); return;
+      default: break;
+    }
+  }
   if (dt == DI_F32) k_softmax<float><<<g, 256, 0, s>>>((const float*)x, (float*)y, inner, rows);
   else k_softmax<f16><<<g, 256, 0, s>>>((const f16*)x, (f16*)y, inner, rows);
 }
@@ -555,9 +607,7 @@ int32_t di_softmax(di_ctx* ctx, di_handle X, di_handle Y, uint32_t inner, uint32
   DI_BUF(ctx, X, x, n * dtype_size(dt));
   DI_BUF(ctx, Y, y, n * dtype_size(dt));
   if (rows == 0) return DI_OK;
-  unsigned g = (rows + 3) / 4;
-  if (dt == DI_F32) k_softmax<float><<<g, 256, 0, ctx->stream>>>((const float*)x->ptr, (float*)y->ptr, inner, rows);
-  else k_softmax<f16><<<g, 256, 0, ctx->stream>>>((const f16*)x->ptr, (f16*)y->ptr, inner, rows);
+  launch_softmax(ctx->stream, x->ptr, y->ptr, inner, rows, dt);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -346,15 +346,49 @@ __device__ __forceinline__ float gn_fold(const float* __restrict__ pn, uint32_t 
 // y = x*a[c] + b[c] (+SiLU) to its pixel block.  SW is a multiple of cpg and
 // of 8.  Thread t keeps vector t % NV of the slice for pixels t / NV + R*i.
 constexpr int kGnSliceMax = 128;
+// statistics of images with more than kGnFoldMin chunks (above 128 x 128
+// pixels) are pre-folded to about kGnFoldTarget chunks
+constexpr uint32_t kGnFoldMin = 256, kGnFoldTarget = 128;
 
+// Pre-fold of producer statistics for large images: every apply workgroup
+// otherwise re-reads all HW / 64 chunks of its channel slice (2 MB per
+// workgroup at 512 x 512).  out[n][k][c][2] = sum over chunks
+// [k * F, min((k + 1) * F, cpi)) of st[n][chunk][c][2]; one thread per
+// (channel, statistic) pair, consecutive threads on consecutive floats.
+__global__ __launch_bounds__(256) void k_gn_stats_fold(GnStats st, float* __restrict__ out,
+                                                       uint32_t C, uint32_t cpi, uint32_t F,
+                                                       uint32_t cpo) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x, k = blockIdx.y, n = blockIdx.z;
+  if (i >= 2 * C) return;
+  const uint32_t c = i / 2, sti = i % 2;
+  const bool first = c < st.c1;
+  const float* base = first ? st.s1 : st.s2;
+  const uint64_t ld = first ? st.ld1 : st.ld2;
+  const uint64_t cc = first ? c : c - st.c1;
+  const uint32_t k0 = k * F, k1 = min(k0 + F, cpi);
+  const float* p = base + ((uint64_t)n * cpi * ld + cc) * 2 + sti;
+  const uint64_t step = ld * 2;
+  // eight independent partial sums keep eight loads in flight
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  uint32_t j = k0;
+  for (; j + 8 <= k1; j += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] += p[(uint64_t)(j + u) * step];
+  }
+  for (; j < k1; j++) a[0] += p[(uint64_t)j * step];
+  out[(((uint64_t)n * cpo + k) * C + c) * 2 + sti] =
+      ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
+// cpi: statistics chunks per image in st (HW / 64 as the GEMM epilogue wrote
+// them, or fewer after k_gn_stats_fold).
 __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
     NhwcSrc x, GnStats st, const float* __restrict__ gamma, const float* __restrict__ beta,
     f16* __restrict__ y, uint32_t C, uint32_t cpg, uint32_t SW, uint32_t HW, uint32_t ppb,
-    float eps, int silu) {
+    float eps, int silu, uint32_t cpi) {
   __shared__ float chs[2][kGnSliceMax];
   __shared__ float gms[2][kGnSliceMax];
   const uint32_t tid = threadIdx.x, n = blockIdx.z, c0 = blockIdx.y * SW;
-  const uint32_t cpi = HW / 64;
   // apply mapping; the first round of pixels and gamma / beta are loaded
   // before the fold so the two memory round trips overlap
   const uint32_t NV = SW / 8, R = 256 / NV, v = tid % NV, lane = tid / NV;
@@ -806,12 +840,28 @@ bool gn_stats_slice(uint32_t C, uint32_t G, uint32_t HW, uint32_t* sw) {
   return false;
 }
 
-bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st, const float* gamma,
+uint64_t gn_fold_ws_floats(uint32_t N, uint32_t C, uint32_t HW) {
+  const uint32_t cpi = HW / 64;
+  if (cpi <= kGnFoldMin) return 0;
+  const uint32_t F = (cpi + kGnFoldTarget - 1) / kGnFoldTarget;
+  return (uint64_t)N * ((cpi + F - 1) / F) * C * 2;
+}
+
+bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st_in, const float* gamma,
                                const float* beta, void* y, uint32_t N, uint32_t C, uint32_t G,
-                               uint32_t HW, float eps, bool silu) {
+                               uint32_t HW, float eps, bool silu, float* fold_ws) {
   uint32_t sw = 0;
-  if (!gn_stats_slice(C, G, HW, &sw) || x.c1 % 8 != 0 || (st.c1 < C && st.c1 % 8 != 0))
+  if (!gn_stats_slice(C, G, HW, &sw) || x.c1 % 8 != 0 || (st_in.c1 < C && st_in.c1 % 8 != 0))
     return false;
+  GnStats st = st_in;
+  uint32_t cpi = HW / 64;
+  if (fold_ws && cpi > kGnFoldMin) {
+    const uint32_t F = (cpi + kGnFoldTarget - 1) / kGnFoldTarget, cpo = (cpi + F - 1) / F;
+    k_gn_stats_fold<<<dim3((2 * C + 255) / 256, cpo, N), 256, 0, s>>>(st_in, fold_ws, C, cpi, F,
+                                                                     cpo);
+    st = GnStats{fold_ws, fold_ws, C, C, C};
+    cpi = cpo;
+  }
   const uint32_t slices = C / sw, R = 256 / (sw / 8);
   // about 512 workgroups over the batch, at least one pixel per lane
   uint32_t pbs = 512 / (N * slices);
@@ -821,7 +871,7 @@ bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st, cons
   const uint32_t ppb = (HW + pbs - 1) / pbs;
   pbs = (HW + ppb - 1) / ppb;
   k_gn_nhwc_apply_st<<<dim3(pbs, slices, N), 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw,
-                                                          HW, ppb, eps, silu ? 1 : 0);
+                                                          HW, ppb, eps, silu ? 1 : 0, cpi);
   return true;
 }
 

@@ -242,9 +242,18 @@ int vae_decode_step(Ctx* c, Vae& v, const float* z, float* img, uint32_t B, uint
   auto st_of = [](const Act& a) { return GnStats{a.st.f(), a.st.f(), a.c, a.c, a.c}; };
   auto gn = [&](const Act& x, const float* g, const float* b, f16* y, uint32_t hw, bool silu) {
     const GnStats xs = st_of(x);
-    if (x.has_st && launch_group_norm_nhwc_st(c->stream, one(x.buf.h(), x.c), xs, g, b, y, B, x.c,
-                                              G, hw, cf.eps, silu))
-      return (int)DI_OK;
+    if (x.has_st) {
+      float* fold = nullptr;
+      if (const uint64_t nf = gn_fold_ws_floats(B, x.c, hw)) {
+        void* fw = nullptr;
+        int r = workspace(c, nf * sizeof(float), &fw);
+        if (r) return r;
+        fold = (float*)fw;
+      }
+      if (launch_group_norm_nhwc_st(c->stream, one(x.buf.h(), x.c), xs, g, b, y, B, x.c, G, hw,
+                                    cf.eps, silu, fold))
+        return (int)DI_OK;
+    }
     void* ws = nullptr;
     int r = workspace(c, gn_nhwc_ws_floats(B, x.c, G, hw) * sizeof(float), &ws);
     if (r) return r;

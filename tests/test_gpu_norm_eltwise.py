@@ -301,3 +301,18 @@ def test_validation_errors(dev):
     assert e.value.code == 5
     st = dev.pool_stats()
     assert st["peak"] >= st["live"] and st["allocs"] >= 1
+
+
+@pytest.mark.parametrize("inner,rows", [(512, 300), (1024, 64), (4096, 257), (640, 33)])
+def test_softmax_f16_rows(dev, rng, inner, rows):
+    """fp16 row softmax: inner a multiple of 512 up to 4096 runs the
+    register-resident kernel (one read, one write), in place as the VAE
+    attention calls it; 640 takes the general kernel."""
+    import drawinstant
+    x = (rng.standard_normal((rows, inner)) * 3).astype(np.float16)
+    b = dev.storage(x)
+    drawinstant.call("di_softmax", dev.ctx, b.handle, b.handle, inner, rows, 1)
+    got = dev.download(b, np.float16, (rows, inner)).astype(np.float32)
+    ref = oracle.softmax(x.astype(np.float32))
+    assert np.abs(got - ref).max() <= 2e-3 * ref.max()
+    assert np.allclose(got.sum(axis=1), 1.0, atol=2e-3)

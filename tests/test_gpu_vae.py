@@ -35,7 +35,9 @@ def test_state_dict_round_trip(small):
         assert np.array_equal(back[k], sd[k]), k
 
 
-@pytest.mark.parametrize("B,h", [(1, 8), (2, 8), (1, 5)])
+# (2, 32): 256x256 images, whose GroupNorm statistics are pre-folded
+# (more than 256 chunks per image), two images per launch
+@pytest.mark.parametrize("B,h", [(1, 8), (2, 8), (1, 5), (2, 32)])
 def test_small_decoder_vs_oracle(small, B, h):
     v, sd, cfg = small
     z = np.random.default_rng(6 + B).standard_normal((B, 4, h, h)).astype(np.float32)
