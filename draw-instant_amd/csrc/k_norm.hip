@@ -20,6 +20,8 @@
 // call), so each issues all of a round's loads (x, partials, gamma/beta)
 // before consuming any: `sched_barrier` stops the scheduler from sinking the
 // loads next to their uses, which would serialise them.
+#include <cstdlib>
+
 #include "di_device.h"
 #include "di_kernels.h"
 
@@ -349,6 +351,7 @@ constexpr int kGnSliceMax = 128;
 // statistics of images with more than kGnFoldMin chunks (above 128 x 128
 // pixels) are pre-folded to about kGnFoldTarget chunks
 constexpr uint32_t kGnFoldMin = 256, kGnFoldTarget = 128;
+constexpr uint32_t kGnApplyWgs = 256;
 
 // Pre-fold of producer statistics for large images: every apply workgroup
 // otherwise re-reads all HW / 64 chunks of its channel slice (2 MB per
@@ -863,8 +866,17 @@ bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st_in, c
     cpi = cpo;
   }
   const uint32_t slices = C / sw, R = 256 / (sw / 8);
-  // about 512 workgroups over the batch, at least one pixel per lane
-  uint32_t pbs = 512 / (N * slices);
+  // about 256 workgroups over the batch, 512 for tensors of 16 MiB and more
+  // (measured: U-Net step and VAE decode; DI_GN_WGS overrides, for tuning
+  // sweeps), at least one pixel per lane
+  static const int wgs_env = [] {
+    const char* e = getenv("DI_GN_WGS");
+    return e ? atoi(e) : 0;
+  }();
+  const uint32_t wgs = wgs_env > 0 ? (uint32_t)wgs_env
+                       : (uint64_t)N * HW * C * 2 >= (16ull << 20) ? 2 * kGnApplyWgs
+                                                                    : kGnApplyWgs;
+  uint32_t pbs = wgs / (N * slices);
   const uint32_t maxpb = (HW + R - 1) / R;
   if (pbs > maxpb) pbs = maxpb;
   if (pbs < 1) pbs = 1;
