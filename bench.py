@@ -485,8 +485,11 @@ def pcie_inclusive(u, inputs, iters=5):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 50 timed steps after 20 warm-up replays: ~0.2 s of GPU time, and the
+    # median-of-batches figure of longer runs to within 1 us (20 / 5 read
+    # 10-25 us high: the clocks and caches are still settling)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-blocks", action="store_true", help="skip the per-block figures")
     ap.add_argument("--roofline-only", action="store_true",
