@@ -23,7 +23,8 @@ HIP events on the library's stream over exactly K graph-replayed steps
   cfg2 conv / cfg3 ResNet / cfg4 transformer / self-attention MFMA %).
 * `denoise_loop`: the 4-step SD-Turbo loop (noise, scaleModelInput, U-Net,
   Euler update) entirely on the device, host wall time including the final
-  wait.
+  wait.  `batch4`: the same step at B=4 (cfg5's other batch), ms per step
+  and per sample.
 * `executor_rewrites` (unless --no-blocks): the op-by-op executor over the
   exported cfg4 attention and LayerNorm + GELU subgraphs, unfused and after
   optimize_graph, wall ms per run.
@@ -87,6 +88,26 @@ def bench_unet(dev, args):
     out = dev.download(bo, np.float32, x.shape)
     finite = bool(np.isfinite(out).all())
     return u, ms, wall, eager, finite, (x, ctx)
+
+
+def bench_unet_batch(dev, u, B=4, iters=20):
+    """The same step at batch B (cfg5's B=4): ms per step and per sample."""
+    rng = np.random.default_rng(4)
+    x = dev.storage(rng.standard_normal((B, 4, 64, 64)).astype(np.float32))
+    c = dev.storage(rng.standard_normal((B, 77, 1024)).astype(np.float32))
+    t = dev.storage(np.full(B, 999.0, np.float32))
+    o = dev.create_buffer(B * 4 * 64 * 64 * 4)
+    try:
+        step = lambda i: u.forward(x, t, c, o, B, 64, 64, 77, graph=True)
+        for i in range(5):
+            step(i)
+        ms = timed(dev, step, iters)
+        out = dev.download(o, np.float32, (B * 4 * 64 * 64,))
+        return {"batch": B, "ms_per_step": round(ms, 4), "ms_per_sample": round(ms / B, 4),
+                "output_finite": bool(np.isfinite(out).all())}
+    finally:
+        for b in (x, c, t, o):
+            b.destroy()
 
 
 def bench_denoise(dev, u, ctx, steps=4, reps=5):
@@ -534,6 +555,7 @@ def main():
         "pcie_inclusive_eager_ms_per_step": round(pcie_inclusive(u, inputs), 3),
         "roofline": roofline_conv(dev),
         "denoise_loop": bench_denoise(dev, u, inputs[1]),
+        "batch4": bench_unet_batch(dev, u, 4),
     }
     line["denoise_loop"]["scheduler_us_per_step"] = round(
         (line["denoise_loop"]["ms_per_step"] - ms) * 1e3, 1)
