@@ -35,8 +35,8 @@ void launch_vae_latent_in(hipStream_t s, const float* z, const float* w, const f
                           uint32_t cpad);
 
 // ---- normalisation (k_norm.hip) ----
-// NCHW group norm (single pass with a cross-workgroup barrier when the group
-// slices fit in registers of co-resident workgroups, else two passes).
+// NCHW group norm: per-slice partial statistics, then fold + apply (two
+// kernels; the partials go to the context workspace).
 int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const float* beta,
                            void* y, uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW,
                            float eps, bool silu, int dt);
