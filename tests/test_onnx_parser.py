@@ -206,3 +206,58 @@ def test_exported_graphs_rewrite_and_evaluate(cases, key, want):
         assert ops.count("Transpose") == 2  # only the NCHW <-> tokens pair remains
         if key == "sdpa":  # the computed sqrt(scale) factors ride along as inputs
             assert all(len(n.inputs) == 5 for n in fa)
+
+
+# ------------------------------------------------ randomised round trips --
+from hypothesis import given, settings, strategies as st  # noqa: E402
+
+_names = st.text(alphabet="abcdefghijklmnopqrstuvwxyz_/.0123456789", min_size=1, max_size=12)
+_ints = st.lists(st.integers(min_value=-(1 << 62), max_value=(1 << 62)), max_size=6)
+_floats = st.lists(st.floats(width=32, allow_nan=False, allow_infinity=False), max_size=5)
+
+
+@st.composite
+def _graphs(draw):
+    nodes = []
+    for _ in range(draw(st.integers(1, 5))):
+        ins = draw(st.lists(_names, max_size=3))
+        outs = draw(st.lists(_names, min_size=1, max_size=2))
+        op = draw(st.sampled_from(["MatMul", "Add", "Reshape", "Transpose", "Softmax", "Conv"]))
+        ints, floats, name_i = draw(_ints), draw(_floats), draw(st.integers(-5, 5))
+        nodes.append((ins, outs, op, ints, floats, name_i))
+    dims = draw(st.lists(st.integers(1, 4), min_size=1, max_size=3))
+    data = np.random.default_rng(draw(st.integers(0, 99))).standard_normal(
+        int(np.prod(dims))).astype(np.float32)
+    packed = draw(st.booleans())
+    return nodes, dims, data, packed
+
+
+@settings(max_examples=60, deadline=None)
+@given(_graphs())
+def test_random_graph_round_trip(case):
+    """Whatever the encoder writes, the parser reads back: node inputs /
+    outputs / op types, int64 attribute lists (negative values as 10-byte
+    varints, packed), float lists, a scalar int attribute and an
+    initializer's dims and bytes."""
+    nodes, dims, data, packed = case
+    gl = []
+    for ins, outs, op, ints, floats, name_i in nodes:
+        attrs = [text(1, "i") + vint(20, 2) + vint(3, name_i)]
+        if ints:
+            body = sum((varint(v) for v in ints), [])
+            attrs.append(text(1, "ints") + (len_delim(8, body) if packed else
+                                            sum((vint(8, v) for v in ints), [])))
+        if floats:
+            attrs.append(text(1, "floats") + len_delim(7, struct.pack(f"<{len(floats)}f", *floats)))
+        gl += len_delim(1, node(ins, outs, op, attrs))
+    gl += len_delim(5, tensor("w", dims, 1, data.tobytes(), packed_dims=packed))
+    parsed = parse_onnx_graph(model(gl))
+    assert len(parsed.nodes) == len(nodes)
+    for n, (ins, outs, op, ints, floats, name_i) in zip(parsed.nodes, nodes):
+        assert n.inputs == ins and n.outputs == outs and n.op_type == op
+        assert get_attr_int(n, "i", None) == name_i
+        assert (get_attr_ints(n, "ints", None) or []) == ints
+        got_f = next((a.floats for a in n.attributes if a.name == "floats"), None) or []
+        assert np.array_equal(np.float32(got_f), np.float32(floats))
+    w = parsed.tensors["w"]
+    assert w.dims == dims and np.array_equal(w.array(), data)
