@@ -566,10 +566,15 @@ def main():
         blk.update(bench_block_chains(dev, u))
         line["blocks"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                               for kk, vv in v.items()} for k, v in blk.items()}
-        line["executor_rewrites"] = bench_executor_rewrites(dev)
-        line["executor_onnx_cfg4"] = bench_executor_onnx(dev)
-        line["vae_decode_512"] = bench_vae(dev)
-        line["executor_vae_decode_512"] = bench_executor_vae(dev)
+        # secondary legs: a failure is reported in the line, never lost with it
+        for key, fn in (("executor_rewrites", bench_executor_rewrites),
+                        ("executor_onnx_cfg4", bench_executor_onnx), ("vae_decode_512", bench_vae),
+                        ("executor_vae_decode_512", bench_executor_vae)):
+            try:
+                line[key] = fn(dev)
+            except Exception as e:  # noqa: BLE001 - recorded, the headline still prints
+                line[key] = {"error": f"{type(e).__name__}: {e}"}
+                print(f"bench.py: {key} failed: {e}", file=sys.stderr, flush=True)
     print(json.dumps(line), flush=True)
 
 
