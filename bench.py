@@ -397,16 +397,16 @@ def bench_executor_vae(dev, reps=3):
     z = dev.storage(feeds["latent"] / 0.18215)  # vae-wgsl.js scaling
     seeds = {"latent": Tensor(z, [1, 4, 64, 64])}
     row = {"exported_nodes": len(graph.nodes), "weights_mb": round(graph.bytes / 2 ** 20, 1)}
-    for key in ("unfused", "fused", "fused_f16_resident"):
+    for key in ("unfused", "fused", "fused_f16_resident", "fused_conv_f16"):
         g = copy.deepcopy(graph)
         if key != "unfused":
             row.setdefault("rewrites", {k: v for k, v in optimize_graph(g).items() if v})
-        if "f16" in key:
+        if "f16_resident" in key:
             for t in g.tensors.values():
                 if t.dtype == "float32":
                     t.data, t.dtype = t.array().astype(np.float16).tobytes(), "float16"
-        wc = WeightCache(dev, g.tensors, keep_f16="f16" in key)
-        ex = Executor(dev, g, wc)
+        wc = WeightCache(dev, g.tensors, keep_f16="f16_resident" in key)
+        ex = Executor(dev, g, wc, conv_f16=key == "fused_conv_f16")
         ts = []
         for r in range(reps + 1):
             t0 = time.perf_counter()

@@ -938,7 +938,8 @@ def _conv(ctx, node, inputs):
     Ho, Wo = (H + 2 * P - K) // S + 1, (W + 2 * P - K) // S + 1
     out = ctx.pool.acquire(N * Cout * Ho * Wo * 4)
     ctx.dispatchers.conv_mm(x.buf, w.buf, bias.buf if bias is not None else None, out, N, Cin,
-                            Cout, H, W, K, S, P, 0, F32W16 if w.dtype == "float16" else F32)
+                            Cout, H, W, K, S, P, CONV_F16_COMPUTE if ctx.conv_f16 else 0,
+                            F32W16 if w.dtype == "float16" else F32)
     return Tensor(out, [N, Cout, Ho, Wo])
 
 
@@ -1724,6 +1725,7 @@ METADATA_OPS = {"Reshape", "Shape", "Unsqueeze", "Squeeze", "Gather", "Slice", "
 # fp16-resident weights: (op, input index) pairs that read them as they are;
 # relabelling ops pass the dtype on; every other consumer gets an fp32 copy
 F16_WEIGHT_INPUTS = {("MatMul", 1), ("Gemm", 1), ("Conv", 1)}
+CONV_F16_COMPUTE = 1  # DI_CONV_F16_COMPUTE
 F16_PASSTHROUGH = {"Reshape", "Unsqueeze", "Squeeze", "Identity", "Expand", "Shape"}
 BINARY_SHAPE_AWARE = {"Add", "Sub", "Mul", "Div"}
 
@@ -1733,22 +1735,29 @@ class ExecutorError(RuntimeError):
 
 
 class _Ctx:
-    def __init__(self, device, pool, dispatchers, weights, promote):
+    def __init__(self, device, pool, dispatchers, weights, promote, conv_f16=False):
         self.device = device
         self.pool = pool
         self.dispatchers = dispatchers
         self.weights = weights
         self.promote = promote
+        self.conv_f16 = conv_f16
 
 
 class Executor:
     """Walks a topologically sorted graph, one C-ABI dispatch per GPU node
     (wgsl-executor.js:1223-1466)."""
 
-    def __init__(self, device: Device, graph: Graph, weight_cache: WeightCache):
+    def __init__(self, device: Device, graph: Graph, weight_cache: WeightCache,
+                 conv_f16: bool = False):
+        """``conv_f16`` (opt-in): Conv nodes run on the fp16 MFMA path
+        (DI_CONV_F16_COMPUTE: fp32 tensors staged to fp16 operands, fp32
+        accumulation and output) instead of the exact fp32 MFMA path the
+        reference's fp32 semantics call for."""
         self.device = device
         self.graph = graph
         self.weights = weight_cache
+        self.conv_f16 = conv_f16
         self.pool = BufferPool(device)
         self.dispatchers = create_dispatchers(device)
         if not graph.inputs or not graph.outputs:
@@ -1804,7 +1813,8 @@ class Executor:
                     env[name] = Tensor(self.device.storage(f), list(f.shape))
             else:
                 raise ExecutorError(f'unsupported input seed for "{name}": {type(val).__name__}')
-        ctx = _Ctx(self.device, self.pool, self.dispatchers, self.weights, self._promote)
+        ctx = _Ctx(self.device, self.pool, self.dispatchers, self.weights, self._promote,
+                   self.conv_f16)
         LOG["t0"] = time.perf_counter()
         LOG["node_count"] = len(self.graph.nodes)
         LOG["op_hist"] = {}

@@ -104,3 +104,29 @@ def test_fp16_resident_weights(dev, cases, key, fused):
     assert np.array_equal(outs[0], outs[1])
     assert nbytes[1] < 0.56 * nbytes[0]
     assert rel_l2(outs[1], y) <= 5e-3  # fp16-rounded weights
+
+
+@pytest.mark.parametrize("key", ["resnet", "vae"])
+@pytest.mark.parametrize("f16_weights", [False, True])
+def test_conv_f16_compute_option(dev, cases, key, f16_weights):
+    """Executor(conv_f16=True): Conv nodes on the fp16 MFMA path (operands
+    rounded to fp16, fp32 accumulation), with fp32 or fp16-resident weights:
+    rel-L2 <= 5e-3 against the modules' float64 output."""
+    data, feeds, y = cases[key]
+    g = parse_onnx_graph(data)
+    optimize_graph(g)
+    if f16_weights:
+        g = as_fp16_file(g)
+    wc = WeightCache(dev, g.tensors, keep_f16=f16_weights)
+    ex = Executor(dev, g, wc, conv_f16=True)
+    try:
+        outs = ex.run(feeds)
+        t = outs["sample" if "sample" in outs else "y"]
+        got = dev.download(t.buf, np.float32, tuple(t.dims))
+        t.buf.destroy()
+    finally:
+        ex.destroy()
+        wc.destroy()
+    e = rel_l2(got, y)
+    print(f"[onnx-conv16] {key} f16_weights={f16_weights} rel_l2={e:.2e}", flush=True)
+    assert e <= 5e-3
