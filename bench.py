@@ -429,6 +429,24 @@ def bench_executor_vae(dev, reps=3):
 ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_gemm_conv3x3_64x64x320_pmc.md")
 
 
+def sclk_levels():
+    """(max, current) shader clock in MHz from the first card's pp_dpm_sclk
+    table (the current level carries a '*'), or (None, None) where sysfs does
+    not expose it."""
+    import glob
+    import re
+    for f in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+        try:
+            lines = open(f).read().splitlines()
+        except OSError:
+            continue
+        lv = [(int(m.group(1)), "*" in ln) for ln in lines
+              for m in [re.search(r"(\d+)\s*[Mm][Hh]z", ln)] if m]
+        if lv:
+            return max(v for v, _ in lv), next((v for v, cur in lv if cur), None)
+    return None, None
+
+
 def roofline_conv(dev, iters=50):
     """Live roofline of the dominant kernel at its U-Net shape."""
     from drawinstant import perf
@@ -443,6 +461,11 @@ def roofline_conv(dev, iters=50):
     for i in range(3):
         conv(i)
     ms = timed(dev, conv, iters)
+    # shader clock sampled while ~10 ms of the same launches run
+    for i in range(400):
+        conv(i)
+    sclk_max, sclk_cur = sclk_levels()
+    dev.sync()
     fl = perf.conv_flops(1, 320, 320, 64, 64, 3)
     achieved = fl / (ms * 1e-3) / 1e12
     peak = perf.PEAK_FP16_FLOPS / 1e12
@@ -456,7 +479,12 @@ def roofline_conv(dev, iters=50):
     return {"kernel": "k_gemm implicit-GEMM conv3x3 320->320 @64x64 NHWC fp16 (fp32 acc)",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": traffic,
-            "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3)}
+            "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3),
+            # the published peak assumes 2.4 GHz; the same peak at the clock
+            # sampled under load, where sysfs exposes it
+            "sclk_mhz": {"max": sclk_max, "under_load": sclk_cur},
+            "frac_at_sclk": (round(achieved / (peak * sclk_cur / 2400.0), 4)
+                             if sclk_cur else None)}
 
 
 def cpu_baseline(u, budget_blocks=None):
