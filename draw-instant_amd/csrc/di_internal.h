@@ -47,6 +47,12 @@ struct Ctx {
   // kernel workspace (partials); grown on demand, never during graph capture
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
+  // Workspaces whose address a captured graph has baked into its kernels:
+  // pointer -> number of live graphs.  A pinned workspace that growth
+  // replaces is parked in `ws_retired` and freed when its last graph is
+  // dropped, so a replay never touches freed memory.
+  std::map<void*, int> ws_refs;
+  std::vector<void*> ws_retired;
   // While set (graph capture), pool_release parks buffers in `held` instead
   // of the free list; the capturing owner takes them over.
   bool hold_releases = false;
@@ -106,8 +112,13 @@ int lookup(Ctx* c, di_handle h, Buffer** out);
     }                                                                            \
   } while (0)
 
-// Workspace of at least `bytes` (grown with hipMalloc on demand).
+// Workspace of at least `bytes` (grown with hipMalloc on demand; refused
+// during graph capture, which the owner's warm-up run makes unnecessary).
 int workspace(Ctx* c, uint64_t bytes, void** out);
+// A captured graph takes a reference on the current workspace (returned, may
+// be null) and gives it back when the graph is destroyed.
+void* workspace_pin(Ctx* c);
+void workspace_unpin(Ctx* c, void* ws);
 
 // Pooled device allocation used by the C ABI and by block compositions.
 int pool_alloc(Ctx* c, uint64_t bytes, void** out, uint64_t* cap);

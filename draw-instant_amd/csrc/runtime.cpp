@@ -101,15 +101,44 @@ int workspace(Ctx* c, uint64_t bytes, void** out) {
     *out = c->ws;
     return DI_OK;
   }
+  DI_REQUIRE(!c->hold_releases, DI_EINVAL,
+             "workspace growth to %llu bytes during graph capture",
+             (unsigned long long)bytes);
   uint64_t want = bytes < (1ull << 20) ? (1ull << 20) : bytes;
   DI_HIP(hipStreamSynchronize(c->stream));
-  if (c->ws) DI_HIP(hipFree(c->ws));
+  if (c->ws) {
+    // A captured graph still writes the old workspace on every replay: keep
+    // it until the last such graph is dropped.
+    if (c->ws_refs.count(c->ws)) c->ws_retired.push_back(c->ws);
+    else DI_HIP(hipFree(c->ws));
+  }
   c->ws = nullptr;
   c->ws_bytes = 0;
   DI_HIP(hipMalloc(&c->ws, want));
   c->ws_bytes = want;
   *out = c->ws;
   return DI_OK;
+}
+
+void* workspace_pin(Ctx* c) {
+  if (c->ws) c->ws_refs[c->ws]++;
+  return c->ws;
+}
+
+void workspace_unpin(Ctx* c, void* ws) {
+  if (!ws) return;
+  auto it = c->ws_refs.find(ws);
+  if (it == c->ws_refs.end()) return;
+  if (--it->second > 0) return;
+  c->ws_refs.erase(it);
+  for (size_t i = 0; i < c->ws_retired.size(); i++) {
+    if (c->ws_retired[i] == ws) {
+      // callers drop graphs only after the stream has drained
+      (void)hipFree(ws);
+      c->ws_retired.erase(c->ws_retired.begin() + i);
+      break;
+    }
+  }
 }
 
 }  // namespace di
@@ -150,6 +179,7 @@ int32_t di_destroy(di_ctx* ctx) {
   for (auto& kv : ctx->free_list)
     for (void* p : kv.second) (void)hipFree(p);
   if (ctx->ws) (void)hipFree(ctx->ws);
+  for (void* p : ctx->ws_retired) (void)hipFree(p);
   for (int i = 0; i < kTimerSlots; i++) {
     if (ctx->ev_begin[i]) (void)hipEventDestroy(ctx->ev_begin[i]);
     if (ctx->ev_end[i]) (void)hipEventDestroy(ctx->ev_end[i]);
@@ -196,6 +226,14 @@ int32_t di_free(di_ctx* ctx, di_handle h) {
   if (rc) return rc;
   pool_release(ctx, b->ptr, b->cap);
   ctx->bufs.erase(h);
+  return DI_OK;
+}
+
+int32_t di_workspace_stats(di_ctx* ctx, uint64_t* bytes, uint32_t* pinned, uint32_t* retired) {
+  DI_CTX(ctx);
+  if (bytes) *bytes = ctx->ws_bytes;
+  if (pinned) *pinned = (uint32_t)ctx->ws_refs.size();
+  if (retired) *retired = (uint32_t)ctx->ws_retired.size();
   return DI_OK;
 }
 

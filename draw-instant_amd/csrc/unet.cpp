@@ -86,6 +86,8 @@ struct UNet {
   uint64_t arena_cap[AR_COUNT] = {};
   // scratch buffers baked into the captured graph (owned until it is dropped)
   std::vector<std::pair<void*, uint64_t>> graph_scratch;
+  // the context workspace the captured graph's kernels address (pinned)
+  void* graph_ws = nullptr;
   int conv_in_w, conv_in_b, t1w, t1b, t2w, t2b, nog, nob, cow, cob;
   std::vector<Level> down, up;
   ResIdx mid_res[2];
@@ -644,6 +646,8 @@ static void drop_graph(di_ctx* ctx, di_unet* u) {
   u->graph = nullptr;
   for (auto& pc : u->graph_scratch) pool_release(ctx, pc.first, pc.second);
   u->graph_scratch.clear();
+  workspace_unpin(ctx, u->graph_ws);
+  u->graph_ws = nullptr;
 }
 
 extern "C" {
@@ -823,6 +827,7 @@ int32_t di_unet_forward(di_ctx* ctx, di_unet* u, di_handle sample, di_handle tim
     }
     DI_REQUIRE(e == hipSuccess, DI_EHIP, "graph capture failed: %s", hipGetErrorString(e));
     u->graph = g;
+    u->graph_ws = workspace_pin(ctx);
     DI_HIP(hipGraphInstantiate(&u->graph_exec, g, nullptr, nullptr, 0));
     memcpy(u->graph_key, key, sizeof(key));
   }

@@ -67,6 +67,8 @@ struct Vae {
   std::vector<std::vector<VRes>> up;
   std::vector<int> up_w, up_b;  // upsampler convs (-1 on the last level)
   std::vector<std::pair<void*, uint64_t>> graph_scratch;
+  // the context workspace the captured graph's kernels address (pinned)
+  void* graph_ws = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   uint64_t graph_key[6] = {0};
@@ -428,6 +430,8 @@ static void vae_drop_graph(di_ctx* ctx, di_vae* v) {
   v->graph = nullptr;
   for (auto& pc : v->graph_scratch) pool_release(ctx, pc.first, pc.second);
   v->graph_scratch.clear();
+  workspace_unpin(ctx, v->graph_ws);
+  v->graph_ws = nullptr;
 }
 
 extern "C" {
@@ -588,6 +592,7 @@ int32_t di_vae_decode(di_ctx* ctx, di_vae* v, di_handle latent, di_handle image,
     }
     DI_REQUIRE(e == hipSuccess, DI_EHIP, "graph capture failed: %s", hipGetErrorString(e));
     v->graph = g;
+    v->graph_ws = workspace_pin(ctx);
     DI_HIP(hipGraphInstantiate(&v->graph_exec, g, nullptr, nullptr, 0));
     memcpy(v->graph_key, key, sizeof(key));
   }

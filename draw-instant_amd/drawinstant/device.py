@@ -142,6 +142,12 @@ class Device:
         call("di_pool_stats", self.ctx, *[ctypes.byref(x) for x in v])
         return dict(zip(("live", "peak", "allocs", "reserved"), (x.value for x in v)))
 
+    def workspace_stats(self) -> dict:
+        b, pinned, retired = ctypes.c_uint64(), ctypes.c_uint32(), ctypes.c_uint32()
+        call("di_workspace_stats", self.ctx, ctypes.byref(b), ctypes.byref(pinned),
+             ctypes.byref(retired))
+        return {"bytes": b.value, "pinned": pinned.value, "retired": retired.value}
+
     def fill_normal(self, buf: Buffer, n: int, seed: int, mean: float = 0.0, std: float = 1.0,
                     dtype=F32):
         call("di_fill_normal", self.ctx, buf.handle, dtype_code(dtype), n, seed, mean, std)

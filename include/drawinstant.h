@@ -118,6 +118,13 @@ int32_t di_buffer_size(di_ctx* ctx, di_handle h, uint64_t* bytes);
 /* BufferPool live/peak/allocs counters (wgsl-executor.js:67-69). */
 int32_t di_pool_stats(di_ctx* ctx, uint64_t* live, uint64_t* peak,
                       uint64_t* allocs, uint64_t* reserved_bytes);
+/* Kernel workspace of the context (split-K partials, GroupNorm partial sums):
+ * current size, how many workspace allocations captured graphs still hold,
+ * and how many of those growth has already replaced (kept alive until their
+ * graph is dropped).  No reference counterpart: WebGPU has no captured
+ * command graphs; this makes the graph/workspace lifetime observable. */
+int32_t di_workspace_stats(di_ctx* ctx, uint64_t* bytes, uint32_t* pinned,
+                           uint32_t* retired);
 /* createStorage / queue.writeBuffer (wgsl-ops.js:1172-1180). */
 int32_t di_upload(di_ctx* ctx, di_handle h, uint64_t offset, const void* src,
                   uint64_t bytes);

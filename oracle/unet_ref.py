@@ -18,6 +18,13 @@ ResNets, 1e-6 in transformers, LN eps 1e-5, attention scale 1/sqrt(64),
 timestep sinusoid [cos || sin] (fused-tembed.js:36-42), GEGLU
 h * GELU(gate) on a last-dim chunk.  Parameters are diffusers-named,
 diffusers-layout float32 arrays (``drawinstant.unet.UNet.state_dict``).
+
+Pinned (tests/test_unet_composition.py) against an independent module-form
+UNet2DConditionModel with diffusers' module tree and names
+(tests/golden/unet_module.py) in float64 on the same weights: rel-L2 < 1e-5
+for the whole step on both backends' configs, < 1e-6 per ResNet and
+transformer block; planted wiring mistakes (skip concat order, an unflipped
+[sin || cos] sinusoid, moved cross-attention levels) fail that comparison.
 """
 from __future__ import annotations
 

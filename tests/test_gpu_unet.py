@@ -147,6 +147,63 @@ def test_sd21_graph_replay_matches_eager(dev, sd21, rng):
         b.destroy()
 
 
+def test_graph_replay_survives_workspace_growth(rng):
+    """A captured U-Net graph keeps addressing the workspace it was captured
+    with: growing the context workspace afterwards (a large split-K linear)
+    retires the old allocation instead of freeing it, the replay stays
+    bit-identical to eager, and dropping the graph frees the retired block."""
+    import drawinstant
+    from drawinstant.unet import UNet, UNetConfig
+    d = drawinstant.Device(0)  # fresh context: its workspace starts empty
+    try:
+        cfg = UNetConfig.small()
+        u = UNet(d, cfg, seed=11)
+        x, ctx = _inputs(rng, 1, 16, 16, 77, cfg.cross_dim)
+        bs, bt, bc = d.storage(x), d.storage(np.array([999.0], np.float32)), d.storage(ctx)
+        bo = d.create_buffer(x.nbytes)
+        u.forward(bs, bt, bc, bo)
+        eager = d.download(bo, np.float32, x.shape)
+        u.forward(bs, bt, bc, bo, graph=True)
+        d.sync()
+        np.testing.assert_array_equal(d.download(bo, np.float32, x.shape), eager)
+        ws0 = d.workspace_stats()
+        print(f"[ws] after capture {ws0}", flush=True)
+        assert ws0["pinned"] == 1 and ws0["retired"] == 0 and ws0["bytes"] > 0
+        # M = 64 rows against a long K: the planner splits K, and the fp32
+        # partials (splits x 64 x N x 4 bytes) outgrow the captured workspace
+        M, N = 64, 2560
+        grown = None
+        for K in (8192, 32768):
+            xa = d.create_buffer(M * K * 2)
+            wa = d.create_buffer(N * K * 2)
+            ya = d.create_buffer(M * N * 2)
+            d.fill_normal(xa, M * K, 3, dtype=drawinstant.F16)
+            d.fill_normal(wa, N * K, 4, std=0.01, dtype=drawinstant.F16)
+            drawinstant.call("di_linear", d.ctx, xa.handle, wa.handle, 0, 0, ya.handle, M, N, K, 0,
+                             drawinstant.F16)
+            d.sync()
+            for b in (xa, wa, ya):
+                b.destroy()
+            grown = d.workspace_stats()
+            print(f"[ws] after linear K={K}: {grown}", flush=True)
+            if grown["bytes"] > ws0["bytes"]:
+                break
+        assert grown["bytes"] > ws0["bytes"], "the split-K linear did not grow the workspace"
+        assert grown["retired"] == 1 and grown["pinned"] == 1
+        for _ in range(2):
+            d.fill_normal(bo, x.size, 9)
+            u.forward(bs, bt, bc, bo, graph=True)
+            d.sync()
+            np.testing.assert_array_equal(d.download(bo, np.float32, x.shape), eager)
+        u.destroy()
+        after = d.workspace_stats()
+        assert after["retired"] == 0 and after["pinned"] == 0
+        for b in (bs, bt, bc, bo):
+            b.destroy()
+    finally:
+        d.destroy()
+
+
 def test_state_dict_round_trip(dev):
     from drawinstant.unet import UNet, UNetConfig
     cfg = UNetConfig.small()
