@@ -173,6 +173,8 @@ class BufferPool:
         self.live = 0
         self.peak = 0
         self.allocs = 0
+        self.live_bytes = 0  # bucket bytes handed out and not yet released
+        self.peak_bytes = 0
 
     @staticmethod
     def key(nbytes: int) -> int:
@@ -183,6 +185,8 @@ class BufferPool:
         lst = self.free.get(k)
         self.live += 1
         self.peak = max(self.peak, self.live)
+        self.live_bytes += k
+        self.peak_bytes = max(self.peak_bytes, self.live_bytes)
         if lst:
             return lst.pop()
         self.allocs += 1
@@ -197,6 +201,7 @@ class BufferPool:
             return
         self.free.setdefault(buf.size, []).append(buf)
         self.live -= 1
+        self.live_bytes -= buf.size
 
     def owns(self, buf: Buffer) -> bool:
         return buf in self.owned
@@ -526,7 +531,7 @@ def _constant(ctx, node, inputs):
         arr = t.array()
         if t.dtype in ("int64", "int32"):
             return CpuTensor(arr, t.dims, t.dtype, True)
-        if t.dtype in ("float32", "float16"):
+        if t.dtype in ("float32", "float16", "float64"):  # every float lives as fp32
             f = arr.astype(np.float32)
             buf = ctx.pool.acquire(max(f.nbytes, 4))
             ctx.device.upload(buf, f)
@@ -1212,7 +1217,7 @@ def fuse_mul_add_pattern(graph: Graph, tensor_shapes: Optional[dict] = None) -> 
 
 
 def _uniform_value(t: TensorProto):
-    if t.dtype not in ("float32", "float16") or t.data is None:
+    if t.dtype not in ("float32", "float16", "float64") or t.data is None:
         return None
     f = t.array().astype(np.float32)
     if f.size == 0:
@@ -1299,7 +1304,18 @@ def _const_value(graph: Graph, producer: dict, name: str) -> Optional[float]:
             return None
     if len(init.dims) > 1 or int(np.prod(init.dims or [1])) != 1:
         return None
-    return _uniform_value(init)
+    v = _uniform_value(init)
+    return None if v is None else _Const(v, init.dtype)
+
+
+class _Const(float):
+    """A scalar constant that remembers its storage type: an fp16 graph
+    stores sqrt(2) as 1.4140625, which must still read as sqrt(2)."""
+
+    def __new__(cls, v, dtype):
+        o = super().__new__(cls, v)
+        o.dtype = dtype
+        return o
 
 
 def _scalar_operand(graph: Graph, producer: dict, node: Node):
@@ -1318,8 +1334,18 @@ def _scalar_operand(graph: Graph, producer: dict, node: Node):
     return None
 
 
-def _near(v: Optional[float], want: float, tol: float = 1e-6) -> bool:
-    return v is not None and abs(v - want) <= tol * max(1.0, abs(want))
+# relative half-ulp of the storage types a constant may come in
+_CONST_TOL = {"float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}
+
+
+def _near(v: Optional[float], want: float, tol: Optional[float] = None) -> bool:
+    """v equals ``want`` up to ``tol`` (relative), by default up to the
+    rounding of v's storage type (1e-6 for fp32 / fp64 constants)."""
+    if v is None:
+        return False
+    if tol is None:
+        tol = _CONST_TOL.get(getattr(v, "dtype", None), 1e-6)
+    return abs(v - want) <= tol * max(1.0, abs(want))
 
 
 def fuse_gelu_pattern(graph: Graph) -> dict:
@@ -1386,6 +1412,10 @@ def fuse_gelu_pattern(graph: Graph) -> dict:
     return {"fused": fused}
 
 
+# ONNX TensorProto types FLOAT, FLOAT16, DOUBLE, BFLOAT16
+_FLOAT_TYPES = (1, 10, 11, 16)
+
+
 def _last_axis_attr(node: Node) -> Optional[int]:
     axes = get_attr_ints(node, "axes", None)
     if axes is None or len(axes) != 1 or get_attr_int(node, "keepdims", 1) != 1:
@@ -1417,11 +1447,23 @@ def fuse_layer_norm_pattern(graph: Graph) -> dict:
         return t is not None and t.data is not None and len(t.dims) >= 1 and \
             all(d == 1 for d in t.dims[:-1])
 
+    def float_cast(name, uses=1):
+        """Index of the float->float Cast that produces ``name`` (the fp16
+        export widens X - mean before the variance and narrows the result)."""
+        if consumers.get(name, 0) != uses:
+            return None
+        pi = producer.get(name)
+        if pi is None or nodes[pi].op_type != "Cast" or \
+                get_attr_int(nodes[pi], "to", 0) not in _FLOAT_TYPES:
+            return None
+        return pi
+
     drop, fused = set(), 0
     for i, dv in enumerate(nodes):
         if dv.op_type != "Div" or i in drop or len(dv.inputs) < 2:
             continue
         xc, sd = dv.inputs[:2]
+        casts = []
         si = prod(sd, "Sqrt")
         if si is None:
             continue
@@ -1440,7 +1482,12 @@ def fuse_layer_norm_pattern(graph: Graph) -> dict:
             continue
         if not _near(_const_value(graph, producer, nodes[pw].inputs[1]), 2.0, 0.0):
             continue
-        sb = prod(xc, "Sub", uses=2)
+        ci = float_cast(xc, uses=2)
+        if ci is not None:
+            casts.append(ci)
+            sb = prod(nodes[ci].inputs[0], "Sub")
+        else:
+            sb = prod(xc, "Sub", uses=2)
         if sb is None:
             continue
         x, mu = nodes[sb].inputs[:2]
@@ -1452,6 +1499,12 @@ def fuse_layer_norm_pattern(graph: Graph) -> dict:
             continue
         # optional affine tail
         xn = dv.outputs[0]
+        if consumers.get(xn, 0) == 1:
+            ci = next((k for k, n in enumerate(nodes) if xn in n.inputs), None)
+            if ci is not None and nodes[ci].op_type == "Cast" and \
+                    get_attr_int(nodes[ci], "to", 0) in _FLOAT_TYPES:
+                casts.append(ci)
+                xn = nodes[ci].outputs[0]
         tail, gamma, beta, out = [], None, None, xn
         if consumers.get(xn, 0) == 1:
             ci = next((k for k, n in enumerate(nodes) if xn in n.inputs), None)
@@ -1472,9 +1525,10 @@ def fuse_layer_norm_pattern(graph: Graph) -> dict:
         ins = [x, gamma or "", beta or ""]
         fused_node = Node("LayerNormalization", (dv.name or "") + "_ln", ins, [out],
                           [Attr("axis", i=ax1), Attr("epsilon", f=float(eps))])
-        keep = tail[-1] if tail else i
+        keep = tail[-1] if tail else (casts[-1] if len(casts) and
+                                          nodes[casts[-1]].outputs[0] == out else i)
         nodes[keep] = fused_node
-        drop.update(k for k in (r1, sb, pw, r2, ai, si, i, *tail) if k != keep)
+        drop.update(k for k in (r1, sb, pw, r2, ai, si, i, *casts, *tail) if k != keep)
         fused += 1
     if fused:
         graph.nodes = [n for k, n in enumerate(nodes) if k not in drop]
@@ -1809,8 +1863,12 @@ class Executor:
                 if val.dtype.kind in "iu":
                     env[name] = CpuTensor(val.reshape(-1), list(val.shape), _dtype_of(val), True)
                 else:
+                    # a pool buffer, returned with the run's other temporaries
                     f = np.ascontiguousarray(val, np.float32)
-                    env[name] = Tensor(self.device.storage(f), list(f.shape))
+                    buf = self.pool.acquire(max(f.nbytes, 4))
+                    self.device.upload(buf, f)
+                    self._temps.append(buf)
+                    env[name] = Tensor(buf, list(f.shape))
             else:
                 raise ExecutorError(f'unsupported input seed for "{name}": {type(val).__name__}')
         ctx = _Ctx(self.device, self.pool, self.dispatchers, self.weights, self._promote,
@@ -1820,7 +1878,27 @@ class Executor:
         LOG["op_hist"] = {}
         if LOG["profile"]:
             LOG["profile_data"] = []
-        deferred: List[Buffer] = []
+        # Live env names per device buffer (a Reshape / Cast / Expand output
+        # aliases its input's buffer): a pool buffer goes back to the free
+        # list as soon as no live name refers to it, i.e. right after the
+        # last consumer of its last alias is enqueued.  Every kernel and copy
+        # runs in order on the one library stream, so a later kernel that
+        # receives the recycled buffer runs after every earlier reader.
+        refs: Dict[int, int] = {}
+        for t in env.values():
+            b = getattr(t, "buf", None)
+            if b is not None:
+                refs[id(b)] = refs.get(id(b), 0) + 1
+        protected = set(self.graph_input_names) | {o["name"] for o in self.graph.outputs}
+
+        def drop(name):
+            t = env.pop(name)
+            b = getattr(t, "buf", None)
+            if b is None:
+                return
+            refs[id(b)] -= 1
+            if refs[id(b)] == 0 and self.pool.owns(b) and b not in self._temps:
+                self.pool.release(b)
         for ni, node in enumerate(self.graph.nodes):
             op = OPS.get(node.op_type)
             if op is None:
@@ -1878,23 +1956,25 @@ class Executor:
                     td["out"] += out.byte_length
                     nb += out.byte_length
                 td["by_op"][node.op_type] = td["by_op"].get(node.op_type, 0) + nb
-            env[node.outputs[0]] = out
+            oname = node.outputs[0]
+            if oname in env:  # a name produced twice: the old value is dead
+                drop(oname)
+            env[oname] = out
+            if getattr(out, "buf", None) is not None:
+                refs[id(out.buf)] = refs.get(id(out.buf), 0) + 1
             if LOG["profile"] and getattr(out, "buf", None) is not None:
                 self.device.sync()
                 LOG["profile_data"].append({"ni": ni, "op": node.op_type, "name": node.name,
                                             "dims": out.dims,
                                             "ms": (time.perf_counter() - t_prof) * 1e3})
-            out_buf = getattr(out, "buf", None)
             for name in node.inputs:
                 if not name or name not in env:
                     continue
-                t = env[name]
                 consumers[name] = consumers.get(name, 0) - 1
-                if consumers[name] <= 0 and getattr(t, "buf", None) is not None and \
-                        t.buf is not out_buf and not self.weights.has(name) and \
-                        name not in self.graph_input_names:
-                    deferred.append(t.buf)
-                    del env[name]
+                if consumers[name] <= 0 and name not in protected:
+                    drop(name)
+            if consumers.get(oname, 0) <= 0 and oname not in protected:
+                drop(oname)  # produced but never read
         # snapshot graph outputs into fresh buffers owned by the caller
         snaps: Dict[str, Tensor] = {}
         for o in self.graph.outputs:
@@ -1910,7 +1990,7 @@ class Executor:
         # outputs' own buffers (the caller holds the snapshots).  The reference
         # keeps the last two live forever, so its pool grows on every run.
         released = set()
-        for buf in deferred + self._temps:
+        for buf in self._temps:
             if id(buf) in released:
                 continue
             released.add(id(buf))
@@ -1924,7 +2004,8 @@ class Executor:
             self.pool.release(b)
         self._temps = []
         _dlog(f"run: done in {(time.perf_counter() - LOG['t0']) * 1e3:.1f} ms "
-              f"pool.allocs={self.pool.allocs} peak={self.pool.peak}")
+              f"pool.allocs={self.pool.allocs} peak={self.pool.peak} "
+              f"peak_bytes={self.pool.peak_bytes}")
         return {o["name"]: snaps.get(o["name"], env.get(o["name"])) for o in self.graph.outputs}
 
     def destroy(self) -> None:

@@ -402,3 +402,32 @@ def load(module: nn.Module, sd: dict, dtype=torch.float64) -> nn.Module:
     """Strict load of a {diffusers name: array} dict (every name must match)."""
     module.load_state_dict({k: torch.as_tensor(v) for k, v in sd.items()}, strict=True)
     return module.to(dtype).eval()
+
+
+def export_case(cfg: dict, sd: dict, H: int, W: int, S: int = 77, seed: int = 0,
+                device: str = "cpu"):
+    """The SD-Turbo-form ONNX graph of this module for a config and weights:
+    (onnx bytes, feeds, fp16-rounded state dict).
+
+    The graph has the I/O of the SD-Turbo U-Net file (unet.js:13-19): fp32
+    ``sample`` [1,4,H,W], int64 ``timestep`` [1], fp32
+    ``encoder_hidden_states`` [1,S,cross_dim], fp16 initializers inside,
+    fp32 ``out_sample``; exported by torch's TorchScript exporter at opset
+    14.  The weights are rounded to fp16 first, so the returned state dict
+    is exactly what the file holds.  ``device`` is where the export trace
+    runs (a full-size fp16 trace is quick on the GPU)."""
+    from golden import onnx_export
+    import numpy as np
+    sd16 = {k: np.asarray(v, np.float32).astype(np.float16).astype(np.float32)
+            for k, v in sd.items()}
+    m = HalfIO(load(from_config(cfg), sd16, dtype=torch.float32)).to(device)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(1, cfg["in_channels"], H, W, generator=g)
+    ctx = torch.randn(1, S, cfg["cross_dim"], generator=g)
+    t = torch.tensor([999], dtype=torch.int64)
+    data = onnx_export.export(m, (x.to(device), t.to(device), ctx.to(device)),
+                              ("sample", "timestep", "encoder_hidden_states"),
+                              output_name="out_sample")
+    del m
+    feeds = {"sample": x.numpy(), "timestep": t.numpy(), "encoder_hidden_states": ctx.numpy()}
+    return data, feeds, sd16

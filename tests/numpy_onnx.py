@@ -128,12 +128,31 @@ def _constant(n, i):
     return t.array().reshape(t.dims) if t.dims else t.array().reshape(())
 
 
+def _constant_of_shape(n, i):
+    v = next((a for a in n.attributes if a.name == "value"), None)
+    fill = v.t.array().reshape(-1)[:1] if v is not None and v.t is not None else \
+        np.zeros(1, np.float32)
+    return np.full([int(d) for d in i[0]], fill[0], fill.dtype)
+
+
+def _expand(n, i):
+    """Numpy-style broadcast of x against the shape operand (ONNX Expand)."""
+    shape = [int(d) for d in i[1]]
+    full = np.broadcast_shapes(i[0].shape, tuple(shape))
+    return np.ascontiguousarray(np.broadcast_to(i[0], full))
+
+
 OPS = {
     "Add": _bin(np.add), "Sub": _bin(np.subtract), "Mul": _bin(np.multiply),
     "Div": lambda n, i: (i[0] / i[1]) if i[0].dtype.kind == "f" else
     np.trunc(i[0] / i[1]).astype(i[0].dtype),
     "Pow": _bin(np.power),
     "Sqrt": lambda n, i: np.sqrt(i[0]),
+    "Sin": lambda n, i: np.sin(i[0].astype(np.float64)).astype(i[0].dtype),
+    "Cos": lambda n, i: np.cos(i[0].astype(np.float64)).astype(i[0].dtype),
+    "Equal": lambda n, i: np.equal(i[0], i[1]),
+    "Where": lambda n, i: np.where(i[0], i[1], i[2]),
+    "Expand": _expand, "ConstantOfShape": _constant_of_shape,
     "Erf": lambda n, i: oracle.unary("Erf", i[0]),
     "Sigmoid": lambda n, i: oracle.unary("Sigmoid", i[0]),
     "Silu": lambda n, i: oracle.unary("SiLU", i[0]),

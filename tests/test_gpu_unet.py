@@ -161,9 +161,10 @@ def test_graph_replay_survives_workspace_growth(rng):
         x, ctx = _inputs(rng, 1, 16, 16, 77, cfg.cross_dim)
         bs, bt, bc = d.storage(x), d.storage(np.array([999.0], np.float32)), d.storage(ctx)
         bo = d.create_buffer(x.nbytes)
-        u.forward(bs, bt, bc, bo)
+        shape = dict(B=1, H=16, W=16, Sctx=77)
+        u.forward(bs, bt, bc, bo, **shape)
         eager = d.download(bo, np.float32, x.shape)
-        u.forward(bs, bt, bc, bo, graph=True)
+        u.forward(bs, bt, bc, bo, graph=True, **shape)
         d.sync()
         np.testing.assert_array_equal(d.download(bo, np.float32, x.shape), eager)
         ws0 = d.workspace_stats()
@@ -192,7 +193,7 @@ def test_graph_replay_survives_workspace_growth(rng):
         assert grown["retired"] == 1 and grown["pinned"] == 1
         for _ in range(2):
             d.fill_normal(bo, x.size, 9)
-            u.forward(bs, bt, bc, bo, graph=True)
+            u.forward(bs, bt, bc, bo, graph=True, **shape)
             d.sync()
             np.testing.assert_array_equal(d.download(bo, np.float32, x.shape), eager)
         u.destroy()
