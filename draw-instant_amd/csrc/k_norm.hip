@@ -21,6 +21,7 @@
 // before consuming any: `sched_barrier` stops the scheduler from sinking the
 // loads next to their uses, which would serialise them.
 #include <cstdlib>
+#include <mutex>
 
 #include "di_device.h"
 #include "di_kernels.h"
@@ -751,15 +752,25 @@ void nchw_slices(uint32_t L, uint32_t NG, uint32_t vec, uint32_t* S_out, uint32_
   *chunk_out = chunk;
 }
 
+// `fixed` (with `fixed_bytes`) replaces the context workspace for the
+// partials when non-null.
 template <typename T, int VEC>
 int gn_nchw_launch(Ctx* c, const void* x, const float* gamma, const float* beta, void* y,
-                   uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu) {
+                   uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu,
+                   float* fixed, uint64_t fixed_bytes) {
   const uint32_t L = cpg * HW, NG = N * G;
   uint32_t S, chunk;
   nchw_slices(L, NG, VEC, &S, &chunk);
-  void* ws = nullptr;
-  int rc = workspace(c, (uint64_t)NG * S * 2 * sizeof(float), &ws);
-  if (rc) return rc;
+  const uint64_t need = (uint64_t)NG * S * 2 * sizeof(float);
+  void* ws = fixed;
+  if (fixed) {
+    DI_REQUIRE(need <= fixed_bytes, DI_EUNSUPPORTED,
+               "group norm: %llu bytes of partials exceed the %llu-byte static scratch",
+               (unsigned long long)need, (unsigned long long)fixed_bytes);
+  } else {
+    int rc = workspace(c, need, &ws);
+    if (rc) return rc;
+  }
   float* part = (float*)ws;
   k_gn_nchw_partial<T, VEC><<<dim3(S, NG), 256, 0, c->stream>>>((const T*)x, L, chunk, part);
   k_gn_nchw_apply<T, VEC><<<dim3(S, NG), 256, 0, c->stream>>>(
@@ -769,14 +780,26 @@ int gn_nchw_launch(Ctx* c, const void* x, const float* gamma, const float* beta,
 
 template <typename T>
 int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* y, uint32_t N,
-            uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu) {
+            uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu, float* fixed,
+            uint64_t fixed_bytes) {
   DI_REQUIRE((uint64_t)N * G <= 65535u, DI_EUNSUPPORTED, "group norm: %llu groups exceed 65535",
              (unsigned long long)N * G);
   DI_REQUIRE((uint64_t)cpg * HW < (1ull << 31), DI_EUNSUPPORTED,
              "group norm: %llu elements per group exceed 2^31", (unsigned long long)cpg * HW);
   constexpr int V = 16 / sizeof(T);
-  if (HW % V == 0) return gn_nchw_launch<T, V>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu);
-  return gn_nchw_launch<T, 1>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu);
+  if (HW % V == 0)
+    return gn_nchw_launch<T, V>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, fixed,
+                                fixed_bytes);
+  return gn_nchw_launch<T, 1>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, fixed,
+                              fixed_bytes);
+}
+
+int gn_nchw_dt(Ctx* c, const void* x, const float* gamma, const float* beta, void* y,
+               uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu, int dt,
+               float* fixed, uint64_t fixed_bytes) {
+  if (dt == DI_F32)
+    return gn_nchw<float>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, fixed, fixed_bytes);
+  return gn_nchw<f16>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, fixed, fixed_bytes);
 }
 
 }  // namespace
@@ -784,8 +807,7 @@ int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* 
 int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const float* beta,
                            void* y, uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW,
                            float eps, bool silu, int dt) {
-  if (dt == DI_F32) return gn_nchw<float>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu);
-  return gn_nchw<f16>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu);
+  return gn_nchw_dt(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, dt, nullptr, 0);
 }
 
 uint32_t gn_nhwc_chunks(uint32_t N, uint32_t HW) {
@@ -979,16 +1001,54 @@ void launch_ln_fold(hipStream_t s, const f16* w, const float* gamma, const float
   k_ln_fold<<<(N + 3) / 4, 256, 0, s>>>(w, gamma, beta, bias, wf, sum, cst, N, K);
 }
 
+// ---------------- static scratch (di_group_norm_noalloc) ----------------
+// Partials of the no-allocation entry point live in this file-scope device
+// array instead of the context workspace: each GPU the library runs on holds
+// one copy until the process ends.  Host code never uses the array's name as
+// an address; it uses the device address hipGetSymbolAddress returns, looked
+// up once per device (with that device current) and kept per device.
+constexpr uint64_t kScratchBytes = 1ull << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the context's device (current on entry).
+int scratch_ptr(Ctx* c, float** out) {
+  DI_REQUIRE(c->device >= 0 && c->device < kMaxDevices, DI_EUNSUPPORTED,
+             "static scratch: device %d out of range", c->device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[c->device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    DI_REQUIRE(e == hipSuccess && p != nullptr, DI_EHIP,
+               "hipGetSymbolAddress(scratch) on device %d failed: %s", c->device,
+               hipGetErrorString(e));
+    g_scratch_ptr[c->device] = p;
+  }
+  *out = (float*)g_scratch_ptr[c->device];
+  return DI_OK;
+}
+
+}  // namespace
+
+// Shared body of di_group_norm and di_group_norm_noalloc: `fixed` (non-null)
+// holds the partials instead of the context workspace.
+int group_norm_impl(Ctx* ctx, di_handle X, di_handle gamma, di_handle beta, di_handle Y,
+                    uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps, int32_t flags,
+                    int32_t dt, int32_t layout, float* fixed, uint64_t fixed_bytes);
+
 }  // namespace di
 
 using namespace di;
 
-extern "C" {
-
-int32_t di_group_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta, di_handle Y,
-                      uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps,
-                      int32_t flags, int32_t dt, int32_t layout) {
-  DI_CTX(ctx);
+int di::group_norm_impl(Ctx* ctx, di_handle X, di_handle gamma, di_handle beta, di_handle Y,
+                        uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps,
+                        int32_t flags, int32_t dt, int32_t layout, float* fixed,
+                        uint64_t fixed_bytes) {
   DI_DTYPE(dt);
   DI_REQUIRE(layout == DI_NCHW || layout == DI_NHWC, DI_EINVAL, "di_group_norm: bad layout %d",
              layout);
@@ -1005,23 +1065,51 @@ int32_t di_group_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
   DI_REQUIRE(x->ptr != y->ptr, DI_EINVAL, "di_group_norm: Y may not alias X");
   bool silu = (flags & DI_NORM_SILU) != 0;
   if (layout == DI_NCHW) {
-    int rc = launch_group_norm_nchw(ctx, x->ptr, (const float*)g->ptr, (const float*)b->ptr,
-                                    y->ptr, N, G, cpg, HW, eps, silu, dt);
+    int rc = gn_nchw_dt(ctx, x->ptr, (const float*)g->ptr, (const float*)b->ptr, y->ptr, N, G,
+                        cpg, HW, eps, silu, dt, fixed, fixed_bytes);
     if (rc) return rc;
   } else {
     DI_REQUIRE(dt == DI_F16, DI_EUNSUPPORTED, "di_group_norm: NHWC requires fp16");
     DI_REQUIRE(C % 8 == 0 && C <= 4096 && G <= 256, DI_EUNSUPPORTED,
                "di_group_norm: NHWC needs C %% 8 == 0, C <= 4096, G <= 256 (C=%u G=%u)", C, G);
     DI_REQUIRE(N <= 65535u, DI_EUNSUPPORTED, "di_group_norm: batch too large");
-    void* ws = nullptr;
-    int rc = workspace(ctx, gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float), &ws);
-    if (rc) return rc;
+    const uint64_t need = gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float);
+    void* ws = fixed;
+    if (fixed) {
+      DI_REQUIRE(need <= fixed_bytes, DI_EUNSUPPORTED,
+                 "group norm: %llu bytes of partials exceed the %llu-byte static scratch",
+                 (unsigned long long)need, (unsigned long long)fixed_bytes);
+    } else {
+      int rc = workspace(ctx, need, &ws);
+      if (rc) return rc;
+    }
     NhwcSrc src{(const f16*)x->ptr, (const f16*)x->ptr, C, C, C};
     launch_group_norm_nhwc(ctx->stream, src, (const float*)g->ptr, (const float*)b->ptr, y->ptr,
                            N, C, G, HW, eps, silu, (float*)ws);
   }
   DI_LAUNCH_CHECK();
   return DI_OK;
+}
+
+extern "C" {
+
+int32_t di_group_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta, di_handle Y,
+                      uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW, float eps,
+                      int32_t flags, int32_t dt, int32_t layout) {
+  DI_CTX(ctx);
+  return group_norm_impl(ctx, X, gamma, beta, Y, N, G, cpg, HW, eps, flags, dt, layout, nullptr,
+                         0);
+}
+
+int32_t di_group_norm_noalloc(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
+                              di_handle Y, uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW,
+                              float eps, int32_t flags, int32_t dt, int32_t layout) {
+  DI_CTX(ctx);
+  float* fixed = nullptr;
+  int rc = scratch_ptr(ctx, &fixed);
+  if (rc) return rc;
+  return group_norm_impl(ctx, X, gamma, beta, Y, N, G, cpg, HW, eps, flags, dt, layout, fixed,
+                         kScratchBytes);
 }
 
 int32_t di_gn_silu(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta, di_handle Y,

@@ -220,6 +220,20 @@ int32_t di_group_norm(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
                       di_handle Y, uint32_t N, uint32_t G, uint32_t cpg,
                       uint32_t HW, float eps, int32_t flags, int32_t dtype,
                       int32_t layout);
+/* di_group_norm that allocates nothing: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results as di_group_norm; the partial sums live in a 1 MiB
+ * static device array per GPU (held until the process ends) instead of the
+ * context workspace.  That covers every NCHW call (at most 65535 groups) and
+ * NHWC calls up to a batch of 4096 at G = 32 (512 at G = 256); larger
+ * requests fail with DI_EUNSUPPORTED.  Nothing in the array needs clearing:
+ * every partial is written before it is read within the call.  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (two streams or contexts at once) race. */
+int32_t di_group_norm_noalloc(di_ctx* ctx, di_handle X, di_handle gamma,
+                              di_handle beta, di_handle Y, uint32_t N,
+                              uint32_t G, uint32_t cpg, uint32_t HW, float eps,
+                              int32_t flags, int32_t dtype, int32_t layout);
 /* The fused-resnet.js GN+SiLU entry point (== di_group_norm with DI_NORM_SILU). */
 int32_t di_gn_silu(di_ctx* ctx, di_handle X, di_handle gamma, di_handle beta,
                    di_handle Y, uint32_t N, uint32_t C, uint32_t G, uint32_t HW,
