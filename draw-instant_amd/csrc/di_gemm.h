@@ -27,7 +27,10 @@ enum TileCfg {
   TILE_128x64_W16 = 10,
   TILE_128x128_W16 = 11,
   TILE_64x64_W16 = 12,
-  TILE_COUNT = 13
+  // 3x3 stride-1 conv with the input halo staged per channel chunk
+  // (k_conv3.hip): 128 output pixels (whole rows) x 64 channels
+  TILE_CONV3_HALO = 13,
+  TILE_COUNT = 14
 };
 
 struct GemmPlan {
@@ -104,6 +107,12 @@ uint64_t gemm_ws_bytes(const GemmArgs& g);
 bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode);
 // Byte extent clamped to the buffer-load limit (0 = too large for it).
 inline uint32_t gemm_extent(uint64_t bytes) { return bytes < 0x7fff0000ull ? (uint32_t)bytes : 0; }
+// The halo conv kernel (TILE_CONV3_HALO, k_conv3.hip): whether it takes
+// this NHWC fp16 conv (3x3, stride 1, pad 1, no upsample, Cin % 64 == 0,
+// Cout % 64 == 0, width 16 / 32 / 64 / 128, one GEMM batch), and its launch
+// (vector epilogue, no split-K).
+bool conv3_halo_ok(const GemmArgs& g);
+void launch_conv3_halo(const GemmArgs& g, hipStream_t s);
 // elem: DI_F16 or DI_F32 operand element type.
 void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s);
 // Whether launch_gemm can produce g.stats for this call: buffer-load fp16

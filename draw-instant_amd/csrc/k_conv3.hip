@@ -1,0 +1,311 @@
+// 3x3 stride-1 NHWC fp16 convolution for gfx950 with the input halo staged
+// once per channel chunk (the U-Net's and VAE's wide-resolution convs).
+//
+// The implicit GEMM of k_gemm_kernel.h re-reads every input pixel for each
+// of the nine taps, and at B = 1 a CU's global-load throughput (measured
+// ~40 B/clk through the vector memory path, whether the data lands in VGPRs
+// or goes straight to LDS) bounds the kernel, not the MFMAs or HBM.  Here a
+// workgroup owns 128 output pixels = R whole image rows of width W (R =
+// 128 / W) and 64 output channels.  For each 64-channel input chunk it loads
+// the (R + 2) x (W + 2) pixel patch around its rows once (out-of-image
+// pixels arrive as zeros: the padding) and runs the chunk's nine taps from
+// it, each tap a 128 x 64 x 64 MFMA step whose A fragments are the patch
+// rows shifted by (ky, kx).  Bytes loaded per stage drop from 24 KB to
+// 8 KB of weights + ~3.7 KB of patch.
+//
+// Loads go global -> LDS directly (buffer_load ... lds: lane l of a wave
+// writes 16 bytes at base + 16 l), so the XOR chunk swizzle of the LDS rows
+// is applied on the global side: the lane that fills physical chunk p of row
+// r loads logical chunk p ^ ((r >> 1) & 7).  Six weight buffers, two patch
+// buffers; iteration s (stage s = chunk * 9 + tap) reads the MFMA fragments
+// of stage s + 1, runs the MFMAs of stage s, issues the weights of stage
+// s + 5 and, at the first taps, pieces of the next chunk's patch, then waits
+// until only the last three iterations' loads are outstanding (loads retire
+// in order) and meets the barrier: weights arriving from HBM get three
+// iterations.  Eight waves: four 32-row wave tiles x two k halves; the halves
+// are summed through LDS and the shared vector epilogue of the GEMM kernel
+// (bias, temb bias, residual, SiLU, GroupNorm statistics) writes the tile,
+// whose rows are contiguous output pixels.  With split-K (small spatial
+// sizes, few tiles) each split takes a range of channel chunks and the
+// epilogue writes fp32 partials for the GEMM's split-K reducer.
+#include <type_traits>
+
+#include "di_kernels.h"
+#include "k_gemm_kernel.h"
+
+namespace di {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+constexpr int CV_BM = 128, CV_BN = 64, CV_NT = 512;
+constexpr int CV_ROW = 128;                    // bytes per LDS row (64 fp16 channels)
+constexpr int CV_BBUF = CV_BN * CV_ROW;        // one weight stage: 8 KB
+constexpr int CV_LDC = CV_BN + 4;              // fp32 C tile row stride
+
+constexpr int CV_NBB = 6;                      // weight stage buffers
+
+template <int W>
+struct ConvGeo {
+  static constexpr int R = CV_BM / W;          // output rows per tile
+  static constexpr int PW = W + 2;             // patch width
+  static constexpr int PR = (R + 2) * PW;      // patch rows (pixels)
+  static constexpr int NP = (PR + 63) / 64;    // patch pieces: one 8-row DMA per wave each
+  static constexpr int PROWS = NP * 64;        // patch rows allocated
+  // pieces per tap: one at taps 0..NP-1, or two at taps 0..3 when NP > 5, so
+  // the last piece is issued by tap 4 (and lands by the end of tap 7)
+  static constexpr int PPT = NP > 5 ? 2 : 1;
+  static constexpr int SMEM_PIPE = 2 * PROWS * CV_ROW + CV_NBB * CV_BBUF;
+  static constexpr int SMEM_C = CV_BM * CV_LDC * 4;
+  static constexpr int SMEM = SMEM_PIPE > SMEM_C ? SMEM_PIPE : SMEM_C;
+  static_assert(NP <= 8 && (NP + PPT - 1) / PPT <= 5, "patch pieces issued by tap 4");
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  // patch pieces issued at tap t, and the vector-memory instructions a wave
+  // issues in a steady-state iteration at tap t (the weights of one stage
+  // plus those pieces)
+  static constexpr int pieces(int t) {
+    return t * PPT >= NP ? 0 : (NP - t * PPT < PPT ? NP - t * PPT : PPT);
+  }
+  static constexpr int issued(int t) { return 1 + pieces(((t % 9) + 9) % 9); }
+};
+
+// s_waitcnt with vmcnt = VM and lgkmcnt = LG (expcnt not waited on)
+template <int VM, int LG>
+__device__ __forceinline__ void cv_wait() {
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LG << 8));
+}
+
+// f(integral_constant<int, I>) for I = B .. E-1: loop bodies whose wait
+// counts and buffer indices must be compile-time constants
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+template <int W>
+__global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
+  using G = ConvGeo<W>;
+  __shared__ __attribute__((aligned(1024))) char smem[G::SMEM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = wave & 3, kh = wave >> 2;  // 32-row wave tile, k half
+  const int wm0 = wq * 32;
+
+  const uint32_t n_tiles = g.N / CV_BN;
+  uint32_t tile = blockIdx.x;
+  {
+    // deal contiguous runs of tiles to each XCD (its own L2): neighbours
+    // share the patch (same pixels) or the weights
+    const uint32_t n_wg = gridDim.x, per = n_wg / 8, rem = n_wg % 8, xcd = tile % 8,
+                   slot = tile / 8;
+    tile = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  }
+  const uint32_t m0 = (tile / n_tiles) * CV_BM, n0 = (tile % n_tiles) * CV_BN;
+  const uint32_t HW = g.H * W;
+  const uint32_t img = m0 / HW, y0 = (m0 % HW) / W;
+  // split-K over input-channel chunks: split blockIdx.y takes chunks
+  // [cb0, cb0 + nch) (the host picks splits dividing Cin / 64)
+  const uint32_t split = blockIdx.y;
+  const int nch = (int)(g.Cin / 64 / g.splits);
+  const int cb0 = (int)split * nch;
+  const int n_stages = nch * 9;
+
+  constexpr uint32_t kInv = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(g.a), (short)0, (int)g.a_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rA2 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(g.a2), (short)0, (int)g.a2_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(g.b), (short)0, (int)g.b_bytes, 0x00020000);
+
+  char* const patch = smem;                                 // [2][PROWS][128 B]
+  char* const wbuf = smem + 2 * G::PROWS * CV_ROW;          // [CV_NBB][64][128 B]
+
+  // ---- this lane's DMA slots ----
+  const int lrow = lane >> 3, lpos = lane & 7;
+  // weights: row n0 + wave * 8 + lrow, logical chunk lpos ^ swizzle
+  const int brow = wave * 8 + lrow;
+  const uint32_t fb = (n0 + brow) * (uint32_t)g.ldb * 2u + (uint32_t)(lpos ^ ((brow >> 1) & 7)) * 16u;
+  // patch pieces: patch row i * 64 + wave * 8 + lrow
+  uint32_t ppix[G::NP], pchk[G::NP];
+#pragma unroll
+  for (int i = 0; i < G::NP; i++) {
+    const int r = i * 64 + wave * 8 + lrow;
+    const int iy = (int)y0 - 1 + r / G::PW, ix = r % G::PW - 1;
+    const bool ok = r < G::PR && iy >= 0 && iy < (int)g.H && ix >= 0 && ix < W;
+    ppix[i] = ok ? (img * g.H + (uint32_t)iy) * W + (uint32_t)ix : kInv;
+    pchk[i] = (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+  }
+  // stage s = local chunk * 9 + tap; chunks below are global
+  auto dma_weights = [&](int stage, int buf) {
+    const uint32_t c = (uint32_t)(cb0 + stage / 9), t = (uint32_t)stage % 9u;
+    const uint32_t koff = (t * g.Cin + c * 64u) * 2u;  // uniform
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr)(wbuf + buf * CV_BBUF + wave * 8 * CV_ROW),
+                                             16, fb, koff, 0, 0);
+  };
+  auto dma_patch = [&](int chunk, int piece) {
+    const uint32_t cb = (uint32_t)chunk * 64u;
+    const bool s2 = cb >= g.c1;
+    const uint32_t ld2 = (uint32_t)(s2 ? g.lda2 : g.lda) * 2u;
+    const uint32_t ch2 = (s2 ? cb - g.c1 : cb) * 2u;
+    const uint32_t p = ppix[piece];
+    const uint32_t off = p != kInv ? p * ld2 + ch2 + pchk[piece] : kInv;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        s2 ? rA2 : rA,
+        (lds_ptr)(patch + (chunk & 1) * G::PROWS * CV_ROW + (piece * 64 + wave * 8) * CV_ROW), 16,
+        off, 0, 0, 0);
+  };
+
+  // ---- MFMA fragments (16x16x32 f16: lane row lane % 16, k (lane / 16) * 8) ----
+  const int fr = lane & 15;
+  const int cidx = kh * 4 + (lane >> 4);  // logical 16-byte k chunk of this lane
+  int pr0[2];
+#pragma unroll
+  for (int a = 0; a < 2; a++) {
+    const int p = wm0 + a * 16 + fr;
+    pr0[a] = (p / W) * G::PW + p % W;
+  }
+  struct Frags {
+    f16x8 a[2];
+    f16x8 b[4];
+  };
+  auto read_frags = [&](int chunk, int tap, int buf, Frags& f) {
+    const f16* pa = (const f16*)(patch + (chunk & 1) * G::PROWS * CV_ROW);
+    const int shift = (tap / 3) * G::PW + tap % 3;
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+      const int pr = pr0[a] + shift;
+      f.a[a] = *(const f16x8*)&pa[pr * 64 + ((cidx ^ ((pr >> 1) & 7)) * 8)];
+    }
+    const f16* pb = (const f16*)(wbuf + buf * CV_BBUF);
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const int rr = b * 16 + fr;
+      f.b[b] = *(const f16x8*)&pb[rr * 64 + ((cidx ^ ((rr >> 1) & 7)) * 8)];
+    }
+  };
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; a++)
+#pragma unroll
+    for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.a[a], f.b[b], acc[a][b], 0, 0, 0);
+  };
+
+  // ---- prologue: patch of the first chunk, weights of stages 0..NBB-2 ----
+  Frags F[2];
+#pragma unroll
+  for (int i = 0; i < G::NP; i++) dma_patch(cb0, i);
+#pragma unroll
+  for (int b = 0; b + 1 < CV_NBB; b++) dma_weights(b, b);
+  cv_wait<0, 15>();
+  __builtin_amdgcn_s_barrier();
+  read_frags(cb0, 0, 0, F[0]);
+  cv_wait<63, 0>();
+  __builtin_amdgcn_s_barrier();
+
+  // ---- steady state: two chunks (18 stages) per round, static tap,
+  // weight-buffer and fragment-set indices.  Iteration s issues the weights
+  // of stage s + NBB - 1 into the buffer stage s - 1 used; loads retire in
+  // order, so leaving the last three iterations' loads outstanding completes
+  // the weights of stage s + 2 (issued at s - 3) and every patch piece
+  // issued up to s - 3 ----
+  static_assert(18 % CV_NBB == 0, "buffer index static over a round");
+  int s0 = 0;
+  for (; s0 + 18 <= n_stages; s0 += 18) {
+    const int c0 = cb0 + s0 / 9;
+    static_for<0, 18>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr int tap = j % 9;
+      const int c = c0 + j / 9, cn = c0 + (j + 1) / 9;
+      read_frags(cn, (j + 1) % 9, (j + 1) % CV_NBB, F[(j + 1) & 1]);
+      mma(F[j & 1]);
+      dma_weights(s0 + j + CV_NBB - 1, (j + CV_NBB - 1) % CV_NBB);
+#pragma unroll
+      for (int q = 0; q < G::pieces(tap); q++) dma_patch(c + 1, tap * G::PPT + q);
+      cv_wait<G::issued(j) + G::issued(j - 1) + G::issued(j - 2), 0>();
+      __builtin_amdgcn_s_barrier();
+    });
+  }
+  // ---- tail: an odd chunk count leaves the last chunk (9 stages); the two
+  // iterations before it issued one load each (taps 7 and 8) ----
+  if (s0 < n_stages) {
+    const int c = cb0 + s0 / 9;
+    static_for<0, 9>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr auto tc = [](int i) { return i < 0 ? 1 : (i + CV_NBB - 1 < 9 ? 1 : 0); };
+      if constexpr (j + 1 < 9) read_frags(c, j + 1, (j + 1) % CV_NBB, F[(j + 1) & 1]);
+      mma(F[j & 1]);
+      if constexpr (j + CV_NBB - 1 < 9)
+        dma_weights(s0 + j + CV_NBB - 1, (j + CV_NBB - 1) % CV_NBB);
+      cv_wait<tc(j) + tc(j - 1) + tc(j - 2), 0>();
+      __builtin_amdgcn_s_barrier();
+    });
+  }
+  // loads past the last stage may still be landing: drain before the C tile
+  // reuses the pipeline's LDS
+  cv_wait<0, 0>();
+  __syncthreads();
+
+  // ---- epilogue: k half 0 writes the fp32 C tile, half 1 adds ----
+  float* sC = reinterpret_cast<float*>(smem);
+  const int rq = (lane >> 4) * 4;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    if (kh == h) {
+#pragma unroll
+      for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float& cc = sC[(wm0 + a * 16 + rq + i) * CV_LDC + b * 16 + fr];
+            cc = h == 0 ? acc[a][b][i] : cc + acc[a][b][i];
+          }
+    }
+    __syncthreads();
+  }
+  gemm_epilogue_vec<CV_BM, CV_BN, CV_LDC, CV_NT, EX_NONE>(g, sC, m0, n0, 0, split);
+  if (g.stats && g.splits == 1) {
+    __syncthreads();
+    gemm_tile_stats<CV_BM, CV_BN, CV_LDC, CV_NT>(g, sC, m0, n0);
+  }
+}
+
+template <int W>
+void launch_w(const GemmArgs& g, hipStream_t s) {
+  const uint32_t tiles = (g.M / CV_BM) * (g.N / CV_BN);
+  k_conv3_halo<W><<<dim3(tiles, g.splits), CV_NT, 0, s>>>(g);
+}
+
+}  // namespace
+
+bool conv3_halo_ok(const GemmArgs& g) {
+  const uint32_t W = g.W;
+  const bool single = g.a2 == nullptr || g.a2 == g.a || g.c1 == 0 || g.c1 == 0xffffffffu;
+  return g.Cin > 0 && g.ks == 3 && g.stride == 1 && g.pad == 1 && g.up == 1 && g.Cin % 64 == 0 &&
+         (single || g.c1 % 64 == 0) && g.N % CV_BN == 0 && g.Ho == g.H && g.Wo == W &&
+         (W == 16 || W == 32 || W == 64 || W == 128) && g.H % (CV_BM / W) == 0 &&
+         g.M % CV_BM == 0 && g.batch == 1 && g.b_vec_ok && g.a_bytes > 0 && g.b_bytes > 0 &&
+         (single || g.a2_bytes > 0) && g.K == 9 * g.Cin;
+}
+
+void launch_conv3_halo(const GemmArgs& g, hipStream_t s) {
+  switch (g.W) {
+    case 16: launch_w<16>(g, s); break;
+    case 32: launch_w<32>(g, s); break;
+    case 64: launch_w<64>(g, s); break;
+    default: launch_w<128>(g, s); break;
+  }
+}
+
+}  // namespace di
