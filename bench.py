@@ -110,28 +110,41 @@ def bench_unet_batch(dev, u, B=4, iters=20):
             b.destroy()
 
 
-def bench_denoise(dev, u, ctx, steps=4, reps=5):
+def bench_denoise(dev, u, ctx, steps=4, reps=21):
     """The SD-Turbo denoise loop (pipeline.js:274-288) on the device: noise,
     then per step scaleModelInput -> U-Net (graph) -> Euler update (scheduler
-    kernels, no host round trip).  HIP events around each whole loop; median
-    of `reps`; `scheduler_us_per_step` = loop time per step minus the bare
-    graph step time of the headline measurement."""
+    kernels, no host round trip).  Interleaved A/B: each rep times the whole
+    loop (A) and, right after, the same `steps` graph replays on the same
+    buffers without the scheduler kernels (B), each bracketed by HIP events;
+    `scheduler_us_per_step` is the median of (A - B) / steps with its
+    interquartile range."""
     from drawinstant import scheduler as S
     bc = dev.storage(ctx)
     lat = dev.create_buffer(4 * 64 * 64 * 4)
     d = S.Denoiser(u, steps=steps)
     d.run(bc, lat, seed=0)  # capture with these buffers
     dev.sync()
-    ts = []
+
+    def bare(i):
+        for _ in range(steps):
+            u.forward(d.model_in, d.tbuf, bc, d.pred, 1, 64, 64, 77, graph=True)
+    loop, diff = [], []
     for _ in range(reps):
-        ts.append(timed(dev, lambda i: d.run(bc, lat, seed=0), 1))
+        a = timed(dev, lambda i: d.run(bc, lat, seed=0), 1)
+        b = timed(dev, bare, 1)
+        loop.append(a)
+        diff.append((a - b) / steps * 1e3)
+    d.run(bc, lat, seed=0)
     out = dev.download(lat, np.float32)
     d.destroy()
     for b in (bc, lat):
         b.destroy()
-    ts.sort()
-    ms = ts[len(ts) // 2]
+    ms = float(np.median(loop))
+    q = np.percentile(diff, [25, 50, 75])
     return {"steps": steps, "ms": round(ms, 4), "ms_per_step": round(ms / steps, 4),
+            "scheduler_us_per_step": round(float(q[1]), 2),
+            "scheduler_us_per_step_iqr": [round(float(q[0]), 2), round(float(q[2]), 2)],
+            "method": f"median of {reps} interleaved A/B pairs (loop vs {steps} bare replays)",
             "final_latent_finite": bool(np.isfinite(out).all())}
 
 
@@ -352,10 +365,10 @@ def bench_executor_onnx(dev, reps=5):
     return row
 
 
-def bench_vae(dev, iters=10):
+def bench_vae(dev, iters=10, graph=True):
     """SD's VAE decoder as one native object (di_vae_decode): latent
-    [1,4,64,64] -> image [1,3,512,512], seeded weights, graph replay; HIP
-    events on the library stream."""
+    [1,4,64,64] -> image [1,3,512,512], seeded weights, graph replay (or
+    eager launches); HIP events on the library stream."""
     from drawinstant import perf
     from drawinstant.vae import VAE
     v = VAE(dev, seed=0)
@@ -363,7 +376,7 @@ def bench_vae(dev, iters=10):
     dev.fill_normal(z, 4 * 64 * 64, 11)
     img = dev.create_buffer(3 * 512 * 512 * 4)
     try:
-        run = lambda i: v.decode(z, img, 1, 64, 64, graph=True)
+        run = lambda i: v.decode(z, img, 1, 64, 64, graph=graph)
         run(0)
         run(0)
         ms = timed(dev, run, iters)
@@ -426,7 +439,7 @@ def bench_executor_vae(dev, reps=3):
     return row
 
 
-ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_gemm_conv3x3_64x64x320_pmc.md")
+ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_conv3_halo_conv3x3_64x64x320_pmc.md")
 
 
 def sclk_levels():
@@ -476,7 +489,8 @@ def roofline_conv(dev, iters=50):
                 traffic = int(float(line.split(":", 1)[1]))
     for b in (x, w, bias, y):
         b.destroy()
-    return {"kernel": "k_gemm implicit-GEMM conv3x3 320->320 @64x64 NHWC fp16 (fp32 acc)",
+    return {"kernel": "k_conv3_halo<64> conv3x3 320->320 @64x64 NHWC fp16 (fp32 acc), input "
+                      "halo staged per channel chunk",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": traffic,
             "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3),
@@ -495,6 +509,8 @@ def cpu_baseline(u, budget_blocks=None):
     sd = {k: v for k, v in u.state_dict(np.float32).items() if k.startswith("down_blocks.0.")
           or k.startswith("down_blocks.1.")}
     ops = unet_ref.OracleOps()
+    acc = oracle.accumulation("fp32")
+    acc.__enter__()
     rng = np.random.default_rng(4)
     h = rng.standard_normal((1, 320, 64, 64)).astype(np.float32)
     ts = rng.standard_normal((1, 1280)).astype(np.float32)
@@ -512,13 +528,17 @@ def cpu_baseline(u, budget_blocks=None):
                          sd["down_blocks.0.downsamplers.0.conv.bias"], stride=2, pad=1)
             w.add("sample_conv", perf.conv_flops(1, 320, 320, 32, 32, 3))
     sec = time.perf_counter() - t0
+    cores = int(oracle.lib().or_threads())
+    acc.__exit__(None, None, None)
     step = perf.unet_work().total
     return {"value": round(sec * 1e3 * step / w.total, 1), "unit": "ms",
-            "cores": int(oracle.lib().or_threads()), "kind": "port",
-            "sample": f"oracle/ C restatement (fp64 accumulation) of down_blocks.0-1 of the same "
-                      f"SD2.1 U-Net (4 ResNet + 4 transformer blocks + downsampler, "
-                      f"{w.total / 1e9:.1f} GFLOP) in {sec:.1f} s, scaled by FLOPs to the "
-                      f"{step / 1e9:.1f} GFLOP step"}
+            "cores": cores, "kind": "port",
+            "sample": f"CPU restatement, not the reference's WGSL (no Deno / Vulkan ICD on the "
+                      f"box): oracle/oracle.c built with fp32 accumulation in the reference "
+                      f"kernels' loop order (liboracle_f32.so, gcc -O3 -fopenmp, {cores} "
+                      f"threads), run on down_blocks.0-1 of the same SD2.1 U-Net (4 ResNet + 4 "
+                      f"transformer blocks + downsampler, {w.total / 1e9:.1f} GFLOP) in "
+                      f"{sec:.1f} s, scaled by FLOPs to the {step / 1e9:.1f} GFLOP step"}
 
 
 def pcie_inclusive(u, inputs, iters=5):
@@ -541,6 +561,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-blocks", action="store_true", help="skip the per-block figures")
+    ap.add_argument("--vae-only", action="store_true",
+                    help="only the native VAE decode leg (for rocprofv3 kernel summaries)")
+    ap.add_argument("--eager-only", type=int, default=0, metavar="K",
+                    help="only K eager (non-graph) U-Net steps after the warm-up, for rocprofv3 "
+                         "kernel summaries (with --vae-only: eager decodes)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline kernel and a 256 MiB copy (for rocprofv3 --pmc runs "
                          "that calibrate FETCH_SIZE / WRITE_SIZE against a known byte count)")
@@ -564,6 +589,24 @@ def main():
         print(json.dumps({"roofline": rl, "calibration_read_bytes": n * 4,
                           "calibration_write_bytes": n * 4}), flush=True)
         return
+    if args.vae_only:
+        print(json.dumps({"vae_decode_512": bench_vae(dev, graph=not args.eager_only)}), flush=True)
+        return
+    if args.eager_only:
+        from drawinstant.unet import UNet
+        u = UNet(dev, seed=501)
+        rng = np.random.default_rng(0)
+        bs = dev.storage(rng.standard_normal((1, 4, 64, 64)).astype(np.float32))
+        bc = dev.storage(rng.standard_normal((1, 77, 1024)).astype(np.float32))
+        bt = dev.storage(np.array([999.0], np.float32))
+        bo = dev.create_buffer(4 * 64 * 64 * 4)
+        step = lambda i: u.forward(bs, bt, bc, bo, 1, 64, 64, 77, graph=False)
+        for i in range(args.warmup):
+            step(i)
+        ms = timed(dev, step, args.eager_only)
+        print(json.dumps({"eager_steps": args.eager_only, "eager_ms_per_step": round(ms, 4)}),
+              flush=True)
+        return
     u, ms, wall, eager, finite, inputs = bench_unet(dev, args)
     work = perf.unet_work()
     line = {
@@ -585,8 +628,6 @@ def main():
         "denoise_loop": bench_denoise(dev, u, inputs[1]),
         "batch4": bench_unet_batch(dev, u, 4),
     }
-    line["denoise_loop"]["scheduler_us_per_step"] = round(
-        (line["denoise_loop"]["ms_per_step"] - ms) * 1e3, 1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(u)
     if not args.no_blocks:

@@ -108,9 +108,10 @@ bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode);
 // Byte extent clamped to the buffer-load limit (0 = too large for it).
 inline uint32_t gemm_extent(uint64_t bytes) { return bytes < 0x7fff0000ull ? (uint32_t)bytes : 0; }
 // The halo conv kernel (TILE_CONV3_HALO, k_conv3.hip): whether it takes
-// this NHWC fp16 conv (3x3, stride 1, pad 1, no upsample, Cin % 64 == 0,
-// Cout % 64 == 0, width 16 / 32 / 64 / 128, one GEMM batch), and its launch
-// (vector epilogue, no split-K).
+// this NHWC fp16 conv (3x3, stride 1, pad 1, optional 2x nearest upsample,
+// Cin % 64 == 0, Cout % 64 == 0, output width 16 / 32 / 64 or a multiple of
+// 128, one GEMM batch), and its launch (vector epilogue; split-K over
+// channel chunks writes partials for the split-K reducer).
 bool conv3_halo_ok(const GemmArgs& g);
 void launch_conv3_halo(const GemmArgs& g, hipStream_t s);
 // elem: DI_F16 or DI_F32 operand element type.

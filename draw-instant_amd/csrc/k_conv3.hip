@@ -6,7 +6,9 @@
 // ~40 B/clk through the vector memory path, whether the data lands in VGPRs
 // or goes straight to LDS) bounds the kernel, not the MFMAs or HBM.  Here a
 // workgroup owns 128 output pixels = R whole image rows of width W (R =
-// 128 / W) and 64 output channels.  For each 64-channel input chunk it loads
+// 128 / W), or a 128-pixel run of one row of a wider image, and 64 output
+// channels; with a fused 2x nearest upsample the patch pixels map to the
+// source at half resolution.  For each 64-channel input chunk it loads
 // the (R + 2) x (W + 2) pixel patch around its rows once (out-of-image
 // pixels arrive as zeros: the padding) and runs the chunk's nine taps from
 // it, each tap a 128 x 64 x 64 MFMA step whose A fragments are the patch
@@ -105,8 +107,11 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
     tile = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
   }
   const uint32_t m0 = (tile / n_tiles) * CV_BM, n0 = (tile % n_tiles) * CV_BN;
-  const uint32_t HW = g.H * W;
-  const uint32_t img = m0 / HW, y0 = (m0 % HW) / W;
+  // output image Ho x Wo (the 2x nearest upsample of the H x W source when
+  // g.up == 2); the tile is R rows x W pixels from (y0, x0), W = min(Wo, 128)
+  const uint32_t HWo = g.Ho * g.Wo;
+  const uint32_t img = m0 / HWo, y0 = (m0 % HWo) / g.Wo, x0 = (m0 % HWo) % g.Wo;
+  const uint32_t ush = g.up == 2 ? 1u : 0u;
   // split-K over input-channel chunks: split blockIdx.y takes chunks
   // [cb0, cb0 + nch) (the host picks splits dividing Cin / 64)
   const uint32_t split = blockIdx.y;
@@ -135,9 +140,9 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < G::NP; i++) {
     const int r = i * 64 + wave * 8 + lrow;
-    const int iy = (int)y0 - 1 + r / G::PW, ix = r % G::PW - 1;
-    const bool ok = r < G::PR && iy >= 0 && iy < (int)g.H && ix >= 0 && ix < W;
-    ppix[i] = ok ? (img * g.H + (uint32_t)iy) * W + (uint32_t)ix : kInv;
+    const int iy = (int)y0 - 1 + r / G::PW, ix = (int)x0 - 1 + r % G::PW;
+    const bool ok = r < G::PR && iy >= 0 && iy < (int)g.Ho && ix >= 0 && ix < (int)g.Wo;
+    ppix[i] = ok ? (img * g.H + ((uint32_t)iy >> ush)) * g.W + ((uint32_t)ix >> ush) : kInv;
     pchk[i] = (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
   }
   // stage s = local chunk * 9 + tap; chunks below are global
@@ -290,17 +295,18 @@ void launch_w(const GemmArgs& g, hipStream_t s) {
 }  // namespace
 
 bool conv3_halo_ok(const GemmArgs& g) {
-  const uint32_t W = g.W;
+  const uint32_t Wo = g.Wo, TW = Wo < 128 ? Wo : 128;
   const bool single = g.a2 == nullptr || g.a2 == g.a || g.c1 == 0 || g.c1 == 0xffffffffu;
-  return g.Cin > 0 && g.ks == 3 && g.stride == 1 && g.pad == 1 && g.up == 1 && g.Cin % 64 == 0 &&
-         (single || g.c1 % 64 == 0) && g.N % CV_BN == 0 && g.Ho == g.H && g.Wo == W &&
-         (W == 16 || W == 32 || W == 64 || W == 128) && g.H % (CV_BM / W) == 0 &&
-         g.M % CV_BM == 0 && g.batch == 1 && g.b_vec_ok && g.a_bytes > 0 && g.b_bytes > 0 &&
-         (single || g.a2_bytes > 0) && g.K == 9 * g.Cin;
+  return g.Cin > 0 && g.ks == 3 && g.stride == 1 && g.pad == 1 && (g.up == 1 || g.up == 2) &&
+         g.Cin % 64 == 0 && (single || g.c1 % 64 == 0) && g.N % CV_BN == 0 &&
+         g.Ho == g.H * g.up && Wo == g.W * g.up &&
+         (TW == 16 || TW == 32 || TW == 64 || TW == 128) && Wo % TW == 0 &&
+         g.Ho % (CV_BM / TW) == 0 && g.M % CV_BM == 0 && g.batch == 1 && g.b_vec_ok &&
+         g.a_bytes > 0 && g.b_bytes > 0 && (single || g.a2_bytes > 0) && g.K == 9 * g.Cin;
 }
 
 void launch_conv3_halo(const GemmArgs& g, hipStream_t s) {
-  switch (g.W) {
+  switch (g.Wo < 128 ? g.Wo : 128) {
     case 16: launch_w<16>(g, s); break;
     case 32: launch_w<32>(g, s); break;
     case 64: launch_w<64>(g, s); break;

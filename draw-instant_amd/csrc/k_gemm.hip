@@ -223,10 +223,13 @@ GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
   const char* env_tile = getenv("DI_GEMM_TILE");
   const char* env_split = getenv("DI_GEMM_SPLITS");
   GemmPlan best{TILE_64x64, 1};
-  // 3x3 convs the halo kernel takes (DI_CONV_HALO=0 turns it off for A/B runs)
+  // 3x3 convs the halo kernel takes, from 5 channel chunks up (with fewer,
+  // measured on the VAE's 128- / 256-channel convs, the pipeline prologue
+  // dominates and the implicit GEMM's larger tiles win); DI_CONV_HALO=0
+  // turns it off for A/B runs
   const char* env_halo = getenv("DI_CONV_HALO");
-  if (elem == DI_F16 && !env_tile && (!env_halo || atoi(env_halo) != 0) && conv3_halo_ok(g) &&
-      vec_epi_ok(g, elem, TILE_CONV3_HALO)) {
+  if (elem == DI_F16 && !env_tile && (!env_halo || atoi(env_halo) != 0) && g.Cin >= 320 &&
+      conv3_halo_ok(g) && vec_epi_ok(g, elem, TILE_CONV3_HALO)) {
     // channel-chunk splits bring the workgroup count near 224 (measured best
     // at 16x16 / 32x32 / 64x64: 200-240 workgroups, one per CU)
     const uint32_t tiles = (g.M / 128) * (g.N / 64), nch = g.Cin / 64;

@@ -6,7 +6,8 @@ CPU baseline), never as the thing measured or shipped.  The product path
 (``drawinstant``) must not import this package.
 
 The arithmetic lives in ``oracle.c`` (a plain-C restatement of the reference
-WGSL kernels with fp64 accumulation, built to ``_build/liboracle.so``); this
+WGSL kernels with fp64 accumulation, built to ``_build/liboracle.so``, and
+once more with fp32 accumulation for the CPU baseline only); this
 module wraps it for numpy arrays and composes the block-level references
 (ResNet block, transformer block, full SD2.1 U-Net) in ``blocks.py``.
 """
@@ -20,7 +21,12 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SO = os.path.join(_HERE, "_build", "liboracle.so")
+# the same loops accumulating in fp32 (-DOR_ACC=float): bench.py's CPU
+# baseline only; every check uses the fp64 build
+_SO32 = os.path.join(_HERE, "_build", "liboracle_f32.so")
 _lib = None
+_libs: dict = {}
+_use_f32 = False
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
@@ -39,13 +45,38 @@ def build(force: bool = False) -> str:
     return _SO
 
 
+class accumulation:
+    """``with oracle.accumulation("fp32"):`` routes the wrappers to the fp32
+    build (the CPU baseline's precision); fp64 otherwise."""
+
+    def __init__(self, kind: str):
+        assert kind in ("fp32", "fp64")
+        self.kind = kind
+
+    def __enter__(self):
+        global _use_f32, _lib
+        self.prev = _use_f32
+        _use_f32 = self.kind == "fp32"
+        _lib = None
+        return self
+
+    def __exit__(self, *exc):
+        global _use_f32, _lib
+        _use_f32 = self.prev
+        _lib = None
+
+
 def lib():
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(_SO):
+    so = _SO32 if _use_f32 else _SO
+    if so in _libs:
+        _lib = _libs[so]
+        return _lib
+    if not os.path.exists(so):
         build()
-    L = ctypes.CDLL(_SO)
+    L = ctypes.CDLL(so)
     sig = {
         "or_threads": ([], _int),
         "or_unary": ([_int, _f32p, _f32p, _i64], None),
@@ -71,6 +102,7 @@ def lib():
         fn = getattr(L, name)
         fn.argtypes = argt
         fn.restype = rest
+    _libs[so] = L
     _lib = L
     return L
 

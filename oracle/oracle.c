@@ -8,6 +8,9 @@
  *
  * Conventions: fp32 tensors in and out, fp64 accumulation, the reference's
  * own formulas and index maths (each function cites the WGSL it restates).
+ * Built a second time with -DOR_ACC=float (liboracle_f32.so): the same loops
+ * accumulating in fp32, the reference kernels' own precision, which
+ * bench.py times as the CPU baseline; the checker is always the fp64 build.
  * Layouts are the reference's: activations NCHW, conv weights OIHW, linear
  * weights as each reference kernel reads them.  Parallel over outer loops with
  * OpenMP; the thread count used is reported by or_threads().
@@ -15,13 +18,19 @@
  * Parity pinning of every function is done by tests/test_oracle.py (closed-
  * form KATs from wgsl-ops-test.js, library routines, invariants).
  */
-#include <math.h>
+#include <tgmath.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
+
+/* accumulation / intermediate type (see the header comment) */
+#ifndef OR_ACC
+#define OR_ACC double
+#endif
+typedef OR_ACC acc_t;
 
 int or_threads(void) {
 #ifdef _OPENMP
@@ -34,22 +43,22 @@ int or_threads(void) {
 /* ---------------- activations (wgsl-ops.js:58-81) ---------------- */
 
 /* Abramowitz & Stegun 7.1.26, wgsl-ops.js:77-81 / wgsl-executor.js:687-691. */
-static double erf_as(double x) {
-  double a = fabs(x);
-  double t = 1.0 / (1.0 + 0.3275911 * a);
-  double y = 1.0 - (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t -
+static acc_t erf_as(acc_t x) {
+  acc_t a = fabs(x);
+  acc_t t = 1.0 / (1.0 + 0.3275911 * a);
+  acc_t y = 1.0 - (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t -
                      0.284496736) * t + 0.254829592) * t * exp(-a * a);
   return x >= 0.0 ? y : -y;
 }
-static double silu(double x) { return x / (1.0 + exp(-x)); }                    /* :68 */
-static double gelu_erf(double x) { return x * 0.5 * (1.0 + erf_as(x * 0.70710678)); } /* :70 */
+static acc_t silu(acc_t x) { return x / (1.0 + exp(-x)); }                    /* :68 */
+static acc_t gelu_erf(acc_t x) { return x * 0.5 * (1.0 + erf_as(x * 0.70710678)); } /* :70 */
 /* fused-block.js:68-75 tanh approximation */
-static double gelu_tanh(double x) {
+static acc_t gelu_tanh(acc_t x) {
   return 0.5 * x * (1.0 + tanh(0.7978845608 * (x + 0.044715 * x * x * x)));
 }
 
 /* op codes match include/drawinstant.h DI_UN_* */
-static double unary_op(int op, double x) {
+static acc_t unary_op(int op, acc_t x) {
   switch (op) {
     case 0: return 1.0 / (1.0 + exp(-x));       /* Sigmoid */
     case 1: return sqrt(x > 0.0 ? x : 0.0);     /* Sqrt */
@@ -73,14 +82,14 @@ void or_unary(int op, const float* x, float* y, int64_t n) {
 }
 
 /* BINARY_EXPRS wgsl-ops.js:130-134, DI_BIN_* codes. */
-static double binary_op(int op, double a, double b) {
+static acc_t binary_op(int op, acc_t a, acc_t b) {
   switch (op) {
     case 0: return a + b;
     case 1: return a - b;
     case 2: return a * b;
     case 3: return a / b;
     case 4: {
-      double r = pow(fabs(a), b);
+      acc_t r = pow(fabs(a), b);
       int neg = a < 0.0 && (b - floor(b)) == 0.0 && (((int)b) & 1) == 1;
       return neg ? -r : r;
     }
@@ -118,13 +127,13 @@ void or_binary_bcast(int op, const float* a, const float* b, float* y, int rank,
 
 /* powScalar wgsl-ops.js:1058-1071. */
 void or_pow_scalar(const float* x, float* y, int64_t n, float e) {
-  double ei = floor(e);
+  acc_t ei = floor(e);
   int is_int = fabs(e - ei) < 1e-6;
   for (int64_t i = 0; i < n; i++) {
-    double v = x[i];
+    acc_t v = x[i];
     if (v < 0.0 && !is_int) y[i] = 0.0f;
     else {
-      double s = (v < 0.0 && (((int)ei) & 1) == 1) ? -1.0 : 1.0;
+      acc_t s = (v < 0.0 && (((int)ei) & 1) == 1) ? -1.0 : 1.0;
       y[i] = (float)(s * pow(fabs(v), e));
     }
   }
@@ -135,7 +144,7 @@ void or_softmax(const float* x, float* y, int64_t rows, int64_t inner) {
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; r++) {
     const float* xr = x + r * inner;
-    double m = -1e300, s = 0.0;
+    acc_t m = -1e300, s = 0.0;
     for (int64_t j = 0; j < inner; j++) m = xr[j] > m ? xr[j] : m;
     for (int64_t j = 0; j < inner; j++) s += exp(xr[j] - m);
     for (int64_t j = 0; j < inner; j++) y[r * inner + j] = (float)(exp(xr[j] - m) / s);
@@ -145,9 +154,9 @@ void or_softmax(const float* x, float* y, int64_t rows, int64_t inner) {
 /* WGSL_REDUCE_MEAN wgsl-ops.js:958-972. */
 void or_reduce_mean(const float* x, float* y, int64_t rows, int64_t inner) {
   for (int64_t r = 0; r < rows; r++) {
-    double s = 0.0;
+    acc_t s = 0.0;
     for (int64_t j = 0; j < inner; j++) s += x[r * inner + j];
-    y[r] = (float)(s / (double)inner);
+    y[r] = (float)(s / (acc_t)inner);
   }
 }
 
@@ -161,19 +170,19 @@ void or_group_norm(const float* x, const float* gamma, const float* beta, float*
 #pragma omp parallel for schedule(static)
   for (int64_t ng = 0; ng < N * G; ng++) {
     const float* xg = x + ng * L;
-    double s = 0.0, q = 0.0;
+    acc_t s = 0.0, q = 0.0;
     for (int64_t i = 0; i < L; i++) {
       s += xg[i];
-      q += (double)xg[i] * xg[i];
+      q += (acc_t)xg[i] * xg[i];
     }
-    double mean = s / (double)L;
-    double var = q / (double)L - mean * mean;
+    acc_t mean = s / (acc_t)L;
+    acc_t var = q / (acc_t)L - mean * mean;
     if (var < 0.0) var = 0.0;
-    double rstd = 1.0 / sqrt(var + (double)eps);
+    acc_t rstd = 1.0 / sqrt(var + (acc_t)eps);
     int64_t g = ng % G;
     for (int64_t i = 0; i < L; i++) {
       int64_t c = g * cpg + i / HW;
-      double t = ((double)xg[i] - mean) * rstd * gamma[c] + beta[c];
+      acc_t t = ((acc_t)xg[i] - mean) * rstd * gamma[c] + beta[c];
       y[ng * L + i] = (float)(silu_on ? silu(t) : t);
     }
   }
@@ -185,17 +194,17 @@ void or_layer_norm(const float* x, const float* gamma, const float* beta, float*
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; r++) {
     const float* xr = x + r * inner;
-    double s = 0.0, q = 0.0;
+    acc_t s = 0.0, q = 0.0;
     for (int64_t i = 0; i < inner; i++) {
       s += xr[i];
-      q += (double)xr[i] * xr[i];
+      q += (acc_t)xr[i] * xr[i];
     }
-    double mean = s / (double)inner;
-    double var = q / (double)inner - mean * mean;
+    acc_t mean = s / (acc_t)inner;
+    acc_t var = q / (acc_t)inner - mean * mean;
     if (var < 0.0) var = 0.0;
-    double rstd = 1.0 / sqrt(var + (double)eps);
+    acc_t rstd = 1.0 / sqrt(var + (acc_t)eps);
     for (int64_t i = 0; i < inner; i++)
-      y[r * inner + i] = (float)(((double)xr[i] - mean) * rstd * gamma[i] + beta[i]);
+      y[r * inner + i] = (float)(((acc_t)xr[i] - mean) * rstd * gamma[i] + beta[i]);
   }
 }
 
@@ -211,17 +220,17 @@ void or_conv2d(const float* x, const float* w, const float* bias, float* y, int6
 #pragma omp parallel for collapse(2) schedule(dynamic)
   for (int64_t n = 0; n < N; n++) {
     for (int64_t oc = 0; oc < Cout; oc++) {
-      double* acc = (double*)malloc(sizeof(double) * Ho * Wo);
+      acc_t* acc = (acc_t*)malloc(sizeof(acc_t) * Ho * Wo);
       for (int64_t p = 0; p < Ho * Wo; p++) acc[p] = bias ? bias[oc] : 0.0;
       for (int64_t ci = 0; ci < Cin; ci++) {
         const float* xc = x + (n * Cin + ci) * H * W;
         for (int64_t ky = 0; ky < K; ky++) {
           for (int64_t kx = 0; kx < K; kx++) {
-            double wv = w[((oc * Cin + ci) * K + ky) * K + kx];
+            acc_t wv = w[((oc * Cin + ci) * K + ky) * K + kx];
             for (int64_t oy = 0; oy < Ho; oy++) {
               int64_t iy = oy * S + ky - PAD;
               if (iy < 0 || iy >= H) continue;
-              double* ar = acc + oy * Wo;
+              acc_t* ar = acc + oy * Wo;
               const float* xr = xc + iy * W;
               for (int64_t ox = 0; ox < Wo; ox++) {
                 int64_t ix = ox * S + kx - PAD;
@@ -246,9 +255,9 @@ void or_matmul(const float* a, const float* b, float* y, int64_t M, int64_t N, i
     for (int64_t r = 0; r < M; r++) {
       const float* ar = a + (bz * M + r) * K;
       const float* bb = b + (b_batched ? bz * K * N : 0);
-      double* acc = (double*)calloc(N, sizeof(double));
+      acc_t* acc = (acc_t*)calloc(N, sizeof(acc_t));
       for (int64_t k = 0; k < K; k++) {
-        double av = ar[k];
+        acc_t av = ar[k];
         const float* br = bb + k * N;
         for (int64_t c = 0; c < N; c++) acc[c] += av * br[c];
       }
@@ -264,9 +273,9 @@ void or_gemm(const float* a, const float* b, const float* c, float* y, int64_t M
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < M; r++) {
     for (int64_t col = 0; col < N; col++) {
-      double s = 0.0;
+      acc_t s = 0.0;
       for (int64_t k = 0; k < K; k++)
-        s += (double)a[r * K + k] * (trans_b ? b[col * K + k] : b[k * N + col]);
+        s += (acc_t)a[r * K + k] * (trans_b ? b[col * K + k] : b[k * N + col]);
       y[r * N + col] = (float)(s + (c ? c[col] : 0.0));
     }
   }
@@ -281,8 +290,8 @@ void or_linear(const float* x, const float* w, const float* bias, float* y, int6
     const float* xr = x + r * K;
     for (int64_t n = 0; n < N; n++) {
       const float* wr = w + n * K;
-      double s = 0.0;
-      for (int64_t k = 0; k < K; k++) s += (double)xr[k] * wr[k];
+      acc_t s = 0.0;
+      for (int64_t k = 0; k < K; k++) s += (acc_t)xr[k] * wr[k];
       y[r * N + n] = (float)(s + (bias ? bias[n] : 0.0));
     }
   }
@@ -303,22 +312,22 @@ void or_attention(const float* q, const float* k, const float* v, float* o, int6
     for (int64_t i = 0; i < Sq; i++) {
       int64_t b = bh / H, h = bh % H;
       const float* qi = q + b * q_bs + h * q_hs + i * q_rs;
-      double* sc = (double*)malloc(sizeof(double) * Skv);
-      double m = -1e300;
+      acc_t* sc = (acc_t*)malloc(sizeof(acc_t) * Skv);
+      acc_t m = -1e300;
       for (int64_t j = 0; j < Skv; j++) {
         const float* kj = k + b * k_bs + h * k_hs + j * k_rs;
-        double s = 0.0;
-        for (int64_t t = 0; t < d; t++) s += (double)qi[t] * kj[t];
+        acc_t s = 0.0;
+        for (int64_t t = 0; t < d; t++) s += (acc_t)qi[t] * kj[t];
         sc[j] = s * scale;
         if (sc[j] > m) m = sc[j];
       }
-      double z = 0.0;
+      acc_t z = 0.0;
       for (int64_t j = 0; j < Skv; j++) {
         sc[j] = exp(sc[j] - m);
         z += sc[j];
       }
       float* oi = o + b * o_bs + h * o_hs + i * o_rs;
-      double* acc = (double*)calloc(d, sizeof(double));
+      acc_t* acc = (acc_t*)calloc(d, sizeof(acc_t));
       for (int64_t j = 0; j < Skv; j++) {
         const float* vj = v + b * v_bs + h * v_hs + j * v_rs;
         for (int64_t t = 0; t < d; t++) acc[t] += sc[j] * vj[t];
@@ -336,21 +345,21 @@ void or_attention(const float* q, const float* k, const float* v, float* o, int6
 void or_tembed(float t, const float* w1, const float* b1, const float* w2, const float* b2,
                float* y, int64_t emb_dim, int64_t hid) {
   int64_t half = emb_dim / 2;
-  double* e = (double*)malloc(sizeof(double) * emb_dim);
-  double* h = (double*)malloc(sizeof(double) * hid);
+  acc_t* e = (acc_t*)malloc(sizeof(acc_t) * emb_dim);
+  acc_t* h = (acc_t*)malloc(sizeof(acc_t) * hid);
   for (int64_t i = 0; i < emb_dim; i++) {
     int64_t fi = i < half ? i : i - half;
-    double freq = exp(-log(10000.0) * (double)fi / (double)half);
-    double arg = (double)t * freq;
+    acc_t freq = exp(-log(10000.0) * (acc_t)fi / (acc_t)half);
+    acc_t arg = (acc_t)t * freq;
     e[i] = i < half ? cos(arg) : sin(arg);
   }
   for (int64_t o = 0; o < hid; o++) {
-    double s = b1[o];
+    acc_t s = b1[o];
     for (int64_t k = 0; k < emb_dim; k++) s += e[k] * w1[o * emb_dim + k];
     h[o] = silu(s);
   }
   for (int64_t o = 0; o < hid; o++) {
-    double s = b2[o];
+    acc_t s = b2[o];
     for (int64_t k = 0; k < hid; k++) s += h[k] * w2[o * hid + k];
     y[o] = (float)s;
   }

@@ -333,3 +333,33 @@ def test_fill_normal_moments():
     assert abs(x.mean()) < 4e-3 and abs(x.std() - 1.0) < 4e-3
     y = oracle.fill_normal(1000, seed=42, mean=2.0, std=0.5)
     np.testing.assert_allclose(y, 2.0 + 0.5 * x[:1000].astype(np.float32), rtol=1e-6)
+
+
+def test_fp32_accumulation_build_matches_fp64():
+    """liboracle_f32.so (the CPU baseline's build) runs the same loops in fp32:
+    within fp32 rounding of the fp64 checker on a conv, a GroupNorm+SiLU, a
+    linear and an attention; a dropped term or a changed loop would not be."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((1, 64, 16, 16)).astype(np.float32)
+    w = (rng.standard_normal((32, 64, 3, 3)) / 24).astype(np.float32)
+    b = rng.standard_normal(32).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(64)).astype(np.float32)
+    bt = (0.1 * rng.standard_normal(64)).astype(np.float32)
+    xl = rng.standard_normal((40, 96)).astype(np.float32)
+    wl = (rng.standard_normal((48, 96)) / 10).astype(np.float32)
+    q, k, v = (rng.standard_normal((1, 2, 33, 64)).astype(np.float32) for _ in range(3))
+
+    def run():
+        return [oracle.conv2d(x, w, b, stride=1, pad=1),
+                oracle.group_norm(x, g, bt, 32, eps=1e-5, silu=True),
+                oracle.linear(xl, wl, None),
+                oracle.attention(q, k, v, layout="bhsd")]
+    ref = run()
+    with oracle.accumulation("fp32"):
+        got = run()
+    after = run()
+    for r, a, z in zip(ref, got, after):
+        assert np.array_equal(r, z)  # the context restores the fp64 build
+        rel = np.linalg.norm(a.astype(np.float64) - r) / np.linalg.norm(r)
+        assert 0 < rel < 1e-5 or np.array_equal(a, r)
+        assert np.max(np.abs(a - r)) <= 1e-4 * max(1.0, float(np.max(np.abs(r))))
