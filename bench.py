@@ -501,44 +501,66 @@ def roofline_conv(dev, iters=50):
                              if sclk_cur else None)}
 
 
-def cpu_baseline(u, budget_blocks=None):
-    """Oracle (C, OpenMP) on down_blocks.0-1 of the same U-Net, scaled to a step."""
+def cpu_baseline(u):
+    """One whole SD2.1 denoise step (same weights, latent, context and
+    timestep as the headline) on the fp32 CPU restatement, timed end to end."""
     import oracle
     from oracle import unet_ref
     from drawinstant import perf
-    sd = {k: v for k, v in u.state_dict(np.float32).items() if k.startswith("down_blocks.0.")
-          or k.startswith("down_blocks.1.")}
-    ops = unet_ref.OracleOps()
-    acc = oracle.accumulation("fp32")
-    acc.__enter__()
-    rng = np.random.default_rng(4)
-    h = rng.standard_normal((1, 320, 64, 64)).astype(np.float32)
-    ts = rng.standard_normal((1, 1280)).astype(np.float32)
+    sd = u.state_dict(np.float32)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, 4, 64, 64)).astype(np.float32)
     ctx = rng.standard_normal((1, 77, 1024)).astype(np.float32)
-    w = perf.Work()
-    t0 = time.perf_counter()
-    for i, (cin, c, hw) in enumerate(((320, 320, 64), (320, 640, 32))):
-        for j in range(2):
-            h = unet_ref.resnet(ops, sd, f"down_blocks.{i}.resnets.{j}", h, ts)
-            perf.resnet_flops(w, 1, cin if j == 0 else c, c, hw, hw)
-            h = unet_ref.transformer(ops, sd, f"down_blocks.{i}.attentions.{j}", h, ctx)
-            perf.transformer_flops(w, 1, c, hw, hw)
-        if i == 0:
-            h = ops.conv(h, sd["down_blocks.0.downsamplers.0.conv.weight"],
-                         sd["down_blocks.0.downsamplers.0.conv.bias"], stride=2, pad=1)
-            w.add("sample_conv", perf.conv_flops(1, 320, 320, 32, 32, 3))
-    sec = time.perf_counter() - t0
-    cores = int(oracle.lib().or_threads())
-    acc.__exit__(None, None, None)
+    with oracle.accumulation("fp32"):
+        ops = unet_ref.OracleOps()
+        t0 = time.perf_counter()
+        out = unet_ref.unet_forward(ops, sd, u.config.as_dict(), x,
+                                    np.array([999.0], np.float32), ctx)
+        sec = time.perf_counter() - t0
+        cores = int(oracle.lib().or_threads())
     step = perf.unet_work().total
-    return {"value": round(sec * 1e3 * step / w.total, 1), "unit": "ms",
-            "cores": cores, "kind": "port",
+    return {"value": round(sec * 1e3, 1), "unit": "ms", "cores": cores, "kind": "port",
+            "finite": bool(np.isfinite(out).all()),
             "sample": f"CPU restatement, not the reference's WGSL (no Deno / Vulkan ICD on the "
-                      f"box): oracle/oracle.c built with fp32 accumulation in the reference "
-                      f"kernels' loop order (liboracle_f32.so, gcc -O3 -fopenmp, {cores} "
-                      f"threads), run on down_blocks.0-1 of the same SD2.1 U-Net (4 ResNet + 4 "
-                      f"transformer blocks + downsampler, {w.total / 1e9:.1f} GFLOP) in "
-                      f"{sec:.1f} s, scaled by FLOPs to the {step / 1e9:.1f} GFLOP step"}
+                      f"box): one whole SD2.1 U-Net step ({step / 1e9:.1f} GFLOP, the headline's "
+                      f"weights and inputs) on oracle/oracle.c built with fp32 accumulation in "
+                      f"the reference kernels' loop order (liboracle_f32.so, gcc -O3 -fopenmp, "
+                      f"{cores} threads)"}
+
+
+def cpu_configs():
+    """The fp32 CPU restatement (liboracle_f32.so) on BASELINE cfg1-cfg4 at
+    full size, ms per call (one call each after a warm-up of cfg1)."""
+    import oracle
+    from oracle import unet_ref
+    rng = np.random.default_rng(7)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    out = {}
+    with oracle.accumulation("fp32"):
+        x = f(1, 320, 64, 64)
+        g, b = 1 + 0.02 * f(320), 0.02 * f(320)
+        oracle.group_norm(x, g, b, 32, eps=1e-5, silu=True)
+        t0 = time.perf_counter()
+        oracle.group_norm(x, g, b, 32, eps=1e-5, silu=True)
+        out["cfg1_gn_silu"] = (time.perf_counter() - t0) * 1e3
+        w = f(320, 320, 3, 3) * 0.026
+        t0 = time.perf_counter()
+        oracle.conv2d(x, w, 0.01 * f(320), stride=1, pad=1)
+        out["cfg2_conv3x3"] = (time.perf_counter() - t0) * 1e3
+        cfg = unet_ref.sd21_config()
+        sd = {k: (0.02 * rng.standard_normal(v)).astype(np.float32)
+              for k, v in unet_ref.unet_param_shapes(cfg).items()
+              if k.startswith("down_blocks.1.resnets.0.") or k.startswith("down_blocks.0.attentions.0.")}
+        ops = unet_ref.OracleOps()
+        t0 = time.perf_counter()
+        unet_ref.resnet(ops, sd, "down_blocks.1.resnets.0", f(1, 320, 32, 32), f(1, 1280))
+        out["cfg3_resnet"] = (time.perf_counter() - t0) * 1e3
+        t0 = time.perf_counter()
+        unet_ref.transformer(ops, sd, "down_blocks.0.attentions.0", x, f(1, 77, 1024))
+        out["cfg4_transformer"] = (time.perf_counter() - t0) * 1e3
+        cores = int(oracle.lib().or_threads())
+    return {"ms": {k: round(v, 2) for k, v in out.items()}, "cores": cores,
+            "kind": "port (fp32 CPU restatement, oracle/oracle.c -DOR_ACC=float)"}
 
 
 def pcie_inclusive(u, inputs, iters=5):
@@ -561,6 +583,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-blocks", action="store_true", help="skip the per-block figures")
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="also time the fp32 CPU restatement on cfg1-cfg4 (one call each)")
     ap.add_argument("--vae-only", action="store_true",
                     help="only the native VAE decode leg (for rocprofv3 kernel summaries)")
     ap.add_argument("--eager-only", type=int, default=0, metavar="K",
@@ -630,6 +654,8 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(u)
+    if args.cpu_configs:
+        line["cpu_configs"] = cpu_configs()
     if not args.no_blocks:
         blk = bench_blocks(dev)
         blk.update(bench_block_chains(dev, u))

@@ -238,6 +238,13 @@ def _conv_case(dev, rng, n, cin, cout, h, w, k, s, pad, up=1, res=False, cin_pad
     (1, 1280, 1280, 8, 8, 3, 1, 1, 2, False),   # Upsample2D conv (fused 2x nearest)
     (1, 2560, 1280, 8, 8, 3, 1, 1, 1, False),   # up0 resnet conv1 (8x8, split-K)
     (2, 64, 48, 7, 9, 3, 1, 1, 1, True),        # batch 2, ragged
+    # the halo kernel (k_conv3.hip): 2x upsample fused, channel-chunk split-K,
+    # batch 2, six chunks, a 256-wide image in 128-pixel row runs
+    (1, 640, 640, 16, 16, 3, 1, 1, 2, True),
+    (1, 1280, 1280, 16, 16, 3, 1, 1, 1, True),
+    (2, 320, 320, 32, 32, 3, 1, 1, 1, True),
+    (1, 384, 128, 64, 64, 3, 1, 1, 1, False),
+    (1, 320, 64, 256, 256, 3, 1, 1, 1, False),
     (1, 8, 320, 64, 64, 3, 1, 1, 1, False),     # conv_in (channels padded to 8)
     (1, 320, 8, 64, 64, 3, 1, 1, 1, False),     # conv_out (padded to 8)
 ])

@@ -56,6 +56,7 @@ def test_group_norm_nchw_f32(dev, N, C, H, W, G, eps, silu):
                      C // G, HW, eps, 1 if silu else 0, F32, NCHW)
     got = dev.download(y).reshape(N, C, H, W)
     ref = oracle.group_norm(xh.reshape(N, C, H, W), gh, bh, G, eps=eps, silu=silu)
+    print(f"   max-rel {max_rel(got, ref):.2e}", flush=True)
     assert max_rel(got, ref) <= 1e-4
     for t in (x, g, b, y):
         t.destroy()
