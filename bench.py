@@ -9,18 +9,20 @@ Prints ONE JSON line.  `value` = ms per step (lower is better), timed with
 HIP events on the library's stream over exactly K graph-replayed steps
 (bracketed by device synchronisation), inputs resident in HBM.
 
-* `roofline`: the dominant kernel, the implicit-GEMM MFMA conv (k_gemm) at
-  its most frequent U-Net shape, conv3x3 320->320 on 64x64 NHWC fp16 (seven
-  launches per step; also BASELINE cfg2), timed live with HIP events on the
-  stream it is launched on.  achieved = 2*HW*Cout*Cin*9 FLOP per launch /
-  average launch time; `traffic` = HBM bytes per launch from the committed
-  rocprofv3 FETCH_SIZE / WRITE_SIZE summary (null without it).
-* `cpu_baseline`: the repo's C restatement of the reference kernels (oracle/,
-  OpenMP, fp64 accumulation) running a bounded sample of the same step
-  (down_blocks.0-1 of the same U-Net, same weights) on the host cores,
-  scaled by FLOPs to ms per step.  Skipped with --no-cpu.
+* `roofline`: the dominant conv shape, conv3x3 320->320 on 64x64 NHWC fp16
+  (seven launches per step; also BASELINE cfg2), which the plan routes to the
+  halo conv kernel (k_conv3_halo), timed live with HIP events on the stream
+  it is launched on.  achieved = 2*HW*Cout*Cin*9 FLOP per launch / average
+  launch time; `traffic` = HBM bytes per launch from the committed rocprofv3
+  FETCH_SIZE / WRITE_SIZE summary (null without it).
+* `cpu_baseline`: one whole step of the repo's C restatement of the
+  reference kernels (oracle/, OpenMP, fp32 accumulation build) composed as
+  the same U-Net with the same weights, on the host cores.  Skipped with
+  --no-cpu.
 * `blocks` (unless --no-blocks): per-config figures (cfg1 GN+SiLU HBM GB/s,
-  cfg2 conv / cfg3 ResNet / cfg4 transformer / self-attention MFMA %).
+  cfg2 conv / cfg3 ResNet / cfg4 transformer / self-attention / GEGLU FFN
+  MFMA %).  `--blocks-only` prints just these (the leg the per-block
+  rocprofv3 counter passes run).
 * `denoise_loop`: the 4-step SD-Turbo loop (noise, scaleModelInput, U-Net,
   Euler update) entirely on the device, host wall time including the final
   wait.  `batch4`: the same step at B=4 (cfg5's other batch), ms per step
@@ -196,6 +198,22 @@ def bench_blocks(dev, num_rot=64):
     ms = timed(dev, att, 50)
     fl = 4.0 * 4096 * 4096 * 320
     res["self_attn_64x64"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+                              "mfma_frac": fl / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, "flops": fl}
+    # GEGLU FFN at 64x64 (down_blocks.0 transformer): 4096 x 320 -> 2x1280
+    # (GELU-gated) -> 320, plus the residual, two GEMM launches (di_ffn)
+    rows, D, F = 4096, 320, 1280
+    fx = dev.storage(rng.standard_normal((rows, D)).astype(np.float16))
+    w1 = dev.storage((rng.standard_normal((2 * F, D)) * 0.04).astype(np.float16))
+    b1 = dev.storage(np.zeros(2 * F, np.float32))
+    w2 = dev.storage((rng.standard_normal((D, F)) * 0.025).astype(np.float16))
+    b2 = dev.storage(np.zeros(D, np.float32))
+    fy = dev.create_buffer(rows * D * 2)
+    ffn = lambda i: call("di_ffn", dev.ctx, fx.handle, w1.handle, b1.handle, w2.handle, b2.handle,
+                         fy.handle, rows, D, F, 2, 1)
+    ffn(0)
+    ms = timed(dev, ffn, 50)
+    fl = 2.0 * rows * D * 2 * F + 2.0 * rows * F * D
+    res["ffn_geglu_64x64"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
                               "mfma_frac": fl / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, "flops": fl}
     return res
 
@@ -590,6 +608,9 @@ def main():
     ap.add_argument("--eager-only", type=int, default=0, metavar="K",
                     help="only K eager (non-graph) U-Net steps after the warm-up, for rocprofv3 "
                          "kernel summaries (with --vae-only: eager decodes)")
+    ap.add_argument("--blocks-only", action="store_true",
+                    help="only the per-block figures (cfg1 GN+SiLU, cfg2 conv, self-attention, "
+                         "GEGLU FFN), for rocprofv3 counter passes")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline kernel and a 256 MiB copy (for rocprofv3 --pmc runs "
                          "that calibrate FETCH_SIZE / WRITE_SIZE against a known byte count)")
@@ -612,6 +633,12 @@ def main():
         dev.sync()
         print(json.dumps({"roofline": rl, "calibration_read_bytes": n * 4,
                           "calibration_write_bytes": n * 4}), flush=True)
+        return
+    if args.blocks_only:
+        blk = bench_blocks(dev)
+        print(json.dumps({"blocks": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                         for kk, vv in v.items()} for k, v in blk.items()}}),
+              flush=True)
         return
     if args.vae_only:
         print(json.dumps({"vae_decode_512": bench_vae(dev, graph=not args.eager_only)}), flush=True)

@@ -18,18 +18,23 @@
 //    order {4g..4g+3, 16+4g..16+4g+3} per 32-key block.  V stays row-major in
 //    LDS; ds_read_b64_tr_b16 gathers the V^T A fragment in that key order.
 //
-// VALU and MFMA work of one SIMD do not overlap on gfx950 (measured), so the
-// softmax is kept to the minimum per score: one max (3-input), one exp2, one
-// add, half a convert.  The running max is raised only when some row's tile
-// max exceeds it by more than kRescale (p <= 2^kRescale in between), and the
-// row sums are reduced across the 4 lanes of a query once, at the end.
+// VALU and MFMA work of one SIMD overlap only partly on gfx950 (measured), so
+// the softmax is kept to the minimum per score: one exp2, one add, half a
+// convert.  The running max is taken from the first key tile only.  Later
+// tiles run against it unchanged while every probability stays <= 2^15
+// (fp16-safe): each lane checks the sum of its 16 probabilities against
+// kLaneSumMax, and only when some lane exceeds it (wave-uniform branch) is
+// the max raised to the tile's and the tile's probabilities recomputed.  Row
+// sums are reduced across the 4 lanes of a query once, at the end.
 //
 // Each workgroup (4 wavefronts = 64 queries) shares double-buffered K / V
 // tiles in LDS (XOR-swizzled 16-byte chunks, conflict-free for the K
 // fragment reads and the transposed V reads; 32 KiB per workgroup, four
-// resident per CU); the next tile is loaded into registers during the
-// MFMAs, by buffer loads whose descriptor ends at the head's last key.  Keys
-// past Skv (cross-attention's 77) read as zeros and are masked to -inf.
+// resident per CU).  The next tile goes straight from memory into LDS
+// (buffer_load ... lds, one 1 KiB row group per instruction, the swizzle
+// applied on the global side) during the MFMAs, by buffer loads whose
+// descriptor ends at the head's last key: keys past Skv (cross-attention's
+// 77) land as zeros and are masked to -inf.
 //
 // KV split: a wave of 16 queries that walks all keys is the smallest unit of
 // work, and 64x64-latent self-attention has 1280 of them for 1024 SIMDs, so
@@ -55,10 +60,13 @@ constexpr int D = 64;              // head dim
 constexpr int BKV = 64;            // keys per tile
 constexpr int K_BYTES = BKV * D * 2;      // 128-byte rows, XOR-swizzled 16-byte chunks
 constexpr int BUF_BYTES = 2 * K_BYTES;    // K tile, then V tile
-constexpr float kRescale = 8.0f;   // log2 units
+// a lane's 16 probabilities of one tile sum to at most this without a
+// rescale, so none exceeds it either (fp16 max is 65504)
+constexpr float kLaneSumMax = 32768.0f;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int N>
 using Int = std::integral_constant<int, N>;
@@ -82,6 +90,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 __device__ __forceinline__ f16x8 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt at their maxima: not waited on)
+constexpr int kWaitVm0 = (7 << 4) | (15 << 8);
 
 // lanes l, l^16, l^32, l^48 hold the same query
 __device__ __forceinline__ float max_q4(float x) {
@@ -127,37 +138,35 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
     for (int j = 0; j < 8; j++) qf[ks][j] = (f16)((float)t[j] * a.scale_log2);
   }
 
-  // K / V tile loads: thread tid moves 16-byte chunk tid%8 of rows tid/8 and
-  // tid/8 + 32.  The buffer descriptor of tile t starts at key 64t and ends
-  // after the head's last key, so rows past Skv read as zeros.
-  const uint32_t ld_row = tid >> 3, ld_c = tid & 7;
-  const uint32_t kvo0 = ld_row * (uint32_t)a.ldk * 2u + ld_c * 16u;
-  const uint32_t kvo1 = (ld_row + 32) * (uint32_t)a.ldk * 2u + ld_c * 16u;
-  const uint32_t vvo0 = ld_row * (uint32_t)a.ldv * 2u + ld_c * 16u;
-  const uint32_t vvo1 = (ld_row + 32) * (uint32_t)a.ldv * 2u + ld_c * 16u;
-  const uint32_t k_st = k_off(ld_row, ld_c), v_st = v_off(ld_row, ld_c);
-  f16x8 rk[2], rv[2];
-  auto load_kv = [&](int t) {
+  // K / V tiles straight into LDS: wave w moves rows 16w .. 16w+15 of each,
+  // 8 rows (1 KiB) per instruction; lane l lands at row + l/8, chunk slot l%8,
+  // so it fetches the global chunk (l%8) XOR swizzle(row).  The buffer
+  // descriptor of tile t starts at key 64t and ends after the head's last
+  // key, so rows past Skv land as zeros.
+  uint32_t dk[2], dv[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const uint32_t row = wave * 16 + i * 8 + (lane >> 3), lc = lane & 7;
+    dk[i] = row * (uint32_t)a.ldk * 2u + ((lc ^ ((row >> 1) & 7u)) << 4);
+    dv[i] = row * (uint32_t)a.ldv * 2u + ((lc ^ (row & 7u)) << 4);
+  }
+  auto dma_kv = [&](int t, auto buf_c) {
     const uint32_t key0 = (uint32_t)t * BKV, left = a.Skv - key0;
     const __amdgpu_buffer_rsrc_t rK =
         make_rsrc(K + (uint64_t)key0 * a.ldk, (left - 1) * (uint32_t)a.ldk * 2u + D * 2);
     const __amdgpu_buffer_rsrc_t rV =
         make_rsrc(V + (uint64_t)key0 * a.ldv, (left - 1) * (uint32_t)a.ldv * 2u + D * 2);
-    rk[0] = buf_load16(rK, kvo0);
-    rk[1] = buf_load16(rK, kvo1);
-    rv[0] = buf_load16(rV, vvo0);
-    rv[1] = buf_load16(rV, vvo1);
-  };
-  auto store_kv = [&](auto buf_c) {
-    unsigned char* base = smem + decltype(buf_c)::value * BUF_BYTES;
-    // rows +32 keep the XOR pattern of rows 0..31
-    *(f16x8*)(base + k_st) = rk[0];
-    *(f16x8*)(base + k_st + 32 * 128) = rk[1];
-    *(f16x8*)(base + K_BYTES + v_st) = rv[0];
-    *(f16x8*)(base + K_BYTES + v_st + 32 * 128) = rv[1];
+    unsigned char* base = smem + decltype(buf_c)::value * BUF_BYTES + wave * 16 * 128;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr)(base + i * 8 * 128), 16, dk[i], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr)(base + K_BYTES + i * 8 * 128), 16,
+                                               dv[i], 0, 0, 0);
+    }
   };
 
   float m = 0.0f, l = 0.0f;  // running max (log2 units) and this lane's partial row sum
+  f32x4 negm = {0.f, 0.f, 0.f, 0.f};  // -m: the score MFMAs' accumulator start
   f32x4 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -181,17 +190,15 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
   auto tile = [&](auto cur_c, int t) {
     constexpr int cur = decltype(cur_c)::value;
     const unsigned char* sb = smem + cur * BUF_BYTES;
-    const bool more = t + 1 < t1;
-    if (more) load_kv(t + 1);
+    if (t + 1 < t1) dma_kv(t + 1, Int<cur ^ 1>{});
 
     // S' = K Q'^T - m
-    const f32x4 cinit = {-m, -m, -m, -m};
     f32x4 s[4];
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
       const f16x8 k0 = *(const f16x8*)(sb + k_rd0 + kt * 2048);
       const f16x8 k1 = *(const f16x8*)(sb + k_rd1 + kt * 2048);
-      s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qf[0], cinit, 0, 0, 0);
+      s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qf[0], negm, 0, 0, 0);
       s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qf[1], s[kt], 0, 0, 0);
     }
     if ((uint32_t)(t + 1) * BKV > a.Skv) {
@@ -201,33 +208,46 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
         for (int i = 0; i < 4; i++)
           if ((uint32_t)(t * BKV + kt * 16 + 4 * g + i) >= a.Skv) s[kt][i] = -INFINITY;
     }
-    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+    // raise the running max by this tile's excess over it (>= 0 after the
+    // first tile; on the first, o and l are still zero)
+    auto raise_max = [&](bool first) {
+      float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
 #pragma unroll
-    for (int kt = 1; kt < 4; kt++)
-      mx = fmaxf(fmaxf(mx, fmaxf(s[kt][0], s[kt][1])), fmaxf(s[kt][2], s[kt][3]));
-    mx = max_q4(mx);
-    // raise the running max on the first tile, or when a row's scores exceed
-    // it by more than kRescale (wave-uniform branch)
-    if (t == t0 || __builtin_amdgcn_ballot_w64(mx > kRescale) != 0) {
-      const float dl = t == t0 ? mx : fmaxf(mx, 0.0f);
+      for (int kt = 1; kt < 4; kt++)
+        mx = fmaxf(fmaxf(mx, fmaxf(s[kt][0], s[kt][1])), fmaxf(s[kt][2], s[kt][3]));
+      mx = max_q4(mx);
+      const float dl = first ? mx : fmaxf(mx, 0.0f);
       m += dl;
+      negm -= dl;
 #pragma unroll
       for (int kt = 0; kt < 4; kt++) s[kt] -= dl;
-      // dl >= 0 after the first tile; on the first, o and l are still zero
-      const float alpha = t == t0 ? 0.0f : __builtin_amdgcn_exp2f(-dl);
+      const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(-dl);
       l *= alpha;
 #pragma unroll
       for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
-    }
+    };
+    if (t == t0) raise_max(true);
     f16x8 pf[2];
+    float ts;
+    auto probs = [&]() {
+      ts = 0.0f;
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++)
+      for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float p = __builtin_amdgcn_exp2f(s[kt][i]);
-        l += p;
-        pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
-      }
+        for (int i = 0; i < 4; i++) {
+          const float p = __builtin_amdgcn_exp2f(s[kt][i]);
+          ts += p;
+          pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
+        }
+    };
+    probs();
+    // a probability above kLaneSumMax (or inf / NaN from an overflowing
+    // score) shows in its lane's sum: rescale and redo the tile
+    if (__builtin_amdgcn_ballot_w64(!(ts <= kLaneSumMax)) != 0) {
+      raise_max(false);
+      probs();
+    }
+    l += ts;
     // O^T += V^T P^T over two 32-key k steps
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
@@ -240,12 +260,13 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[ks], o[dt], 0, 0, 0);
       }
     }
-    if (more) store_kv(Int<cur ^ 1>{});
+    // the next tile has landed in LDS (vmcnt 0), every wave is done with this one
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
   };
 
-  load_kv(t0);
-  store_kv(Int<0>{});
+  dma_kv(t0, Int<0>{});
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
   // two tiles per iteration so each LDS buffer has fixed offsets
   for (int t = t0; t < t1; t += 2) {

@@ -200,6 +200,100 @@ __global__ __launch_bounds__(256) void k_gn_nchw_apply(const T* __restrict__ x,
   }
 }
 
+// Single-launch NCHW GroupNorm for groups of up to 16 x 1024 vectors:
+// workgroup w of S per group reads the WHOLE group (one round of U vector
+// loads per thread, all in flight at once), reduces (sum, sumsq) in a fixed
+// order - so the S workgroups of a group derive bit-identical statistics -
+// then normalises its own slice [s*chunk, min((s+1)*chunk, L)), re-read from
+// the cache.  No workspace and no inter-workgroup communication: the extra
+// reads replace the partials pass.  Workgroups are numbered so that the S
+// slices of a group run on one XCD (blocks are dealt round-robin over the 8
+// XCDs), where every read after the first hits that XCD's L2.
+constexpr int kFusedT = 1024;
+
+template <typename T, int VEC, int U>
+__global__ __launch_bounds__(kFusedT) void k_gn_nchw_fused(
+    const T* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    T* __restrict__ y, uint32_t G, uint32_t cpg, uint32_t HW, uint32_t S, uint32_t chunk,
+    float eps, int silu) {
+  __shared__ float sh[2 * (kFusedT / kWave)];
+  __shared__ float s_mean, s_rstd;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t NT = gridDim.x, bid = blockIdx.x, xcd = bid & 7u, idx = bid >> 3;
+  const uint32_t per = NT >> 3, extra = NT & 7u;
+  const uint32_t w = xcd < extra ? xcd * (per + 1) + idx : extra * (per + 1) + (xcd - extra) * per + idx;
+  const uint32_t ng = w / S, s = w % S;
+  const uint32_t L = cpg * HW;
+  const uint64_t gbase = (uint64_t)ng * L;
+  float v[U][VEC];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t e = (u * kFusedT + tid) * VEC;
+    load_vec<T, VEC>(x + gbase + (e < L ? e : 0), v[u]);
+  }
+  sched_fence();
+  float ts = 0.0f, tq = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const bool ok = (u * kFusedT + tid) * VEC < L;
+#pragma unroll
+    for (int j = 0; j < VEC; j++) {
+      const float f = ok ? v[u][j] : 0.0f;
+      ts += f;
+      tq += f * f;
+    }
+  }
+  ts = wave_sum(ts);
+  tq = wave_sum(tq);
+  const uint32_t wv = tid / kWave;
+  if (tid % kWave == 0) {
+    sh[wv] = ts;
+    sh[kFusedT / kWave + wv] = tq;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float a = 0.0f, b = 0.0f;
+    for (int i = 0; i < kFusedT / kWave; i++) {
+      a += sh[i];
+      b += sh[kFusedT / kWave + i];
+    }
+    const float mean = a / (float)L;
+    const float var = fmaxf(b / (float)L - mean * mean, 0.0f);
+    s_mean = mean;
+    s_rstd = 1.0f / sqrtf(var + eps);
+  }
+  __syncthreads();
+  const float mean = s_mean, rstd = s_rstd;
+  const uint32_t c0 = (ng % G) * cpg;
+  const uint32_t lo = s * chunk, hi = min(lo + chunk, L);
+  for (uint32_t b = lo; b < hi; b += kFusedT * VEC * 2) {
+    float t[2][VEC], gm[2], bt[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      uint32_t e = b + (u * kFusedT + tid) * VEC;
+      e = e < hi ? e : lo;
+      load_vec<T, VEC>(x + gbase + e, t[u]);
+      gm[u] = gamma[c0 + e / HW];
+      bt[u] = beta[c0 + e / HW];
+    }
+    sched_fence();
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const uint32_t e = b + (u * kFusedT + tid) * VEC;
+      if (e < hi) {
+        const float a = rstd * gm[u], sb = bt[u] - mean * a;
+        float o[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+          const float z = t[u][j] * a + sb;
+          o[j] = silu ? silu_f(z) : z;
+        }
+        store_vec<T, VEC>(y + gbase + e, o);
+      }
+    }
+  }
+}
+
 // ---------------- NHWC fp16 (U-Net path) ----------------
 // Thread layout for a row of C channels: CV = C/8 vectors of 8 halfs;
 // cvb = min(CV, 256) threads across the row, R = 256/cvb pixel lanes, and
@@ -778,6 +872,60 @@ int gn_nchw_launch(Ctx* c, const void* x, const float* gamma, const float* beta,
   return DI_OK;
 }
 
+// Slices per group for the single-launch kernel (0: use the two-kernel
+// path): the grid should cover the CUs, and every slice re-reads its whole
+// group, so no more slices than that.  Groups of more than 64 Ki elements
+// (64 floats in registers per thread) or of less than one round of 1024
+// vectors (most of a 1024-thread workgroup idle), and fewer than 8 groups
+// (too few workgroups whichever way), take the two-kernel path.
+uint32_t gn_fused_slices(uint32_t NG, uint32_t L, uint32_t vec) {
+  static const int env = [] {
+    const char* e = getenv("DI_GN_FUSED");
+    return e ? atoi(e) : 1;
+  }();
+  if (!env || NG < 8 || L > 64u * kFusedT || L < kFusedT * vec || NG > (1u << 20)) return 0;
+  static const uint32_t env_s = [] {  // tuning override: DI_GN_SLICES=n
+    const char* e = getenv("DI_GN_SLICES");
+    return e ? (uint32_t)atoi(e) : 0u;
+  }();
+  uint32_t S = env_s ? env_s : 256 / NG;
+  if (S < 1) S = 1;
+  if (S > 16) S = 16;
+  const uint32_t smax = (L + kFusedT * vec - 1) / (kFusedT * vec);  // at least a round each
+  return S < smax ? S : smax;
+}
+
+template <typename T, int VEC, int U>
+void gn_fused_launch(hipStream_t st, const T* x, const float* gamma, const float* beta, T* y,
+                     uint32_t NG, uint32_t G, uint32_t cpg, uint32_t HW, uint32_t S, float eps,
+                     bool silu) {
+  const uint32_t L = cpg * HW;
+  uint32_t chunk = (L + S - 1) / S;
+  chunk = (chunk + VEC - 1) / VEC * VEC;
+  const uint32_t Sr = (L + chunk - 1) / chunk;  // non-empty slices
+  k_gn_nchw_fused<T, VEC, U><<<NG * Sr, kFusedT, 0, st>>>(x, gamma, beta, y, G, cpg, HW, Sr,
+                                                           chunk, eps, silu ? 1 : 0);
+}
+
+template <typename T, int VEC>
+void gn_fused(hipStream_t st, const T* x, const float* gamma, const float* beta, T* y,
+              uint32_t NG, uint32_t G, uint32_t cpg, uint32_t HW, uint32_t S, float eps,
+              bool silu) {
+  const uint32_t rounds = (cpg * HW + kFusedT * VEC - 1) / (kFusedT * VEC);
+#define DI_GN_FUSED_U(u) \
+  gn_fused_launch<T, VEC, u>(st, x, gamma, beta, y, NG, G, cpg, HW, S, eps, silu)
+  if (rounds <= 1) DI_GN_FUSED_U(1);
+  else if (rounds <= 2) DI_GN_FUSED_U(2);
+  else if (rounds <= 3) DI_GN_FUSED_U(3);
+  else if (rounds <= 4) DI_GN_FUSED_U(4);
+  else if (rounds <= 6) DI_GN_FUSED_U(6);
+  else if (rounds <= 8) DI_GN_FUSED_U(8);
+  else if (VEC <= 4 && rounds <= 10) DI_GN_FUSED_U(VEC <= 4 ? 10 : 1);
+  else if (VEC <= 4 && rounds <= 12) DI_GN_FUSED_U(VEC <= 4 ? 12 : 1);
+  else DI_GN_FUSED_U(VEC <= 4 ? 16 : 1);
+#undef DI_GN_FUSED_U
+}
+
 template <typename T>
 int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* y, uint32_t N,
             uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu, float* fixed,
@@ -787,6 +935,14 @@ int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* 
   DI_REQUIRE((uint64_t)cpg * HW < (1ull << 31), DI_EUNSUPPORTED,
              "group norm: %llu elements per group exceed 2^31", (unsigned long long)cpg * HW);
   constexpr int V = 16 / sizeof(T);
+  if (HW % V == 0) {
+    const uint32_t S = gn_fused_slices(N * G, cpg * HW, V);
+    if (S) {
+      gn_fused<T, V>(c->stream, (const T*)x, gamma, beta, (T*)y, N * G, G, cpg, HW, S, eps,
+                     silu);
+      return DI_OK;
+    }
+  }
   if (HW % V == 0)
     return gn_nchw_launch<T, V>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, fixed,
                                 fixed_bytes);

@@ -24,11 +24,14 @@ def _call(dev, fn, *a):
     drawinstant.call(fn, dev.ctx, *a)
 
 
-def _attn_case(dev, rng, B, H, Sq, Skv, layout, dt, fn, scale=0.0):
+def _attn_case(dev, rng, B, H, Sq, Skv, layout, dt, fn, scale=0.0, qkv=None):
     shp = (lambda s: (B, s, H, 64)) if layout == BSHD else (lambda s: (B, H, s, 64))
-    q = rng.standard_normal(shp(Sq)).astype(np.float16)
-    k = rng.standard_normal(shp(Skv)).astype(np.float16)
-    v = rng.standard_normal(shp(Skv)).astype(np.float16)
+    if qkv is None:
+        q = rng.standard_normal(shp(Sq)).astype(np.float16)
+        k = rng.standard_normal(shp(Skv)).astype(np.float16)
+        v = rng.standard_normal(shp(Skv)).astype(np.float16)
+    else:
+        q, k, v = (a.astype(np.float16) for a in qkv)
     npdt = np.float16 if dt == F16 else np.float32
     bq, bk, bv = (dev.storage(a.astype(npdt)) for a in (q, k, v))
     o = dev.create_buffer(q.size * (2 if dt == F16 else 4))
@@ -69,6 +72,24 @@ def test_attn_self_fp16(dev, rng, B, H, S, layout):
 def test_attn_cross_fp16(dev, rng, B, H, Sq, Skv, layout):
     print(f"[attn cross] B={B} H={H} Sq={Sq} Skv={Skv}", flush=True)
     assert _attn_case(dev, rng, B, H, Sq, Skv, layout, F16, "di_attn_cross") <= 2e-3
+
+
+@pytest.mark.parametrize("B,H,Sq,Skv,growth", [
+    (1, 2, 256, 4096, 6.0),   # one key range: the max rises over 64 tiles
+    (1, 3, 130, 2113, 4.0),   # key-range split, ragged last tile
+    (2, 2, 64, 77, 12.0),     # cross-attention length, steep rise within two tiles
+])
+def test_attn_rising_scores_fp16(dev, rng, B, H, Sq, Skv, growth):
+    """Key norms grow along the sequence (x1 -> x(1+growth)), so later key
+    tiles hold scores up to ~20 log2 units above the first tile's max: the
+    kernel's running max must be raised mid-range (the lane-sum overflow
+    check and the tile redo) without losing the earlier tiles' weight."""
+    print(f"[attn rising] B={B} H={H} Sq={Sq} Skv={Skv} growth={growth}", flush=True)
+    q = rng.standard_normal((B, Sq, H, 64))
+    ramp = 1.0 + growth * (np.arange(Skv) / max(1, Skv - 1))
+    k = rng.standard_normal((B, Skv, H, 64)) * ramp[None, :, None, None]
+    v = rng.standard_normal((B, Skv, H, 64))
+    assert _attn_case(dev, rng, B, H, Sq, Skv, BSHD, F16, "di_attn_cross", qkv=(q, k, v)) <= 2e-3
 
 
 def test_attn_fp32_tensors_and_explicit_scale(dev, rng):

@@ -45,6 +45,8 @@ def _gn_inputs(dev, N, C, HW, seed, dt=F32):
     (1, 128, 128, 128, 32, 1e-5, True),   # many slices per group
     (1, 32, 768, 768, 32, 1e-5, False),   # 256 slices, several rounds per thread
     (16, 512, 4, 4, 512, 1e-5, False),    # 8192 groups of 16 elements
+    (2, 320, 32, 32, 32, 1e-5, True),     # single launch, 4 slices per group
+    (1, 64, 40, 40, 8, 1e-5, True),       # single launch, slices end inside a round
 ])
 def test_group_norm_nchw_f32(dev, N, C, H, W, G, eps, silu):
     import drawinstant
