@@ -223,7 +223,11 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
   // of stage s + NBB - 1 into the buffer stage s - 1 used; loads retire in
   // order, so leaving the last three iterations' loads outstanding completes
   // the weights of stage s + 2 (issued at s - 3) and every patch piece
-  // issued up to s - 3 ----
+  // issued up to s - 3.  The barrier does not wait for the fragment reads of
+  // stage s + 1 (the compiler's waits before their MFMAs do, one iteration
+  // later): a weight buffer is refilled two iterations after its fragments
+  // were read, a patch buffer a whole chunk after, so no DMA overwrites a
+  // buffer with reads in flight ----
   static_assert(18 % CV_NBB == 0, "buffer index static over a round");
   int s0 = 0;
   for (; s0 + 18 <= n_stages; s0 += 18) {
@@ -237,7 +241,7 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
       dma_weights(s0 + j + CV_NBB - 1, (j + CV_NBB - 1) % CV_NBB);
 #pragma unroll
       for (int q = 0; q < G::pieces(tap); q++) dma_patch(c + 1, tap * G::PPT + q);
-      cv_wait<G::issued(j) + G::issued(j - 1) + G::issued(j - 2), 0>();
+      cv_wait<G::issued(j) + G::issued(j - 1) + G::issued(j - 2), 15>();
       __builtin_amdgcn_s_barrier();
     });
   }
@@ -252,7 +256,7 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
       mma(F[j & 1]);
       if constexpr (j + CV_NBB - 1 < 9)
         dma_weights(s0 + j + CV_NBB - 1, (j + CV_NBB - 1) % CV_NBB);
-      cv_wait<tc(j) + tc(j - 1) + tc(j - 2), 0>();
+      cv_wait<tc(j) + tc(j - 1) + tc(j - 2), 15>();
       __builtin_amdgcn_s_barrier();
     });
   }
