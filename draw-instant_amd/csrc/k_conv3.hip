@@ -18,13 +18,20 @@
 // Loads go global -> LDS directly (buffer_load ... lds: lane l of a wave
 // writes 16 bytes at base + 16 l), so the XOR chunk swizzle of the LDS rows
 // is applied on the global side: the lane that fills physical chunk p of row
-// r loads logical chunk p ^ ((r >> 1) & 7).  Six weight buffers, two patch
-// buffers; iteration s (stage s = chunk * 9 + tap) reads the MFMA fragments
-// of stage s + 1, runs the MFMAs of stage s, issues the weights of stage
-// s + 5 and, at the first taps, pieces of the next chunk's patch, then waits
-// until only the last three iterations' loads are outstanding (loads retire
-// in order) and meets the barrier: weights arriving from HBM get three
-// iterations.  Eight waves: four 32-row wave tiles x two k halves; the halves
+// r loads logical chunk p ^ (r & 7).  A fragment read covers 16 consecutive
+// rows from any start row (the tap shifts the patch rows by 0..2 + k * PW)
+// and 4 chunks; per-row XOR keeps that free of bank conflicts on gfx950
+// for every start row, where XOR by row pairs costs 1.33 extra LDS cycles
+// per read unless the start row is a multiple of 16 (measured with the
+// SQ_LDS_BANK_CONFLICT counter).  Six weight buffers, two patch buffers;
+// iteration s (stage s = chunk * 9 + tap) reads the MFMA fragments of stage
+// s + 1, runs the MFMAs of stage s, issues the weights of stage s + 5 and,
+// at the first taps, pieces of the next chunk's patch.  Every second
+// iteration waits until the loads the next two iterations read have landed
+// (loads retire in order) and for its own LDS reads, and meets the barrier:
+// one barrier per 16 MFMAs of a wave instead of per 8.  The schedule
+// (k_conv3_sched.h) is replayed on the host by a test.
+// Eight waves: four 32-row wave tiles x two k halves; the halves
 // are summed through LDS and the shared vector epilogue of the GEMM kernel
 // (bias, temb bias, residual, SiLU, GroupNorm statistics) writes the tile,
 // whose rows are contiguous output pixels.  With split-K (small spatial
@@ -33,6 +40,7 @@
 #include <type_traits>
 
 #include "di_kernels.h"
+#include "k_conv3_sched.h"
 #include "k_gemm_kernel.h"
 
 namespace di {
@@ -41,36 +49,7 @@ namespace {
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-constexpr int CV_BM = 128, CV_BN = 64, CV_NT = 512;
-constexpr int CV_ROW = 128;                    // bytes per LDS row (64 fp16 channels)
-constexpr int CV_BBUF = CV_BN * CV_ROW;        // one weight stage: 8 KB
-constexpr int CV_LDC = CV_BN + 4;              // fp32 C tile row stride
-
-constexpr int CV_NBB = 6;                      // weight stage buffers
-
-template <int W>
-struct ConvGeo {
-  static constexpr int R = CV_BM / W;          // output rows per tile
-  static constexpr int PW = W + 2;             // patch width
-  static constexpr int PR = (R + 2) * PW;      // patch rows (pixels)
-  static constexpr int NP = (PR + 63) / 64;    // patch pieces: one 8-row DMA per wave each
-  static constexpr int PROWS = NP * 64;        // patch rows allocated
-  // pieces per tap: one at taps 0..NP-1, or two at taps 0..3 when NP > 5, so
-  // the last piece is issued by tap 4 (and lands by the end of tap 7)
-  static constexpr int PPT = NP > 5 ? 2 : 1;
-  static constexpr int SMEM_PIPE = 2 * PROWS * CV_ROW + CV_NBB * CV_BBUF;
-  static constexpr int SMEM_C = CV_BM * CV_LDC * 4;
-  static constexpr int SMEM = SMEM_PIPE > SMEM_C ? SMEM_PIPE : SMEM_C;
-  static_assert(NP <= 8 && (NP + PPT - 1) / PPT <= 5, "patch pieces issued by tap 4");
-  static_assert(SMEM <= 160 * 1024, "LDS");
-  // patch pieces issued at tap t, and the vector-memory instructions a wave
-  // issues in a steady-state iteration at tap t (the weights of one stage
-  // plus those pieces)
-  static constexpr int pieces(int t) {
-    return t * PPT >= NP ? 0 : (NP - t * PPT < PPT ? NP - t * PPT : PPT);
-  }
-  static constexpr int issued(int t) { return 1 + pieces(((t % 9) + 9) % 9); }
-};
+using namespace conv3;
 
 // s_waitcnt with vmcnt = VM and lgkmcnt = LG (expcnt not waited on)
 template <int VM, int LG>
@@ -128,13 +107,13 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
       const_cast<void*>(g.b), (short)0, (int)g.b_bytes, 0x00020000);
 
   char* const patch = smem;                                 // [2][PROWS][128 B]
-  char* const wbuf = smem + 2 * G::PROWS * CV_ROW;          // [CV_NBB][64][128 B]
+  char* const wbuf = smem + 2 * G::PROWS * CV_ROW;          // [G::NBB][64][128 B]
 
   // ---- this lane's DMA slots ----
   const int lrow = lane >> 3, lpos = lane & 7;
   // weights: row n0 + wave * 8 + lrow, logical chunk lpos ^ swizzle
   const int brow = wave * 8 + lrow;
-  const uint32_t fb = (n0 + brow) * (uint32_t)g.ldb * 2u + (uint32_t)(lpos ^ ((brow >> 1) & 7)) * 16u;
+  const uint32_t fb = (n0 + brow) * (uint32_t)g.ldb * 2u + (uint32_t)(lpos ^ (brow & 7)) * 16u;
   // patch pieces: patch row i * 64 + wave * 8 + lrow
   uint32_t ppix[G::NP], pchk[G::NP];
 #pragma unroll
@@ -143,14 +122,19 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
     const int iy = (int)y0 - 1 + r / G::PW, ix = (int)x0 - 1 + r % G::PW;
     const bool ok = r < G::PR && iy >= 0 && iy < (int)g.Ho && ix >= 0 && ix < (int)g.Wo;
     ppix[i] = ok ? (img * g.H + ((uint32_t)iy >> ush)) * g.W + ((uint32_t)ix >> ush) : kInv;
-    pchk[i] = (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+    pchk[i] = (uint32_t)(lpos ^ (r & 7)) * 16u;
   }
-  // stage s = local chunk * 9 + tap; chunks below are global
+  // stage s = local chunk * 9 + tap; chunks below are global.  Stages past
+  // the split (issued by the last iterations, never read) and the chunk
+  // after its last get an out-of-range per-lane offset (kInv, checked
+  // against the buffer's range; fb < 2 GiB): their DMAs write zeros without
+  // touching memory and still count as loads for the waits
   auto dma_weights = [&](int stage, int buf) {
+    const bool live = stage < n_stages;
     const uint32_t c = (uint32_t)(cb0 + stage / 9), t = (uint32_t)stage % 9u;
-    const uint32_t koff = (t * g.Cin + c * 64u) * 2u;  // uniform
+    const uint32_t koff = live ? (t * g.Cin + c * 64u) * 2u : 0u;  // uniform
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr)(wbuf + buf * CV_BBUF + wave * 8 * CV_ROW),
-                                             16, fb, koff, 0, 0);
+                                             16, live ? fb : kInv, koff, 0, 0);
   };
   auto dma_patch = [&](int chunk, int piece) {
     const uint32_t cb = (uint32_t)chunk * 64u;
@@ -158,7 +142,7 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
     const uint32_t ld2 = (uint32_t)(s2 ? g.lda2 : g.lda) * 2u;
     const uint32_t ch2 = (s2 ? cb - g.c1 : cb) * 2u;
     const uint32_t p = ppix[piece];
-    const uint32_t off = p != kInv ? p * ld2 + ch2 + pchk[piece] : kInv;
+    const uint32_t off = p != kInv && chunk < cb0 + nch ? p * ld2 + ch2 + pchk[piece] : kInv;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         s2 ? rA2 : rA,
         (lds_ptr)(patch + (chunk & 1) * G::PROWS * CV_ROW + (piece * 64 + wave * 8) * CV_ROW), 16,
@@ -184,13 +168,13 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
 #pragma unroll
     for (int a = 0; a < 2; a++) {
       const int pr = pr0[a] + shift;
-      f.a[a] = *(const f16x8*)&pa[pr * 64 + ((cidx ^ ((pr >> 1) & 7)) * 8)];
+      f.a[a] = *(const f16x8*)&pa[pr * 64 + ((cidx ^ (pr & 7)) * 8)];
     }
     const f16* pb = (const f16*)(wbuf + buf * CV_BBUF);
 #pragma unroll
     for (int b = 0; b < 4; b++) {
       const int rr = b * 16 + fr;
-      f.b[b] = *(const f16x8*)&pb[rr * 64 + ((cidx ^ ((rr >> 1) & 7)) * 8)];
+      f.b[b] = *(const f16x8*)&pb[rr * 64 + ((cidx ^ (rr & 7)) * 8)];
     }
   };
   f32x4 acc[2][4];
@@ -211,8 +195,8 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < G::NP; i++) dma_patch(cb0, i);
 #pragma unroll
-  for (int b = 0; b + 1 < CV_NBB; b++) dma_weights(b, b);
-  cv_wait<0, 15>();
+  for (int b = 0; b + 1 < G::NBB; b++) dma_weights(b, b);
+  cv_wait<G::prologue_allow, 15>();
   __builtin_amdgcn_s_barrier();
   read_frags(cb0, 0, 0, F[0]);
   cv_wait<63, 0>();
@@ -220,15 +204,20 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
 
   // ---- steady state: two chunks (18 stages) per round, static tap,
   // weight-buffer and fragment-set indices.  Iteration s issues the weights
-  // of stage s + NBB - 1 into the buffer stage s - 1 used; loads retire in
-  // order, so leaving the last three iterations' loads outstanding completes
-  // the weights of stage s + 2 (issued at s - 3) and every patch piece
-  // issued up to s - 3.  The barrier does not wait for the fragment reads of
-  // stage s + 1 (the compiler's waits before their MFMAs do, one iteration
-  // later): a weight buffer is refilled two iterations after its fragments
-  // were read, a patch buffer a whole chunk after, so no DMA overwrites a
-  // buffer with reads in flight ----
-  static_assert(18 % CV_NBB == 0, "buffer index static over a round");
+  // of stage s + NBB - 1 into the buffer stage s - 1 used.  A barrier follows
+  // every BAR-th iteration.  At the barrier after iteration s, leaving the
+  // last SLACK iterations' loads outstanding (loads retire in order)
+  // completes everything issued up to s - SLACK: the weights of stages up to
+  // s + BAR + 1, which the next BAR iterations read, and the patch pieces
+  // of the next chunk (issued at its first five taps, read from its last
+  // tap on).  A weight buffer is refilled two iterations after its
+  // fragments were read, and one of those two iterations ends in a barrier
+  // (BAR <= 2) that waits for the wave's LDS reads (lgkmcnt 0); a patch
+  // buffer is refilled a whole chunk after.  So no DMA overwrites a buffer
+  // with reads in flight.  Near the end of the split the weights of stages
+  // past it are still issued (they read in-bounds weights or, past the
+  // buffer's range, zeros) and land in buffers no stage reads ----
+
   int s0 = 0;
   for (; s0 + 18 <= n_stages; s0 += 18) {
     const int c0 = cb0 + s0 / 9;
@@ -236,28 +225,32 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
       constexpr int j = decltype(jc)::value;
       constexpr int tap = j % 9;
       const int c = c0 + j / 9, cn = c0 + (j + 1) / 9;
-      read_frags(cn, (j + 1) % 9, (j + 1) % CV_NBB, F[(j + 1) & 1]);
+      read_frags(cn, (j + 1) % 9, (j + 1) % G::NBB, F[(j + 1) & 1]);
       mma(F[j & 1]);
-      dma_weights(s0 + j + CV_NBB - 1, (j + CV_NBB - 1) % CV_NBB);
+      dma_weights(s0 + j + G::NBB - 1, (j + G::NBB - 1) % G::NBB);
 #pragma unroll
       for (int q = 0; q < G::pieces(tap); q++) dma_patch(c + 1, tap * G::PPT + q);
-      cv_wait<G::issued(j) + G::issued(j - 1) + G::issued(j - 2), 15>();
-      __builtin_amdgcn_s_barrier();
+      if constexpr (j % G::BAR == G::BAR - 1) {
+        cv_wait<G::allow(j), 0>();
+        __builtin_amdgcn_s_barrier();
+      }
     });
   }
-  // ---- tail: an odd chunk count leaves the last chunk (9 stages); the two
-  // iterations before it issued one load each (taps 7 and 8) ----
+  // ---- tail: an odd chunk count leaves the last chunk (9 stages), entered
+  // right after a barrier; barriers after its odd iterations as above (the
+  // drain below follows the last) ----
   if (s0 < n_stages) {
     const int c = cb0 + s0 / 9;
     static_for<0, 9>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
-      constexpr auto tc = [](int i) { return i < 0 ? 1 : (i + CV_NBB - 1 < 9 ? 1 : 0); };
-      if constexpr (j + 1 < 9) read_frags(c, j + 1, (j + 1) % CV_NBB, F[(j + 1) & 1]);
+      if constexpr (j + 1 < 9) read_frags(c, j + 1, (j + 1) % G::NBB, F[(j + 1) & 1]);
       mma(F[j & 1]);
-      if constexpr (j + CV_NBB - 1 < 9)
-        dma_weights(s0 + j + CV_NBB - 1, (j + CV_NBB - 1) % CV_NBB);
-      cv_wait<tc(j) + tc(j - 1) + tc(j - 2), 15>();
-      __builtin_amdgcn_s_barrier();
+      if constexpr (j + G::NBB - 1 < 9)
+        dma_weights(s0 + j + G::NBB - 1, (j + G::NBB - 1) % G::NBB);
+      if constexpr (j % G::BAR == G::BAR - 1) {
+        cv_wait<G::tail_allow(j), 0>();
+        __builtin_amdgcn_s_barrier();
+      }
     });
   }
   // loads past the last stage may still be landing: drain before the C tile
