@@ -460,25 +460,7 @@ def bench_executor_vae(dev, reps=3):
 ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_conv3_halo_conv3x3_64x64x320_pmc.md")
 
 
-def sclk_levels():
-    """(max, current) shader clock in MHz from the first card's pp_dpm_sclk
-    table (the current level carries a '*'), or (None, None) where sysfs does
-    not expose it."""
-    import glob
-    import re
-    for f in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
-        try:
-            lines = open(f).read().splitlines()
-        except OSError:
-            continue
-        lv = [(int(m.group(1)), "*" in ln) for ln in lines
-              for m in [re.search(r"(\d+)\s*[Mm][Hh]z", ln)] if m]
-        if lv:
-            return max(v for v, _ in lv), next((v for v, cur in lv if cur), None)
-    return None, None
-
-
-def roofline_conv(dev, iters=50):
+def roofline_conv(dev, iters=200):
     """Live roofline of the dominant kernel at its U-Net shape."""
     from drawinstant import perf
     from drawinstant.device import call
@@ -489,14 +471,9 @@ def roofline_conv(dev, iters=50):
     y = dev.create_buffer(64 * 64 * 320 * 2)
     conv = lambda i: call("di_conv2d", dev.ctx, x.handle, w.handle, bias.handle, 0, y.handle, 1,
                           320, 320, 64, 64, 3, 1, 1, 0, 1, 1)
-    for i in range(3):
+    for i in range(20):
         conv(i)
     ms = timed(dev, conv, iters)
-    # shader clock sampled while ~10 ms of the same launches run
-    for i in range(400):
-        conv(i)
-    sclk_max, sclk_cur = sclk_levels()
-    dev.sync()
     fl = perf.conv_flops(1, 320, 320, 64, 64, 3)
     achieved = fl / (ms * 1e-3) / 1e12
     peak = perf.PEAK_FP16_FLOPS / 1e12
@@ -511,12 +488,7 @@ def roofline_conv(dev, iters=50):
                       "halo staged per channel chunk",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": traffic,
-            "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3),
-            # the published peak assumes 2.4 GHz; the same peak at the clock
-            # sampled under load, where sysfs exposes it
-            "sclk_mhz": {"max": sclk_max, "under_load": sclk_cur},
-            "frac_at_sclk": (round(achieved / (peak * sclk_cur / 2400.0), 4)
-                             if sclk_cur else None)}
+            "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3)}
 
 
 def cpu_baseline(u):
@@ -623,7 +595,7 @@ def main():
     from drawinstant import perf
     dev = drawinstant.Device(0)
     if args.roofline_only:
-        rl = roofline_conv(dev, iters=20)
+        rl = roofline_conv(dev)
         # calibration: a streaming kernel of known traffic (di_unary NEG over
         # 64 Mi floats reads 256 MiB and writes 256 MiB)
         from drawinstant.device import call
