@@ -226,13 +226,74 @@ __device__ __forceinline__ void epi_math8(const GemmArgs& g, float* x, const f32
 // GEMM's allocation.
 enum { EX_NONE = 0, EX_ROWSTATS = 1, EX_LNFOLD = 2 };
 
+// Barrier for hand-offs through LDS inside a workgroup: waits for the
+// wave's LDS operations only and meets the other waves, leaving global
+// loads in flight (__syncthreads also waits for those); the signal fences
+// keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt not waited on
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// The vector epilogue's operands (bias, temb bias, residual) for one batch
+// of up to 4 output vectors of a thread: vector v0 + u is 8 columns of one
+// row of the BM x BN tile.  A kernel loads the first batch with epi_prefetch
+// before it stages the C tile in LDS, so the loads' latency overlaps the
+// staging.
+template <int BM, int BN, int NT>
+struct EpiOps {
+  static constexpr int VPR8 = BN / 8;
+  static constexpr int NV = (BM * VPR8 + NT - 1) / NT;
+  static constexpr int CH = NV < 4 ? NV : 4;  // vectors per load batch
+  f32x4 bb[CH][2], tb[CH][2];
+  f16x8 rr[CH];
+};
+
+template <int BM, int BN, int NT>
+__device__ __forceinline__ void epi_load(const GemmArgs& g, uint32_t m0, uint32_t n0, uint32_t bz,
+                                         int v0, EpiOps<BM, BN, NT>& o) {
+  using O = EpiOps<BM, BN, NT>;
+  const int tid = threadIdx.x;
+  const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr;
+#pragma unroll
+  for (int u = 0; u < O::CH; u++) {
+    const int idx = tid + (v0 + u) * NT;
+    const int r = idx / O::VPR8, c8 = (idx % O::VPR8) * 8;
+    const uint32_t m = m0 + r, n = n0 + c8;
+    const bool ok = v0 + u < O::NV && idx < BM * O::VPR8 && m < g.M && n < g.N;
+    const uint32_t mc = ok ? m : m0, nc = ok ? n : n0;
+    if (g.bias) {
+      o.bb[u][0] = ld4(g.bias + nc);
+      o.bb[u][1] = ld4(g.bias + nc + 4);
+    }
+    if (g.bias2) {
+      const float* t = g.bias2 + (uint64_t)(mc / g.rows_b2) * g.ld_b2 + nc;
+      o.tb[u][0] = ld4(t);
+      o.tb[u][1] = ld4(t + 4);
+    }
+    if (g.res) o.rr[u] = *(const f16x8*)(R + (uint64_t)mc * g.ldr + nc);
+  }
+}
+
+// First-batch operands for gemm_epilogue_vec, or nothing when that
+// epilogue will not use them (split-K partials, GEGLU's own layout).
+template <int BM, int BN, int NT>
+__device__ __forceinline__ void epi_prefetch(const GemmArgs& g, uint32_t m0, uint32_t n0, uint32_t bz,
+                                             EpiOps<BM, BN, NT>& o) {
+  if (g.splits <= 1 && g.act != ACT_GEGLU) epi_load<BM, BN, NT>(g, m0, n0, bz, 0, o);
+}
+
 // Writes (GEGLU-combined when act == GEGLU) results for the rows/columns of
 // one C tile staged in LDS as fp32 sC[BM][LDC].  Split-K partials are
 // stored as fp32 vectors instead.  All operand loads of a batch of vectors
-// are issued before any is consumed.
+// are issued before any is consumed; `pre` holds the first batch's when the
+// kernel prefetched them (epi_prefetch with the same tile).
 template <int BM, int BN, int LDC, int NT, int EX>
 __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float* sC, uint32_t m0,
-                                                  uint32_t n0, uint32_t bz, uint32_t split) {
+                                                  uint32_t n0, uint32_t bz, uint32_t split,
+                                                  const EpiOps<BM, BN, NT>* pre = nullptr) {
   const int tid = threadIdx.x;
   if (g.splits > 1) {
     constexpr int VPR4 = BN / 4;
@@ -297,13 +358,16 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     }
     return;
   }
-  constexpr int VPR8 = BN / 8;
-  constexpr int NV = (BM * VPR8 + NT - 1) / NT;
-  constexpr int CH = NV < 4 ? NV : 4;  // vectors per load batch
+  using O = EpiOps<BM, BN, NT>;
+  constexpr int VPR8 = O::VPR8, NV = O::NV, CH = O::CH;
 #pragma unroll
   for (int v0 = 0; v0 < NV; v0 += CH) {
-    f32x4 bb[CH][2], tb[CH][2];
-    f16x8 rr[CH];
+    O ops;
+    if (v0 == 0 && pre) ops = *pre;
+    else epi_load<BM, BN, NT>(g, m0, n0, bz, v0, ops);
+    auto& bb = ops.bb;
+    auto& tb = ops.tb;
+    auto& rr = ops.rr;
     uint32_t mm[CH], nn[CH];
     bool okv[CH];
 #pragma unroll
@@ -313,30 +377,6 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
       mm[u] = m0 + r;
       nn[u] = n0 + c8;
       okv[u] = v0 + u < NV && idx < BM * VPR8 && mm[u] < g.M && nn[u] < g.N;
-    }
-    if (g.bias) {
-#pragma unroll
-      for (int u = 0; u < CH; u++) {
-        const uint32_t nc = okv[u] ? nn[u] : n0;
-        bb[u][0] = ld4(g.bias + nc);
-        bb[u][1] = ld4(g.bias + nc + 4);
-      }
-    }
-    if (g.bias2) {
-#pragma unroll
-      for (int u = 0; u < CH; u++) {
-        const uint32_t mc = okv[u] ? mm[u] : m0, nc = okv[u] ? nn[u] : n0;
-        const float* t = g.bias2 + (uint64_t)(mc / g.rows_b2) * g.ld_b2 + nc;
-        tb[u][0] = ld4(t);
-        tb[u][1] = ld4(t + 4);
-      }
-    }
-    if (g.res) {
-#pragma unroll
-      for (int u = 0; u < CH; u++) {
-        const uint32_t mc = okv[u] ? mm[u] : m0, nc = okv[u] ? nn[u] : n0;
-        rr[u] = *(const f16x8*)(R + (uint64_t)mc * g.ldr + nc);
-      }
     }
 #pragma unroll
     for (int u = 0; u < CH; u++) {
@@ -885,7 +925,10 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
       constexpr int LDC = BN + 4;
       static_assert(BM * LDC * 4 <= (int)sizeof(smem), "C tile fits the LDS allocation");
       float* sC = reinterpret_cast<float*>(smem);
-      __syncthreads();  // every wave is done reading the last stage
+      // bias / temb bias / residual loads in flight while the tile is staged
+      EpiOps<BM, BN, NT> pre;
+      epi_prefetch<BM, BN, NT>(g, m0, n0, bz, pre);
+      lds_barrier();  // every wave is done reading the last stage
       // LayerNorm fold (EX_LNFOLD, launched without split-K): the (mean,
       // rstd) of this thread's accumulator rows and ln_s of its columns
       float2 lmr[EX == EX_LNFOLD ? TM : 1][4];
@@ -917,11 +960,11 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
                 c = v;
               }
         }
-        __syncthreads();
+        lds_barrier();
       }
-      gemm_epilogue_vec<BM, BN, LDC, NT, EX>(g, sC, m0, n0, bz, split);
+      gemm_epilogue_vec<BM, BN, LDC, NT, EX>(g, sC, m0, n0, bz, split, &pre);
       if (g.stats && splits == 1) {
-        __syncthreads();
+        lds_barrier();
         gemm_tile_stats<BM, BN, LDC, NT>(g, sC, m0, n0);
       }
       return;
