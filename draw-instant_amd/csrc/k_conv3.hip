@@ -258,25 +258,20 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
   cv_wait<0, 0>();
   __syncthreads();
 
-  // ---- epilogue: k half 0 writes the fp32 C tile, half 1 adds ----
+  // ---- epilogue: the two k halves write their fp32 tiles side by side at
+  // once; the shared vector epilogue adds them as it reads ----
   float* sC = reinterpret_cast<float*>(smem);
+  float* const sCh = sC + kh * (CV_BM * CV_LDC);
   const int rq = (lane >> 4) * 4;
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
-    if (kh == h) {
+  for (int a = 0; a < 2; a++)
 #pragma unroll
-      for (int a = 0; a < 2; a++)
+    for (int b = 0; b < 4; b++)
 #pragma unroll
-        for (int b = 0; b < 4; b++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            float& cc = sC[(wm0 + a * 16 + rq + i) * CV_LDC + b * 16 + fr];
-            cc = h == 0 ? acc[a][b][i] : cc + acc[a][b][i];
-          }
-    }
-    __syncthreads();
-  }
-  gemm_epilogue_vec<CV_BM, CV_BN, CV_LDC, CV_NT, EX_NONE>(g, sC, m0, n0, 0, split);
+      for (int i = 0; i < 4; i++) sCh[(wm0 + a * 16 + rq + i) * CV_LDC + b * 16 + fr] = acc[a][b][i];
+  __syncthreads();
+  gemm_epilogue_vec<CV_BM, CV_BN, CV_LDC, CV_NT, EX_NONE>(g, sC, m0, n0, 0, split, nullptr,
+                                                          sC + CV_BM * CV_LDC);
   if (g.stats && g.splits == 1) {
     __syncthreads();
     gemm_tile_stats<CV_BM, CV_BN, CV_LDC, CV_NT>(g, sC, m0, n0);

@@ -44,7 +44,7 @@ struct ConvGeo {
   // iteration -m stands for the load of stage NBB-1-m
   static constexpr int prologue_allow = NBB - 4;
   static constexpr int SMEM_PIPE = 2 * PROWS * CV_ROW + NBB * CV_BBUF;
-  static constexpr int SMEM_C = CV_BM * CV_LDC * 4;
+  static constexpr int SMEM_C = 2 * CV_BM * CV_LDC * 4;  // the two k halves' fp32 tiles
   static constexpr int SMEM = SMEM_PIPE > SMEM_C ? SMEM_PIPE : SMEM_C;
   static_assert(NP <= 8 && last_tap <= 4, "patch pieces issued by tap 4");
   static_assert(SMEM <= 160 * 1024, "LDS");

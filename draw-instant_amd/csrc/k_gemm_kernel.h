@@ -286,15 +286,20 @@ __device__ __forceinline__ void epi_prefetch(const GemmArgs& g, uint32_t m0, uin
 }
 
 // Writes (GEGLU-combined when act == GEGLU) results for the rows/columns of
-// one C tile staged in LDS as fp32 sC[BM][LDC].  Split-K partials are
-// stored as fp32 vectors instead.  All operand loads of a batch of vectors
-// are issued before any is consumed; `pre` holds the first batch's when the
-// kernel prefetched them (epi_prefetch with the same tile).
+// one C tile staged in LDS as fp32 sC[BM][LDC] (plus sC2, a second partial
+// tile of the same layout, where a kernel stages its k halves separately).
+// Split-K partials are stored as fp32 vectors instead.  All operand loads of
+// a batch of vectors are issued before any is consumed; `pre` holds the
+// first batch's when the kernel prefetched them (epi_prefetch with the same
+// tile).
 template <int BM, int BN, int LDC, int NT, int EX>
 __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float* sC, uint32_t m0,
                                                   uint32_t n0, uint32_t bz, uint32_t split,
-                                                  const EpiOps<BM, BN, NT>* pre = nullptr) {
+                                                  const EpiOps<BM, BN, NT>* pre = nullptr,
+                                                  const float* sC2 = nullptr) {
   const int tid = threadIdx.x;
+  auto tile4 = [&](int i) { return sC2 ? ld4(&sC[i]) + ld4(&sC2[i]) : ld4(&sC[i]); };
+  auto tile1 = [&](int i) { return sC2 ? sC[i] + sC2[i] : sC[i]; };
   if (g.splits > 1) {
     constexpr int VPR4 = BN / 4;
     constexpr int NV = (BM * VPR4 + NT - 1) / NT;
@@ -305,7 +310,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
       if (idx < BM * VPR4) {
         const int r = idx / VPR4, c4 = (idx % VPR4) * 4;
         const uint32_t m = m0 + r, n = n0 + c4;
-        if (m < g.M && n < g.N) *(f32x4*)&P[(uint64_t)m * g.N + n] = ld4(&sC[r * LDC + c4]);
+        if (m < g.M && n < g.N) *(f32x4*)&P[(uint64_t)m * g.N + n] = tile4(r * LDC + c4);
       }
     }
     return;
@@ -338,8 +343,8 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
       float h[8], gt[8];
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        h[j] = sC[r * LDC + cl + j];
-        gt[j] = sC[r * LDC + cl + 16 + j];
+        h[j] = tile1(r * LDC + cl + j);
+        gt[j] = tile1(r * LDC + cl + 16 + j);
       }
       // bias only (no bias2 / activation on GEGLU projections)
 #pragma unroll
@@ -385,7 +390,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
       float rs = 0.0f, rq = 0.0f;
       if (okv[u]) {
         float x[8];
-        const f32x4 a0 = ld4(&sC[r * LDC + c8]), a1 = ld4(&sC[r * LDC + c8 + 4]);
+        const f32x4 a0 = tile4(r * LDC + c8), a1 = tile4(r * LDC + c8 + 4);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           x[j] = a0[j];
