@@ -270,8 +270,8 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 4; i++) sCh[(wm0 + a * 16 + rq + i) * CV_LDC + b * 16 + fr] = acc[a][b][i];
   __syncthreads();
-  gemm_epilogue_vec<CV_BM, CV_BN, CV_LDC, CV_NT, EX_NONE>(g, sC, m0, n0, 0, split, nullptr,
-                                                          sC + CV_BM * CV_LDC);
+  gemm_epilogue_vec<CV_BM, CV_BN, CV_LDC, CV_NT, EX_NONE, 2>(g, sC, m0, n0, 0, split, nullptr,
+                                                             CV_BM * CV_LDC);
   if (g.stats && g.splits == 1) {
     __syncthreads();
     gemm_tile_stats<CV_BM, CV_BN, CV_LDC, CV_NT>(g, sC, m0, n0);

@@ -286,20 +286,30 @@ __device__ __forceinline__ void epi_prefetch(const GemmArgs& g, uint32_t m0, uin
 }
 
 // Writes (GEGLU-combined when act == GEGLU) results for the rows/columns of
-// one C tile staged in LDS as fp32 sC[BM][LDC] (plus sC2, a second partial
-// tile of the same layout, where a kernel stages its k halves separately).
-// Split-K partials are stored as fp32 vectors instead.  All operand loads of
-// a batch of vectors are issued before any is consumed; `pre` holds the
-// first batch's when the kernel prefetched them (epi_prefetch with the same
-// tile).
-template <int BM, int BN, int LDC, int NT, int EX>
+// one C tile staged in LDS as fp32 sC[BM][LDC], or as the sum of NSUM
+// partial tiles of that layout tstride floats apart (added in tile order),
+// where a kernel stages its k parts separately.  Split-K partials are
+// stored as fp32 vectors instead.  All operand loads of a batch of vectors
+// are issued before any is consumed; `pre` holds the first batch's when the
+// kernel prefetched them (epi_prefetch with the same tile).
+template <int BM, int BN, int LDC, int NT, int EX, int NSUM = 1>
 __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float* sC, uint32_t m0,
                                                   uint32_t n0, uint32_t bz, uint32_t split,
                                                   const EpiOps<BM, BN, NT>* pre = nullptr,
-                                                  const float* sC2 = nullptr) {
+                                                  int tstride = 0) {
   const int tid = threadIdx.x;
-  auto tile4 = [&](int i) { return sC2 ? ld4(&sC[i]) + ld4(&sC2[i]) : ld4(&sC[i]); };
-  auto tile1 = [&](int i) { return sC2 ? sC[i] + sC2[i] : sC[i]; };
+  auto tile4 = [&](int i) {
+    f32x4 v = ld4(&sC[i]);
+#pragma unroll
+    for (int t = 1; t < NSUM; t++) v += ld4(&sC[i + t * tstride]);
+    return v;
+  };
+  auto tile1 = [&](int i) {
+    float v = sC[i];
+#pragma unroll
+    for (int t = 1; t < NSUM; t++) v += sC[i + t * tstride];
+    return v;
+  };
   if (g.splits > 1) {
     constexpr int VPR4 = BN / 4;
     constexpr int NV = (BM * VPR4 + NT - 1) / NT;
@@ -407,7 +417,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
           *(f32x4*)w = f32x4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
           *(f32x4*)(w + 4) = f32x4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
         }
-        if (EX == EX_ROWSTATS) {
+        if constexpr (EX == EX_ROWSTATS) {
 #pragma unroll
           for (int j = 0; j < 8; j++) {
             const float f = (float)o[j];
@@ -416,7 +426,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
           }
         }
       }
-      if (EX == EX_ROWSTATS) {
+      if constexpr (EX == EX_ROWSTATS) {
         // row statistics over the tile's columns: the VPR8 lanes holding
         // one row are consecutive (VPR8 divides the wavefront)
         static_assert(64 % VPR8 == 0 || BN == 160, "row groups inside a wavefront");
