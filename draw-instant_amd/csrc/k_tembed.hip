@@ -8,7 +8,13 @@
 // reduction), hundreds of workgroups per launch; the input vector (the
 // sinusoid of fused-tembed.js:39-42, computed in fp64, or SiLU of the
 // previous output) is staged per workgroup in LDS.  The same kernel computes
-// every ResNet's time_emb_proj(SiLU(temb)) of a U-Net step in one launch.
+// every ResNet's time_emb_proj(SiLU(temb)) of a U-Net step in one launch
+// (20,160 rows of 1280 fp16 weights at SD2.1: 51.6 MB, HBM-bound).  In the
+// vector path every lane issues all loads of its rows' weights before it
+// stages the input vector, each wavefront covers RPW rows, and the staged
+// vector takes B * K floats of LDS (not the B = 8 maximum), so enough
+// weight bytes are in flight to stream HBM instead of waiting on one
+// 16-byte load per lane at a time.
 #include "di_device.h"
 #include "di_kernels.h"
 #include "di_tembed.h"
@@ -94,11 +100,115 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs g) {
   }
 }
 
+// x' of the GEMV (sinusoid when SIN, else SiLU or plain) into xs[b * K + k]
+template <bool SIN>
+__device__ __forceinline__ void gemv_stage_x(const GemvArgs& g, float* xs) {
+  const uint32_t B = g.B, K = g.K;
+  for (uint32_t i = threadIdx.x; i < B * K; i += 256) {
+    const uint32_t b = i / K, k = i % K;
+    float v;
+    if constexpr (SIN) {
+      const uint32_t half = K / 2;
+      const uint32_t fi = k < half ? k : k - half;
+      const double freq = exp(-9.210340371976184 * (double)fi / (double)half);
+      const double arg = (double)g.t[b] * freq;
+      v = (float)(k < half ? cos(arg) : sin(arg));
+    } else {
+      v = g.x[(uint64_t)b * g.ldx + k];
+      if (g.x_mode == GEMV_X_SILU) v = silu_f(v);
+    }
+    xs[i] = v;
+  }
+}
+
+// Vector path (K % V == 0, K <= 64 * V * NV, B <= BMAX): wavefront w of workgroup i
+// owns rows (4 i + w) * RPW .. + RPW - 1; lane l holds vectors l, l + 64, ..
+// of each row.  Rows past N load row N - 1 (in range) and store nothing.
+template <typename W, int NV, int RPW, int BMAX, bool SIN>
+__global__ __launch_bounds__(256) void k_gemv_vec(GemvArgs g) {
+  extern __shared__ float xs[];  // [B][K]
+  using WV = typename WVec<W>::type;
+  constexpr int V = WVec<W>::V;
+  const int lane = threadIdx.x & 63;
+  const uint32_t n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  const uint32_t K = g.K, B = g.B;
+  WV wv[RPW][NV];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint32_t n = min(n0 + r, g.N - 1);
+    const W* wr = (const W*)g.w + (uint64_t)n * g.ldw;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const uint32_t k = (uint32_t)(lane + 64 * i) * V;
+      wv[r][i] = k < K ? *(const WV*)(wr + k) : WV{};
+    }
+  }
+  gemv_stage_x<SIN>(g, xs);
+  __syncthreads();
+  float acc[RPW][BMAX];
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int b = 0; b < BMAX; b++) acc[r][b] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const uint32_t k = (uint32_t)(lane + 64 * i) * V;
+    if (k < K) {
+#pragma unroll
+      for (int b = 0; b < BMAX; b++) {
+        if (b < (int)B) {
+          float x[V];
+#pragma unroll
+          for (int j = 0; j < V; j++) x[j] = xs[b * K + k + j];
+#pragma unroll
+          for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int j = 0; j < V; j++) acc[r][b] += (float)wv[r][i][j] * x[j];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint32_t n = n0 + r;
+#pragma unroll
+    for (int b = 0; b < BMAX; b++) {
+      if (b < (int)B) {
+        float s = wave_sum(acc[r][b]);
+        if (lane == 0 && n < g.N) {
+          s += g.bias ? g.bias[n] : 0.0f;
+          if (g.act == GEMV_ACT_SILU) s = silu_f(s);
+          g.y[(uint64_t)b * g.ldy + n] = s;
+        }
+      }
+    }
+  }
+}
+
+// Eight rows per wavefront for tall matrices at B <= 2 (the U-Net's stacked
+// time_emb_proj: 630 workgroups, resident at once), else one (1280-row
+// GEMVs keep 320 workgroups)
+template <typename W, int NV>
+void launch_gemv_vec(const GemvArgs& g, hipStream_t s) {
+  const size_t lds = (size_t)g.B * g.K * sizeof(float);
+  const bool sin = g.x_mode == GEMV_X_SINUSOID;
+  if (g.B <= 2 && !sin && g.N >= 8192)
+    k_gemv_vec<W, NV, 8, 2, false><<<(g.N + 31) / 32, 256, lds, s>>>(g);
+  else if (!sin) k_gemv_vec<W, NV, 1, kMaxB, false><<<(g.N + 3) / 4, 256, lds, s>>>(g);
+  else k_gemv_vec<W, NV, 1, kMaxB, true><<<(g.N + 3) / 4, 256, lds, s>>>(g);
+}
+
 }  // namespace
 
 int gemv_supported(uint32_t B, uint32_t K) { return B >= 1 && B <= kMaxB && K >= 1 && K <= kMaxK; }
 
 void launch_gemv(const GemvArgs& g, int wdt, hipStream_t s) {
+  if (g.vec_ok && g.N > 0) {
+    // K <= kMaxK = 1280: three 8-wide fp16 or five 4-wide fp32 vectors per lane
+    if (wdt == DI_F16) launch_gemv_vec<f16, 3>(g, s);
+    else launch_gemv_vec<float, 5>(g, s);
+    return;
+  }
   unsigned blocks = (g.N + 3) / 4;
   if (wdt == DI_F16) k_gemv<f16><<<blocks, 256, 0, s>>>(g);
   else k_gemv<float><<<blocks, 256, 0, s>>>(g);

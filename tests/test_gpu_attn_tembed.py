@@ -120,6 +120,33 @@ def test_tembed_fp32_reference_shape(dev, rng, t):
     assert max_rel(dev.download(y), oracle.tembed(t, w1, b1, w2, b2)) <= 1e-4
 
 
+@pytest.mark.parametrize("B,emb,hid,dt", [
+    (1, 1280, 1280, F16),  # K = 1280: the last vector slot of half the lanes is empty
+    (2, 96, 1000, F16),    # rows not a multiple of 4 per workgroup
+    (3, 320, 1280, F32),   # B > 2: one row per wavefront
+    (8, 64, 200, F32),     # the largest batch
+    (2, 100, 1277, F16),   # K % 8 != 0: the scalar path
+])
+def test_tembed_gemv_shapes(dev, rng, B, emb, hid, dt):
+    """Both GEMV paths (vector loads issued before the input is staged, and
+    the scalar fallback) across batch sizes, ragged row counts and K."""
+    ts = np.linspace(999.0, 0.0, B).astype(np.float32)
+    wt = np.float16 if dt == F16 else np.float32
+    w1 = (rng.standard_normal((hid, emb)) * math.sqrt(1 / emb)).astype(wt)
+    b1 = (0.01 * rng.standard_normal(hid)).astype(np.float32)
+    w2 = (rng.standard_normal((hid, hid)) * math.sqrt(1 / hid)).astype(wt)
+    b2 = (0.01 * rng.standard_normal(hid)).astype(np.float32)
+    y = dev.create_buffer(B * hid * 4)
+    _call(dev, "di_tembed", dev.storage(ts).handle, dev.storage(w1).handle, dev.storage(b1).handle,
+          dev.storage(w2).handle, dev.storage(b2).handle, y.handle, B, emb, hid, dt)
+    got = dev.download(y).reshape(B, hid)
+    for i, t in enumerate(ts):
+        ref = oracle.tembed(float(t), w1.astype(np.float32), b1, w2.astype(np.float32), b2)
+        err = max_rel(got[i], ref)
+        print(f"[tembed] B={B} emb={emb} hid={hid} dt={dt} t={t:.0f} max-rel {err:.2e}", flush=True)
+        assert err <= 1e-4
+
+
 def test_tembed_fp16_weights_batched(dev, rng):
     emb, hid, B = 320, 1280, 4
     ts = np.array([999.0, 750.0, 1.0, 0.0], np.float32)
