@@ -222,6 +222,18 @@ bool tuned_plan(const GemmArgs& g, GemmPlan* out) {
 }  // namespace
 
 GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
+  // DI_GEMM_PLAN="M,N,K,tile,splits;..." fixes the plan of the listed fp16
+  // shapes only (tuning runs of the whole step; tile 13 = the halo conv)
+  if (const char* env_plan = getenv("DI_GEMM_PLAN"); env_plan && elem == DI_F16) {
+    for (const char* p = env_plan; p && *p;) {
+      unsigned m, n, k, t, sp;
+      if (sscanf(p, "%u,%u,%u,%u,%u", &m, &n, &k, &t, &sp) == 5 && m == g.M && n == g.N &&
+          k == g.K && t < TILE_COUNT && t != TILE_128x160 && sp >= 1)
+        return GemmPlan{(int)t, sp};
+      p = strchr(p, ';');
+      if (p) p++;
+    }
+  }
   const char* env_tile = getenv("DI_GEMM_TILE");
   const char* env_split = getenv("DI_GEMM_SPLITS");
   GemmPlan best{TILE_64x64, 1};
@@ -246,18 +258,6 @@ GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
     if (hs >= 1 && nch % hs == 0) return GemmPlan{TILE_CONV3_HALO, hs};
   }
   if (elem == DI_F16 && tuned_plan(g, &best)) {
-    // DI_GEMM_PLAN="M,N,K,tile,splits;..." replaces the measured plan of the
-    // listed shapes only (tuning runs of the whole step)
-    if (const char* env_plan = getenv("DI_GEMM_PLAN")) {
-      for (const char* p = env_plan; p && *p;) {
-        unsigned m, n, k, t, sp;
-        if (sscanf(p, "%u,%u,%u,%u,%u", &m, &n, &k, &t, &sp) == 5 && m == g.M && n == g.N &&
-            k == g.K && t < TILE_COUNT && t != TILE_128x160 && t != TILE_CONV3_HALO)
-          best = GemmPlan{(int)t, sp};
-        p = strchr(p, ';');
-        if (p) p++;
-      }
-    }
     if (env_tile) best.tile = atoi(env_tile);
     if (env_split) best.splits = (uint32_t)atoi(env_split);
     if (best.splits < 1) best.splits = 1;
