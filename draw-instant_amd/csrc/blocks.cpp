@@ -233,7 +233,7 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   int rc = t.alloc(c, rows * C * 2);
   // row statistics of h from the GEMM that wrote it: the next LayerNorm runs
   // inside the consuming GEMM's A staging
-  if (!rc) rc = rs.alloc(c, rows * ((C + 63) / 64) * 2 * sizeof(float));
+  if (!rc) rc = rs.alloc(c, rows * ((C + 31) / 32) * 2 * sizeof(float));
   if (!rc) rc = h.alloc(c, rows * C * 2);
   if (!rc) rc = n.alloc(c, rows * C * 2);
   if (!rc) rc = qkv.alloc(c, rows * 3 * C * 2);

@@ -23,7 +23,8 @@ struct StatsOut {
 };
 
 // Request for a GEMM's row statistics (GemmArgs::rstats): p is the
-// destination ([rows][ceil(N/64)] pairs suffice); nt and done are reported.
+// destination ([rows][ceil(N/32)] pairs suffice: tiles of 32 columns and
+// more write it); nt and done are reported.
 struct RowStatsOut {
   float* p = nullptr;
   uint32_t nt = 0;

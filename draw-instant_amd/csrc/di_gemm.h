@@ -30,7 +30,11 @@ enum TileCfg {
   // 3x3 stride-1 conv with the input halo staged per channel chunk
   // (k_conv3.hip): 128 output pixels (whole rows) x 64 channels
   TILE_CONV3_HALO = 13,
-  TILE_COUNT = 14
+  // eight wavefronts, 2x2 wave tiles of 32 x 16 (two k halves): half the
+  // B rows per workgroup of 64x64 K2, so a small-M GEMM spreads its loads
+  // over twice the CUs
+  TILE_64x32_K2 = 14,
+  TILE_COUNT = 15
 };
 
 struct GemmPlan {

@@ -181,12 +181,12 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
   }
 }
 
-const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64, 64, 128, 64, 64, 128, 128, 64, 128};
-const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160, 64, 64, 128, 128, 64, 128, 64, 64};
+const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64, 64, 128, 64, 64, 128, 128, 64, 128, 64};
+const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160, 64, 64, 128, 128, 64, 128, 64, 64, 32};
 // Relative per-CU MFMA efficiency of each tile shape (the 2x2 wavefront tile
 // sets LDS bytes per MFMA cycle); tuned by measurement.
 const double kTileEff[TILE_COUNT] = {0.35, 0.5, 0.5, 0.8, 0.85, 0.55, 0.35, 0.5, 0.5,
-                                      0.5, 0.5, 0.8, 0.35, 0.8};
+                                      0.5, 0.5, 0.8, 0.35, 0.8, 0.25};
 bool vec_epi_ok(const GemmArgs& g, int elem, int tile_cfg);
 
 }  // namespace
@@ -363,9 +363,11 @@ bool gemm_stats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile
 bool gemm_rstats_ok(const GemmArgs& g, int elem, int a_mode, int b_mode, int tile_cfg) {
   GemmArgs h = g;
   h.splits = 1;
-  // row groups of the vector epilogue must divide a wavefront (not 160 wide)
+  // row groups of the vector epilogue must divide a wavefront (not 160
+  // wide); at least 32 columns per tile, so that [rows][ceil(N / 32)] pairs
+  // hold the layout (the callers' buffers are sized so)
   return gemm_stats_ok(h, elem, a_mode, b_mode, tile_cfg) && g.splits <= 1 &&
-         64 % (kTileN[tile_cfg] / 8) == 0;
+         kTileN[tile_cfg] >= 32 && 64 % (kTileN[tile_cfg] / 8) == 0;
 }
 
 bool gemm_lnfold_ok(const GemmArgs& g, int elem, int tile_cfg) {

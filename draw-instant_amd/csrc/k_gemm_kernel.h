@@ -1092,6 +1092,7 @@ void launch_fast_d(const GemmArgs& g, int tile_cfg, hipStream_t s) {
     case TILE_128x64_W16: launch_cfg<f16, 128, 64, 4, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
     case TILE_128x128_W16: launch_cfg<f16, 128, 128, 2, 4, AM, B_NK, true, D, 2, EX>(g, s); break;
     case TILE_64x64_W16: launch_cfg<f16, 64, 64, 2, 4, AM, B_NK, true, D, 2, EX>(g, s); break;
+    case TILE_64x32_K2: launch_cfg<f16, 64, 32, 2, 2, AM, B_NK, true, D, 2, EX>(g, s); break;
     default: launch_cfg<f16, 64, 64, 2, 2, AM, B_NK, true, D, 1, EX>(g, s); break;
   }
 }

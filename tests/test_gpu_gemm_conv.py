@@ -189,7 +189,7 @@ def test_linear_fp16_every_plan(dev, rng, monkeypatch, M, N, K, act, res):
         ref = full
     if res:
         ref = ref + r.astype(np.float32)
-    for tile in (0, 1, 2, 3, 5, 6, 7, 8, 9, 10, 11, 12):
+    for tile in (0, 1, 2, 3, 5, 6, 7, 8, 9, 10, 11, 12, 14):
         for splits in (1, 2, 3):
             monkeypatch.setenv("DI_GEMM_TILE", str(tile))
             monkeypatch.setenv("DI_GEMM_SPLITS", str(splits))
@@ -253,7 +253,7 @@ def test_conv_nhwc_fp16(dev, rng, n, cin, cout, h, w, k, s, pad, up, res):
     assert _conv_case(dev, rng, n, cin, cout, h, w, k, s, pad, up, res) <= 2e-3
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 5, 6, 7, 8, 9, 10, 11, 12])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 5, 6, 7, 8, 9, 10, 11, 12, 14])
 def test_conv_nhwc_fp16_every_tile(dev, rng, monkeypatch, tile):
     """conv3x3 (implicit GEMM, buffer-load path) with every tile shape forced,
     including the eight-wavefront k-half variants, split-K 1 and 2."""

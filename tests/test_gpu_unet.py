@@ -57,6 +57,28 @@ def test_small_unet_vs_oracle(dev, rng):
         u.destroy()
 
 
+def test_small_unet_narrow_tile_vs_oracle(dev, rng, monkeypatch):
+    """Every GEMM / conv of a step on the 64 x 32 tile (DI_GEMM_TILE=14):
+    the transformers' projections write row statistics of their outputs per
+    32-column tile, twice the pairs of a 64-column tile, into the
+    [rows][ceil(N / 32)] buffer, and the folded LayerNorms read them; the
+    step matches the oracle composition."""
+    from drawinstant.unet import UNet, UNetConfig
+    monkeypatch.setenv("DI_GEMM_TILE", "14")
+    cfg = UNetConfig.small()
+    u = UNet(dev, cfg, seed=7)
+    try:
+        x, ctx = _inputs(rng, 1, 16, 16, 77, cfg.cross_dim)
+        got = u(x, 999.0, ctx)
+        ref = unet_ref.unet_forward(unet_ref.OracleOps(), u.state_dict(), cfg.as_dict(), x,
+                                    np.array([999.0], np.float32), ctx)
+        err = rel_l2(got, ref)
+        print(f"[small unet, 64x32 tile] rel-L2 {err:.2e}", flush=True)
+        assert np.isfinite(got).all() and err <= 1e-2
+    finally:
+        u.destroy()
+
+
 def test_layer_norm_fold_follows_uploads(dev, rng):
     """The transformer LayerNorms (norm1/2/3) run inside their projections'
     GEMMs, on weights derived from the parameters (W * gamma, beta . W + bias)
