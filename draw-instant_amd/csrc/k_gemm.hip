@@ -38,8 +38,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
   }
 }
 
-// Vector split-K reduction + epilogue (vec_epi): one thread per 8 output
-// columns; the partials of all splits are summed in split order.
+// Sum of the split-K partials of 8 columns of row m, in split order.
 __device__ __forceinline__ void sum_splits8(const GemmArgs& g, uint32_t bz, uint32_t m, uint32_t n,
                                             float* out) {
   const uint64_t mn = (uint64_t)g.M * g.N;
@@ -68,62 +67,83 @@ __device__ __forceinline__ void sum_splits8(const GemmArgs& g, uint32_t bz, uint
   }
 }
 
+// One output vector of the split-K reduction + epilogue (vec_epi): row m,
+// output columns c8 .. c8 + 7 (with GEGLU, of the N / 2 combined columns).
+// The stored fp16 values are returned in v as floats.
+__device__ __forceinline__ void splitk_vec8(const GemmArgs& g, uint32_t bz, uint32_t m, uint32_t c8,
+                                            float* v) {
+  f16* C = (f16*)g.c + (uint64_t)bz * g.sc + (uint64_t)m * g.ldc + c8;
+  const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr + (uint64_t)m * g.ldr + c8;
+  float x[8];
+  float mean = 0.0f, rstd = 0.0f;
+  if (g.ln_rows) ln_coef(g, m, mean, rstd);
+  if (g.act == ACT_GEGLU) {
+    const uint32_t nh = (c8 / 16) * 32 + c8 % 16;
+    float gt[8];
+    sum_splits8(g, bz, m, nh, x);
+    sum_splits8(g, bz, m, nh + 16, gt);
+    if (g.ln_rows) {
+      const f32x4 sh[2] = {ld4(g.ln_s + nh), ld4(g.ln_s + nh + 4)};
+      const f32x4 sg[2] = {ld4(g.ln_s + nh + 16), ld4(g.ln_s + nh + 20)};
+      ln_fold8(x, mean, rstd, sh);
+      ln_fold8(gt, mean, rstd, sg);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float hv = x[j] * g.alpha + (g.bias ? g.bias[nh + j] : 0.0f);
+      const float gv = gt[j] * g.alpha + (g.bias ? g.bias[nh + 16 + j] : 0.0f);
+      x[j] = hv * gelu_erf_f(gv);
+    }
+  } else {
+    f32x4 bb[2] = {}, tb[2] = {};
+    if (g.bias) {
+      bb[0] = ld4(g.bias + c8);
+      bb[1] = ld4(g.bias + c8 + 4);
+    }
+    if (g.bias2) {
+      const float* tp = g.bias2 + (uint64_t)(m / g.rows_b2) * g.ld_b2 + c8;
+      tb[0] = ld4(tp);
+      tb[1] = ld4(tp + 4);
+    }
+    sum_splits8(g, bz, m, c8, x);
+    if (g.ln_rows) {
+      const f32x4 ls[2] = {ld4(g.ln_s + c8), ld4(g.ln_s + c8 + 4)};
+      ln_fold8(x, mean, rstd, ls);
+    }
+    epi_math8(g, x, bb, tb);
+  }
+  f16x8 rv = {};
+  if (g.res) rv = *(const f16x8*)R;
+  f16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rv[j] : x[j]);
+  *(f16x8*)C = o;
+#pragma unroll
+  for (int j = 0; j < 8; j++) v[j] = (float)o[j];
+}
+
+// Column sum of 64 staged values (or of their squares), in row order.
+__device__ __forceinline__ float splitk_colsum64(const float* p, int ld, bool squares) {
+  float a = 0.0f;
+  for (int r = 0; r < 64; r++) {
+    const float x = p[r * ld];
+    a += squares ? __fmul_rn(x, x) : x;
+  }
+  return a;
+}
+
+// Vector split-K reduction + epilogue (vec_epi): one thread per 8 output
+// columns (splitk_vec8).
 __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
-  const bool geglu = g.act == ACT_GEGLU;
-  const uint32_t ncols = geglu ? g.N / 2 : g.N;
+  const uint32_t ncols = g.act == ACT_GEGLU ? g.N / 2 : g.N;
   const uint32_t vpr = ncols / 8;
   const uint64_t total = (uint64_t)g.batch * g.M * vpr;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const uint32_t c8 = (uint32_t)(i % vpr) * 8;
     const uint64_t t = i / vpr;
-    const uint32_t m = (uint32_t)(t % g.M), bz = (uint32_t)(t / g.M);
-    f16* C = (f16*)g.c + (uint64_t)bz * g.sc + (uint64_t)m * g.ldc + c8;
-    const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr + (uint64_t)m * g.ldr + c8;
-    float x[8];
-    float mean = 0.0f, rstd = 0.0f;
-    if (g.ln_rows) ln_coef(g, m, mean, rstd);
-    if (geglu) {
-      const uint32_t nh = (c8 / 16) * 32 + c8 % 16;
-      float gt[8];
-      sum_splits8(g, bz, m, nh, x);
-      sum_splits8(g, bz, m, nh + 16, gt);
-      if (g.ln_rows) {
-        const f32x4 sh[2] = {ld4(g.ln_s + nh), ld4(g.ln_s + nh + 4)};
-        const f32x4 sg[2] = {ld4(g.ln_s + nh + 16), ld4(g.ln_s + nh + 20)};
-        ln_fold8(x, mean, rstd, sh);
-        ln_fold8(gt, mean, rstd, sg);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float hv = x[j] * g.alpha + (g.bias ? g.bias[nh + j] : 0.0f);
-        const float gv = gt[j] * g.alpha + (g.bias ? g.bias[nh + 16 + j] : 0.0f);
-        x[j] = hv * gelu_erf_f(gv);
-      }
-    } else {
-      f32x4 bb[2] = {}, tb[2] = {};
-      if (g.bias) {
-        bb[0] = ld4(g.bias + c8);
-        bb[1] = ld4(g.bias + c8 + 4);
-      }
-      if (g.bias2) {
-        const float* tp = g.bias2 + (uint64_t)(m / g.rows_b2) * g.ld_b2 + c8;
-        tb[0] = ld4(tp);
-        tb[1] = ld4(tp + 4);
-      }
-      sum_splits8(g, bz, m, c8, x);
-      if (g.ln_rows) {
-        const f32x4 ls[2] = {ld4(g.ln_s + c8), ld4(g.ln_s + c8 + 4)};
-        ln_fold8(x, mean, rstd, ls);
-      }
-      epi_math8(g, x, bb, tb);
-    }
-    f16x8 rv = {};
-    if (g.res) rv = *(const f16x8*)R;
-    f16x8 o;
-#pragma unroll
-    for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rv[j] : x[j]);
-    *(f16x8*)C = o;
+    float v[8];
+    splitk_vec8(g, (uint32_t)(t / g.M), (uint32_t)(t % g.M), c8, v);
   }
 }
 
@@ -132,52 +152,20 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
 // owns rows [64y, 64y + 64) x columns [32x, 32x + 32); thread t reduces
 // columns 32x + 8*(t % 4) .. +8 of row 64y + t/4.
 __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
-  __shared__ float red[2][64][33];
+  constexpr int LDR = 33;
+  __shared__ float red[64 * LDR];
   const uint32_t t = threadIdx.x, cv = t % 4, rr = t / 4;
   const uint32_t n = blockIdx.x * 32 + cv * 8, bz = blockIdx.z;
   const uint32_t m = blockIdx.y * 64 + rr;
-  float s[8], q[8];
+  float v[8] = {};
+  if (m < g.M) splitk_vec8(g, bz, m, n, v);
 #pragma unroll
-  for (int j = 0; j < 8; j++) s[j] = q[j] = 0.0f;
-  if (m < g.M) {
-    f32x4 bb[2] = {}, tb[2] = {};
-    if (g.bias) {
-      bb[0] = ld4(g.bias + n);
-      bb[1] = ld4(g.bias + n + 4);
-    }
-    if (g.bias2) {
-      const float* tp = g.bias2 + (uint64_t)(m / g.rows_b2) * g.ld_b2 + n;
-      tb[0] = ld4(tp);
-      tb[1] = ld4(tp + 4);
-    }
-    f16x8 rv = {};
-    if (g.res) rv = *(const f16x8*)((const f16*)g.res + (uint64_t)bz * g.sr + (uint64_t)m * g.ldr + n);
-    float x[8];
-    sum_splits8(g, bz, m, n, x);
-    epi_math8(g, x, bb, tb);
-    f16x8 o;
-#pragma unroll
-    for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rv[j] : x[j]);
-    *(f16x8*)((f16*)g.c + (uint64_t)bz * g.sc + (uint64_t)m * g.ldc + n) = o;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const float v = (float)o[j];
-      s[j] = v;
-      q[j] = v * v;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    red[0][rr][cv * 8 + j] = s[j];
-    red[1][rr][cv * 8 + j] = q[j];
-  }
+  for (int j = 0; j < 8; j++) red[rr * LDR + cv * 8 + j] = v[j];
   __syncthreads();
   if (t < 64) {
     const uint32_t col = t % 32, st = t / 32;
-    float a = 0.0f;
-    for (int r = 0; r < 64; r++) a += red[st][r][col];
     const uint64_t chunk = (uint64_t)bz * ((g.M + 63) / 64) + blockIdx.y;
-    g.stats[(chunk * g.N + blockIdx.x * 32 + col) * 2 + st] = a;
+    g.stats[(chunk * g.N + blockIdx.x * 32 + col) * 2 + st] = splitk_colsum64(red + col, LDR, st == 1);
   }
 }
 
