@@ -65,6 +65,28 @@ def timed(dev, fn, iters):
     return ms / iters
 
 
+def step_spread(dev, step, batch=10, batches=9, slope_reps=7):
+    """Spread of the graph-replayed step, measured after the headline's K
+    steps: (a) `batches` batches of `batch` back-to-back replays, each
+    bracketed by HIP events (ms per step: median and interquartile range);
+    (b) the reference's slope method (bench-timing.js:49-97): interleaved
+    batches of N and 2N replays, (t2N - tN) / N, median and IQR of
+    `slope_reps` pairs, which cancels the per-batch fixed cost."""
+    per = [timed(dev, step, batch) for _ in range(batches)]
+    slopes = []
+    for _ in range(slope_reps):
+        t1 = timed(dev, step, batch) * batch
+        t2 = timed(dev, step, 2 * batch) * 2 * batch
+        slopes.append((t2 - t1) / batch)
+    q = np.percentile(per, [25, 50, 75])
+    qs = np.percentile(slopes, [25, 50, 75])
+    return {"batches": {"n": batches, "steps_each": batch, "median_ms": round(float(q[1]), 4),
+                        "iqr_ms": [round(float(q[0]), 4), round(float(q[2]), 4)],
+                        "min_ms": round(float(min(per)), 4), "max_ms": round(float(max(per)), 4)},
+            "slope": {"n": slope_reps, "N": batch, "median_ms": round(float(qs[1]), 4),
+                      "iqr_ms": [round(float(qs[0]), 4), round(float(qs[2]), 4)]}}
+
+
 def bench_unet(dev, args):
     from drawinstant.unet import UNet
     u = UNet(dev, seed=501)
@@ -86,10 +108,11 @@ def bench_unet(dev, args):
     t0 = time.perf_counter()
     ms = timed(dev, step, args.steps)
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    spread = step_spread(dev, step)
     eager = timed(dev, lambda i: step(i, False), max(2, args.steps // 4))
     out = dev.download(bo, np.float32, x.shape)
     finite = bool(np.isfinite(out).all())
-    return u, ms, wall, eager, finite, (x, ctx)
+    return u, ms, wall, eager, finite, (x, ctx), spread
 
 
 def bench_unet_batch(dev, u, B=4, iters=20):
@@ -215,6 +238,43 @@ def bench_blocks(dev, num_rot=64):
     fl = 2.0 * rows * D * 2 * F + 2.0 * rows * F * D
     res["ffn_geglu_64x64"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
                               "mfma_frac": fl / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, "flops": fl}
+    # cfg4 cross-attention (fused-cross-attn.js:112-173): 4096 queries x 5
+    # heads x 64 against the 77 context tokens, fp16 [B,S,H,d]
+    cq = dev.storage(rng.standard_normal((1, 4096, 5, 64)).astype(np.float16))
+    ck = dev.storage(rng.standard_normal((1, 77, 5, 64)).astype(np.float16))
+    cv = dev.storage(rng.standard_normal((1, 77, 5, 64)).astype(np.float16))
+    co = dev.create_buffer(4096 * 320 * 2)
+    xatt = lambda i: call("di_attn_cross", dev.ctx, cq.handle, ck.handle, cv.handle, co.handle, 1,
+                          5, 4096, 77, 64, 0, 0.0, 1)
+    xatt(0)
+    ms = timed(dev, xatt, 100)
+    fl = 4.0 * 4096 * 77 * 320
+    res["cross_attn_64x64"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+                               "mfma_frac": fl / (ms * 1e-3) / perf.PEAK_FP16_FLOPS, "flops": fl}
+    # timestep embedding (fused-tembed.js:73-130): sinusoid(t) -> Linear
+    # 320->1280 + SiLU -> Linear 1280->1280, fp16 weights, B = 1; the weights
+    # rotate over 96 copies (> 256 MB Infinity Cache), as a step reads them cold
+    E, Hd, nrot = 320, 1280, 96
+    tt = dev.storage(np.array([999.0], np.float32))
+    tw1 = [dev.create_buffer(Hd * E * 2) for _ in range(nrot)]
+    tw2 = [dev.create_buffer(Hd * Hd * 2) for _ in range(nrot)]
+    for i in range(nrot):
+        dev.fill_normal(tw1[i], Hd * E, 7000 + i, 0.0, 0.05, dtype=np.float16)
+        dev.fill_normal(tw2[i], Hd * Hd, 8000 + i, 0.0, 0.03, dtype=np.float16)
+    tb1 = dev.storage((0.02 * rng.standard_normal(Hd)).astype(np.float32))
+    tb2 = dev.storage((0.02 * rng.standard_normal(Hd)).astype(np.float32))
+    ty = dev.create_buffer(Hd * 4)
+    temb = lambda i: call("di_tembed", dev.ctx, tt.handle, tw1[i % nrot].handle, tb1.handle,
+                          tw2[i % nrot].handle, tb2.handle, ty.handle, 1, E, Hd, 1)
+    for i in range(nrot):
+        temb(i)
+    ms = timed(dev, temb, 2 * nrot)
+    nbytes = 2 * (Hd * E + Hd * Hd) + 4 * (2 * Hd + 1 + Hd)
+    res["tembed_1280"] = {"us": ms * 1e3, "GBps": nbytes / (ms * 1e-3) / 1e9,
+                          "hbm_frac": nbytes / (ms * 1e-3) / perf.PEAK_HBM_BYTES, "bytes": nbytes,
+                          "launches": 2}
+    for b in tw1 + tw2 + [tt, tb1, tb2, ty, cq, ck, cv, co]:
+        b.destroy()
     return res
 
 
@@ -460,8 +520,9 @@ def bench_executor_vae(dev, reps=3):
 ROOFLINE_PMC = os.path.join(REPO, "profiles", "k_conv3_halo_conv3x3_64x64x320_pmc.md")
 
 
-def roofline_conv(dev, iters=200):
-    """Live roofline of the dominant kernel at its U-Net shape."""
+def roofline_conv(dev, iters=200, cold=True):
+    """Live roofline of the dominant kernel at its U-Net shape (warm: the
+    same weights every launch; `cold`: also with the weights from HBM)."""
     from drawinstant import perf
     from drawinstant.device import call
     rng = np.random.default_rng(3)
@@ -477,6 +538,21 @@ def roofline_conv(dev, iters=200):
     fl = perf.conv_flops(1, 320, 320, 64, 64, 3)
     achieved = fl / (ms * 1e-3) / 1e12
     peak = perf.PEAK_FP16_FLOPS / 1e12
+    # the same launches with the weights read cold, as in the U-Net step:
+    # 160 weight copies (295 MB > the 256 MB Infinity Cache) in rotation
+    nrot = 160 if cold else 0
+    ws = [dev.create_buffer(320 * 9 * 320 * 2) for _ in range(nrot)]
+    for i, b in enumerate(ws):
+        dev.fill_normal(b, 320 * 9 * 320, 9000 + i, 0.0, 0.026, dtype=np.float16)
+    conv_cold = lambda i: call("di_conv2d", dev.ctx, x.handle, ws[i % nrot].handle, bias.handle, 0,
+                          y.handle, 1, 320, 320, 64, 64, 3, 1, 1, 0, 1, 1)
+    ms_cold = None
+    if nrot:
+        for i in range(nrot):
+            conv_cold(i)
+        ms_cold = timed(dev, conv_cold, nrot)
+    for b in ws:
+        b.destroy()
     traffic = None
     if os.path.exists(ROOFLINE_PMC):
         for line in open(ROOFLINE_PMC):
@@ -488,7 +564,12 @@ def roofline_conv(dev, iters=200):
                       "halo staged per channel chunk",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": traffic,
-            "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3)}
+            "flop_per_launch": fl, "us_per_launch": round(ms * 1e3, 3),
+            "cold_weights": None if ms_cold is None else {
+                "us_per_launch": round(ms_cold * 1e3, 3),
+                "achieved": round(fl / (ms_cold * 1e-3) / 1e12, 2),
+                "frac": round(fl / (ms_cold * 1e-3) / 1e12 / peak, 4),
+                "note": "weights from HBM (160 copies in rotation), as in the step"}}
 
 
 def cpu_baseline(u):
@@ -595,7 +676,7 @@ def main():
     from drawinstant import perf
     dev = drawinstant.Device(0)
     if args.roofline_only:
-        rl = roofline_conv(dev)
+        rl = roofline_conv(dev, cold=False)
         # calibration: a streaming kernel of known traffic (di_unary NEG over
         # 64 Mi floats reads 256 MiB and writes 256 MiB)
         from drawinstant.device import call
@@ -630,7 +711,7 @@ def main():
         print(json.dumps({"eager_steps": args.eager_only, "eager_ms_per_step": round(ms, 4)}),
               flush=True)
         return
-    u, ms, wall, eager, finite, inputs = bench_unet(dev, args)
+    u, ms, wall, eager, finite, inputs, spread = bench_unet(dev, args)
     work = perf.unet_work()
     line = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
@@ -641,6 +722,7 @@ def main():
                                "random-init fp16 weights (865.9M params), HIP-graph replay",
                    "batch": 1, "latent": [64, 64], "gflop_per_step": round(work.total / 1e9, 2),
                    "parallelism": "single GPU"},
+        "step_spread": spread,
         "eager_ms_per_step": round(eager, 4),
         "wall_ms_per_step": round(wall, 4),
         "step_tflops": round(work.total / (ms * 1e-3) / 1e12, 1),

@@ -36,8 +36,14 @@ int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rs
   if (rst && rst->p) {
     rst->done = gemm_rstats_ok(g, DI_F16, a_mode, B_NK, tile);
     if (rst->done) {
+      const uint32_t nt = gemm_rstats_tiles(g, tile);
+      const uint64_t need = (uint64_t)g.M * nt * 2 * sizeof(float);  // [M][nt] float2
+      DI_REQUIRE(need <= rst->bytes, DI_EINVAL,
+                 "row statistics of M=%u N=%u (tile %d, %u column tiles) need %llu bytes, "
+                 "buffer holds %llu", g.M, g.N, tile, nt, (unsigned long long)need,
+                 (unsigned long long)rst->bytes);
       g.rstats = rst->p;
-      rst->nt = gemm_rstats_tiles(g, tile);
+      rst->nt = nt;
     }
   }
   DI_REQUIRE(!g.ln_rows || gemm_lnfold_ok(g, DI_F16, tile), DI_EUNSUPPORTED,
@@ -233,7 +239,8 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   int rc = t.alloc(c, rows * C * 2);
   // row statistics of h from the GEMM that wrote it: the next LayerNorm runs
   // inside the consuming GEMM's A staging
-  if (!rc) rc = rs.alloc(c, rows * ((C + 31) / 32) * 2 * sizeof(float));
+  const uint64_t rs_bytes = rows * ((C + 31) / 32) * 2 * sizeof(float);
+  if (!rc) rc = rs.alloc(c, rs_bytes);
   if (!rc) rc = h.alloc(c, rows * C * 2);
   if (!rc) rc = n.alloc(c, rows * C * 2);
   if (!rc) rc = qkv.alloc(c, rows * 3 * C * 2);
@@ -245,7 +252,7 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   // GN (eps 1e-6 in diffusers Transformer2DModel) -> proj_in
   rc = gn_nhwc(c, single(x, C), w.n_g, w.n_b, t.h(), s.B, C, s.groups, HW, s.gn_eps, false, x_st);
   // a producer of h writes its row statistics when the next LayerNorm is folded
-  RowStatsOut ro{rs.f()};
+  RowStatsOut ro{rs.f(), rs_bytes};
   auto ro_for = [&](const float* fs) {
     ro.done = false;
     return fs ? &ro : nullptr;

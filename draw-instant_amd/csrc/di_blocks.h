@@ -23,10 +23,12 @@ struct StatsOut {
 };
 
 // Request for a GEMM's row statistics (GemmArgs::rstats): p is the
-// destination ([rows][ceil(N/32)] pairs suffice: tiles of 32 columns and
-// more write it); nt and done are reported.
+// destination of `bytes` bytes ([rows][ceil(N/32)] float pairs suffice:
+// tiles of 32 columns and more write it); nt and done are reported.  run()
+// refuses a plan whose [rows][nt] pairs would not fit.
 struct RowStatsOut {
   float* p = nullptr;
+  uint64_t bytes = 0;
   uint32_t nt = 0;
   bool done = false;
 };

@@ -120,6 +120,16 @@ int workspace(Ctx* c, uint64_t bytes, void** out);
 void* workspace_pin(Ctx* c);
 void workspace_unpin(Ctx* c, void* ws);
 
+// Debug checks of captured graphs (DI_GRAPH_CHECK=1): every node of `g` is a
+// kernel launch with a grid, block and LDS size in range (count returned);
+// and, before a replay, every allocation the graph baked in is still owned
+// by it: the pinned workspace is current or retired-and-pinned, no scratch
+// buffer is on the pool's free list, every I/O pointer is a live buffer.
+bool graph_check_enabled();
+int graph_check_nodes(hipGraph_t g, size_t* kernels);
+int graph_check_live(Ctx* c, const void* ws, const std::vector<std::pair<void*, uint64_t>>& scratch,
+                     const void* const* io, size_t nio);
+
 // Pooled device allocation used by the C ABI and by block compositions.
 int pool_alloc(Ctx* c, uint64_t bytes, void** out, uint64_t* cap);
 void pool_release(Ctx* c, void* p, uint64_t cap);

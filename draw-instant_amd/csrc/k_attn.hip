@@ -63,6 +63,8 @@ constexpr int BUF_BYTES = 2 * K_BYTES;    // K tile, then V tile
 // a lane's 16 probabilities of one tile sum to at most this without a
 // rescale, so none exceeds it either (fp16 max is 65504)
 constexpr float kLaneSumMax = 32768.0f;
+constexpr uint32_t kLaneSumMaxBits = 0x47000000u;  // bits of 32768.0f
+static_assert(__builtin_bit_cast(uint32_t, kLaneSumMax) == kLaneSumMaxBits, "kLaneSumMaxBits");
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -242,8 +244,10 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
     };
     probs();
     // a probability above kLaneSumMax (or inf / NaN from an overflowing
-    // score) shows in its lane's sum: rescale and redo the tile
-    if (__builtin_amdgcn_ballot_w64(!(ts <= kLaneSumMax)) != 0) {
+    // score) shows in its lane's sum: rescale and redo the tile.  The test
+    // compares the sum's bits as an integer (sign cleared), which orders
+    // finite < inf < NaN and which -fno-honor-nans cannot fold away.
+    if (__builtin_amdgcn_ballot_w64((__float_as_uint(ts) & 0x7fffffffu) > kLaneSumMaxBits) != 0) {
       raise_max(false);
       probs();
     }

@@ -209,6 +209,29 @@ bool tuned_plan(const GemmArgs& g, GemmPlan* out) {
 
 }  // namespace
 
+// DI_GEMM_TILE / DI_GEMM_SPLITS (tuning runs): a value that is not a whole
+// number, names no built tile (or the halo conv for a conv it cannot take),
+// or asks for splits outside [1, 64] is ignored, so no override can index
+// the tile tables out of range.
+static void env_plan_override(const GemmArgs& g, int elem, const char* env_tile,
+                              const char* env_split, GemmPlan* plan) {
+  if (env_tile) {
+    char* end = nullptr;
+    const long t = strtol(env_tile, &end, 10);
+    const bool ok = end != env_tile && *end == '\0' && t >= 0 && t < TILE_COUNT &&
+                    t != TILE_128x160 &&
+                    (t != TILE_CONV3_HALO ||
+                     (conv3_halo_ok(g) && vec_epi_ok(g, elem, TILE_CONV3_HALO)));
+    if (ok) plan->tile = (int)t;
+  }
+  if (env_split) {
+    char* end = nullptr;
+    const long sp = strtol(env_split, &end, 10);
+    if (end != env_split && *end == '\0' && sp >= 1 && sp <= 64) plan->splits = (uint32_t)sp;
+  }
+  if (plan->splits < 1) plan->splits = 1;
+}
+
 GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
   // DI_GEMM_PLAN="M,N,K,tile,splits;..." fixes the plan of the listed fp16
   // shapes only (tuning runs of the whole step; tile 13 = the halo conv)
@@ -246,9 +269,7 @@ GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
     if (hs >= 1 && nch % hs == 0) return GemmPlan{TILE_CONV3_HALO, hs};
   }
   if (elem == DI_F16 && tuned_plan(g, &best)) {
-    if (env_tile) best.tile = atoi(env_tile);
-    if (env_split) best.splits = (uint32_t)atoi(env_split);
-    if (best.splits < 1) best.splits = 1;
+    env_plan_override(g, elem, env_tile, env_split, &best);
     return best;
   }
   if (elem == DI_F32) {
@@ -280,9 +301,7 @@ GemmPlan gemm_plan(const GemmArgs& g, int elem, int num_cus) {
       }
     }
   }
-  if (env_tile) best.tile = atoi(env_tile);
-  if (env_split) best.splits = (uint32_t)atoi(env_split);
-  if (best.splits < 1) best.splits = 1;
+  env_plan_override(g, elem, env_tile, env_split, &best);
   return best;
 }
 

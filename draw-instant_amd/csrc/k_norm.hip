@@ -20,6 +20,7 @@
 // call), so each issues all of a round's loads (x, partials, gamma/beta)
 // before consuming any: `sched_barrier` stops the scheduler from sinking the
 // loads next to their uses, which would serialise them.
+#include <cstdio>
 #include <cstdlib>
 #include <mutex>
 
@@ -878,12 +879,17 @@ int gn_nchw_launch(Ctx* c, const void* x, const float* gamma, const float* beta,
 // (64 floats in registers per thread) or of less than one round of 1024
 // vectors (most of a 1024-thread workgroup idle), and fewer than 8 groups
 // (too few workgroups whichever way), take the two-kernel path.
+// largest per-group round count gn_fused instantiates for a vector width
+constexpr uint32_t gn_fused_max_rounds(uint32_t vec) { return vec <= 4 ? 16u : 8u; }
+
 uint32_t gn_fused_slices(uint32_t NG, uint32_t L, uint32_t vec) {
   static const int env = [] {
     const char* e = getenv("DI_GN_FUSED");
     return e ? atoi(e) : 1;
   }();
   if (!env || NG < 8 || L > 64u * kFusedT || L < kFusedT * vec || NG > (1u << 20)) return 0;
+  // every round of a group needs an instantiated unroll (gn_fused)
+  if ((L + kFusedT * vec - 1) / (kFusedT * vec) > gn_fused_max_rounds(vec)) return 0;
   static const uint32_t env_s = [] {  // tuning override: DI_GN_SLICES=n
     const char* e = getenv("DI_GN_SLICES");
     return e ? (uint32_t)atoi(e) : 0u;
@@ -900,6 +906,11 @@ void gn_fused_launch(hipStream_t st, const T* x, const float* gamma, const float
                      uint32_t NG, uint32_t G, uint32_t cpg, uint32_t HW, uint32_t S, float eps,
                      bool silu) {
   const uint32_t L = cpg * HW;
+  // the kernel reads U rounds of kFusedT * VEC elements per group
+  if ((L + kFusedT * VEC - 1) / (kFusedT * VEC) > (uint32_t)U) {
+    fprintf(stderr, "gn_fused_launch: %u elements per group exceed %d rounds\n", L, U);
+    abort();
+  }
   uint32_t chunk = (L + S - 1) / S;
   chunk = (chunk + VEC - 1) / VEC * VEC;
   const uint32_t Sr = (L + chunk - 1) / chunk;  // non-empty slices
@@ -907,11 +918,16 @@ void gn_fused_launch(hipStream_t st, const T* x, const float* gamma, const float
                                                            chunk, eps, silu ? 1 : 0);
 }
 
+// Launches the single-pass kernel with an unroll U >= the group's rounds of
+// kFusedT * VEC elements; returns false (nothing launched) for more rounds
+// than any instantiation holds, which gn_fused_slices never plans.
 template <typename T, int VEC>
-void gn_fused(hipStream_t st, const T* x, const float* gamma, const float* beta, T* y,
+bool gn_fused(hipStream_t st, const T* x, const float* gamma, const float* beta, T* y,
               uint32_t NG, uint32_t G, uint32_t cpg, uint32_t HW, uint32_t S, float eps,
               bool silu) {
   const uint32_t rounds = (cpg * HW + kFusedT * VEC - 1) / (kFusedT * VEC);
+  static_assert(gn_fused_max_rounds(VEC) == (VEC <= 4 ? 16u : 8u), "unrolls below");
+  if (rounds > gn_fused_max_rounds(VEC)) return false;
 #define DI_GN_FUSED_U(u) \
   gn_fused_launch<T, VEC, u>(st, x, gamma, beta, y, NG, G, cpg, HW, S, eps, silu)
   if (rounds <= 1) DI_GN_FUSED_U(1);
@@ -920,10 +936,13 @@ void gn_fused(hipStream_t st, const T* x, const float* gamma, const float* beta,
   else if (rounds <= 4) DI_GN_FUSED_U(4);
   else if (rounds <= 6) DI_GN_FUSED_U(6);
   else if (rounds <= 8) DI_GN_FUSED_U(8);
-  else if (VEC <= 4 && rounds <= 10) DI_GN_FUSED_U(VEC <= 4 ? 10 : 1);
-  else if (VEC <= 4 && rounds <= 12) DI_GN_FUSED_U(VEC <= 4 ? 12 : 1);
-  else DI_GN_FUSED_U(VEC <= 4 ? 16 : 1);
+  else if constexpr (VEC <= 4) {
+    if (rounds <= 10) DI_GN_FUSED_U(10);
+    else if (rounds <= 12) DI_GN_FUSED_U(12);
+    else DI_GN_FUSED_U(16);
+  }
 #undef DI_GN_FUSED_U
+  return true;
 }
 
 template <typename T>
@@ -937,11 +956,9 @@ int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* 
   constexpr int V = 16 / sizeof(T);
   if (HW % V == 0) {
     const uint32_t S = gn_fused_slices(N * G, cpg * HW, V);
-    if (S) {
-      gn_fused<T, V>(c->stream, (const T*)x, gamma, beta, (T*)y, N * G, G, cpg, HW, S, eps,
-                     silu);
+    if (S && gn_fused<T, V>(c->stream, (const T*)x, gamma, beta, (T*)y, N * G, G, cpg, HW, S,
+                            eps, silu))
       return DI_OK;
-    }
   }
   if (HW % V == 0)
     return gn_nchw_launch<T, V>(c, x, gamma, beta, y, N, G, cpg, HW, eps, silu, fixed,

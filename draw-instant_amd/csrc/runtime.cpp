@@ -125,6 +125,63 @@ void* workspace_pin(Ctx* c) {
   return c->ws;
 }
 
+bool graph_check_enabled() {
+  const char* e = getenv("DI_GRAPH_CHECK");
+  return e && atoi(e) != 0;
+}
+
+int graph_check_nodes(hipGraph_t g, size_t* kernels) {
+  size_t n = 0;
+  DI_HIP(hipGraphGetNodes(g, nullptr, &n));
+  std::vector<hipGraphNode_t> nodes(n);
+  if (n) DI_HIP(hipGraphGetNodes(g, nodes.data(), &n));
+  for (size_t i = 0; i < n; i++) {
+    hipGraphNodeType t;
+    DI_HIP(hipGraphNodeGetType(nodes[i], &t));
+    DI_REQUIRE(t == hipGraphNodeTypeKernel, DI_EHIP,
+               "graph check: node %zu of %zu has type %d, not a kernel launch", i, n, (int)t);
+    hipKernelNodeParams kp{};
+    DI_HIP(hipGraphKernelNodeGetParams(nodes[i], &kp));
+    const uint64_t threads = (uint64_t)kp.blockDim.x * kp.blockDim.y * kp.blockDim.z;
+    DI_REQUIRE(kp.func != nullptr && kp.gridDim.x >= 1 && kp.gridDim.y >= 1 &&
+                   kp.gridDim.z >= 1 && threads >= 1 && threads <= 1024 &&
+                   kp.sharedMemBytes <= 160u * 1024u,
+               DI_EHIP,
+               "graph check: kernel node %zu: grid %ux%ux%u block %ux%ux%u lds %u out of range", i,
+               kp.gridDim.x, kp.gridDim.y, kp.gridDim.z, kp.blockDim.x, kp.blockDim.y,
+               kp.blockDim.z, kp.sharedMemBytes);
+  }
+  if (kernels) *kernels = n;
+  return DI_OK;
+}
+
+int graph_check_live(Ctx* c, const void* ws, const std::vector<std::pair<void*, uint64_t>>& scratch,
+                     const void* const* io, size_t nio) {
+  if (ws) {
+    auto it = c->ws_refs.find(const_cast<void*>(ws));
+    bool retired = false;
+    for (void* r : c->ws_retired) retired |= r == ws;
+    DI_REQUIRE(it != c->ws_refs.end() && it->second > 0 && (ws == c->ws || retired), DI_EHIP,
+               "graph check: the graph's workspace %p is neither current nor retired-and-pinned",
+               ws);
+  }
+  for (const auto& pc : scratch) {
+    auto fl = c->free_list.find(pc.second);
+    if (fl == c->free_list.end()) continue;
+    for (void* f : fl->second)
+      DI_REQUIRE(f != pc.first, DI_EHIP,
+                 "graph check: graph scratch %p (%llu bytes) is on the pool's free list", pc.first,
+                 (unsigned long long)pc.second);
+  }
+  for (size_t i = 0; i < nio; i++) {
+    bool live = false;
+    for (const auto& kv : c->bufs) live |= kv.second.ptr == io[i];
+    DI_REQUIRE(live, DI_EHIP, "graph check: graph I/O pointer %zu (%p) is not a live buffer", i,
+               io[i]);
+  }
+  return DI_OK;
+}
+
 void workspace_unpin(Ctx* c, void* ws) {
   if (!ws) return;
   auto it = c->ws_refs.find(ws);

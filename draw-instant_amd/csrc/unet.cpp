@@ -98,6 +98,7 @@ struct UNet {
   // captured step
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
+  size_t graph_kernels = 0;  // kernel nodes of the captured graph (DI_GRAPH_CHECK)
   uint64_t graph_key[8] = {0};
 
   int add(const std::string& name, std::vector<uint32_t> shape, int arena, float mean, float std,
@@ -828,8 +829,17 @@ int32_t di_unet_forward(di_ctx* ctx, di_unet* u, di_handle sample, di_handle tim
     DI_REQUIRE(e == hipSuccess, DI_EHIP, "graph capture failed: %s", hipGetErrorString(e));
     u->graph = g;
     u->graph_ws = workspace_pin(ctx);
+    if (graph_check_enabled()) {
+      int crc = graph_check_nodes(g, &u->graph_kernels);
+      if (crc) return crc;
+    }
     DI_HIP(hipGraphInstantiate(&u->graph_exec, g, nullptr, nullptr, 0));
     memcpy(u->graph_key, key, sizeof(key));
+  }
+  if (graph_check_enabled()) {
+    const void* io[4] = {s->ptr, t->ptr, cx->ptr, o->ptr};
+    int crc = graph_check_live(ctx, u->graph_ws, u->graph_scratch, io, 4);
+    if (crc) return crc;
   }
   DI_HIP(hipGraphLaunch(u->graph_exec, ctx->stream));
   return DI_OK;

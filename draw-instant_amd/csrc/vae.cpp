@@ -593,8 +593,18 @@ int32_t di_vae_decode(di_ctx* ctx, di_vae* v, di_handle latent, di_handle image,
     DI_REQUIRE(e == hipSuccess, DI_EHIP, "graph capture failed: %s", hipGetErrorString(e));
     v->graph = g;
     v->graph_ws = workspace_pin(ctx);
+    if (graph_check_enabled()) {
+      size_t kernels = 0;
+      int crc = graph_check_nodes(g, &kernels);
+      if (crc) return crc;
+    }
     DI_HIP(hipGraphInstantiate(&v->graph_exec, g, nullptr, nullptr, 0));
     memcpy(v->graph_key, key, sizeof(key));
+  }
+  if (graph_check_enabled()) {
+    const void* io[2] = {z->ptr, im->ptr};
+    int crc = graph_check_live(ctx, v->graph_ws, v->graph_scratch, io, 2);
+    if (crc) return crc;
   }
   DI_HIP(hipGraphLaunch(v->graph_exec, ctx->stream));
   return DI_OK;

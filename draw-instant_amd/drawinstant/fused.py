@@ -158,17 +158,23 @@ def run_group_norm_bench(device: Optional[Device] = None, shape=None, on_progres
 
 # ------------------------------------------------------------------ Conv --
 def run_conv_bench(device: Optional[Device] = None, shape=None, on_progress=None,
-                   repeats: int = REPEATS, warm_ms: float = WARM_MS, seed: int = 2):
+                   repeats: int = REPEATS, warm_ms: float = WARM_MS, seed: int = 2,
+                   return_tensors: bool = False):
     """conv3x3 with the WGSL_CONV epilogue silu(conv + bias) + residual.
     naive: conv -> SiLU -> Add (3 dispatches); fused: one di_conv2d with
-    DI_CONV_SILU and the residual.  fp32 NCHW, exact fp32 MFMA."""
+    DI_CONV_SILU and the residual.  fp32 NCHW, exact fp32 MFMA.
+
+    ``return_tensors`` adds ``tensors``: the host inputs (x, w, bias, r in
+    NCHW / OIHW) and the fused output y, for a parity check of the fused
+    epilogue against an independent evaluation."""
     S = dict(shape or CONV_SHAPE)
     B, C, H, W, K = S["B"], S["C"], S["H"], S["W"], S["K"]
     bn = _Bench(device, seed)
     n = B * C * H * W
-    x, r = bn.up(bn.rand(n)), bn.up(bn.rand(n))
-    w = bn.up(bn.rand(C * C * K * K, math.sqrt(3.0 / (C * K * K))))
-    bias = bn.up(bn.rand(C, 0.05))
+    xs, rs = bn.rand(n), bn.rand(n)
+    ws = bn.rand(C * C * K * K, math.sqrt(3.0 / (C * K * K)))
+    bs = bn.rand(C, 0.05)
+    x, r, w, bias = bn.up(xs), bn.up(rs), bn.up(ws), bn.up(bs)
     t1, t2, yn, yf = bn.out(n * 4), bn.out(n * 4), bn.out(n * 4), bn.out(n * 4)
     d = bn.d
 
@@ -181,8 +187,20 @@ def run_conv_bench(device: Optional[Device] = None, shape=None, on_progress=None
         call("di_conv2d", bn.dev.ctx, x.handle, w.handle, bias.handle, r.handle, yf.handle, B, C,
              C, H, W, K, 1, K // 2, DI_CONV_SILU, F32, NCHW)
 
-    return bn.finish(S, naive, fused, lambda: bn.read(yn, (n,)), lambda: bn.read(yf, (n,)), 3, 1,
-                     repeats, warm_ms, flops=2.0 * B * H * W * C * C * K * K)
+    kept = {}
+
+    def read_fused():
+        y = bn.read(yf, (n,))
+        if return_tensors:
+            kept["tensors"] = {"x": xs.reshape(B, C, H, W), "w": ws.reshape(C, C, K, K),
+                               "bias": bs, "r": rs.reshape(B, C, H, W),
+                               "y": y.reshape(B, C, H, W)}
+        return y
+
+    res = bn.finish(S, naive, fused, lambda: bn.read(yn, (n,)), read_fused, 3, 1,
+                    repeats, warm_ms, flops=2.0 * B * H * W * C * C * K * K)
+    res.update(kept)
+    return res
 
 
 # ---------------------------------------------------------------- ResNet --

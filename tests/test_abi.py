@@ -73,3 +73,27 @@ def test_create_without_gpu_fails_loudly():
     with pytest.raises(DiError) as e:
         Device(0)
     assert e.value.code == 3 and "no HIP device" in str(e.value)
+
+
+def _deno_table():
+    """{name: parameter count} of the Deno.dlopen table in INTEGRATION.md."""
+    src = open(os.path.join(REPO, "INTEGRATION.md")).read()
+    block = src[src.index("Deno.dlopen("):]
+    block = block[:block.index("\n})")]
+    return {m.group(1): len([p for p in m.group(2).split(",") if p.strip()])
+            for m in re.finditer(r"^\s*(di_\w+):\s*\{\s*parameters:\s*\[([^\]]*)\]", block, re.M)}
+
+
+def test_deno_table_matches_exports():
+    """The maintainer's FFI table names every exported entry point, and each
+    with the header prototype's parameter count."""
+    import subprocess
+    from drawinstant import _lib
+    table = _deno_table()
+    protos = _lib.parse_header()
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIBRARY], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if ln.split()[-1].startswith("di_")}
+    assert set(table) == exported == set(protos)
+    wrong = {n: (table[n], len(protos[n][1])) for n in table if table[n] != len(protos[n][1])}
+    assert not wrong, f"parameter counts differ (table, header): {wrong}"

@@ -115,6 +115,49 @@ def test_conv_fp32_stride2_batched_residual(dev, rng):
     assert max_rel(dev.download(y).reshape(ref.shape), ref + r) <= 1e-4
 
 
+def _silu_res_ref(x, wt, bias, r):
+    """fused-conv.js:206 evaluated by the oracle: conv (+bias) -> SiLU -> + r."""
+    conv = oracle.conv2d(x, wt, bias)
+    return oracle.unary("SiLU", conv.ravel()).reshape(conv.shape) + r
+
+
+@pytest.mark.parametrize("n,c,h,w", [
+    (1, 1280, 16, 16),   # fused-conv.js SHAPE
+    (1, 37, 11, 13),     # ragged: channels and both spatial dims off every tile
+    (2, 45, 7, 9),       # ragged, two images
+])
+def test_conv_silu_residual_epilogue_vs_oracle(dev, rng, n, c, h, w):
+    """di_conv2d with DI_CONV_SILU and a residual (the runConvBench fused
+    path, fp32 NCHW, exact fp32 MFMA) against oracle conv2d -> SiLU -> + r."""
+    x = rng.standard_normal((n, c, h, w)).astype(np.float32)
+    wt = (rng.standard_normal((c, c, 3, 3)) * math.sqrt(2.0 / (9 * c))).astype(np.float32)
+    bias = (rng.standard_normal(c) * 0.1).astype(np.float32)
+    r = rng.standard_normal((n, c, h, w)).astype(np.float32)
+    ref = _silu_res_ref(x, wt, bias, r)
+    y = dev.create_buffer(ref.nbytes)
+    _call(dev, "di_conv2d", dev.storage(x).handle, dev.storage(wt).handle, dev.storage(bias).handle,
+          dev.storage(r).handle, y.handle, n, c, c, h, w, 3, 1, 1, 4, F32, NCHW)  # 4 = DI_CONV_SILU
+    got = dev.download(y).reshape(ref.shape)
+    err = max_rel(got, ref)
+    print(f"[conv silu+res {n}x{c}x{h}x{w}] max-rel {err:.2e}", flush=True)
+    assert err <= 1e-4
+    # the epilogue is SiLU *then* the residual: a plain conv + r is far off
+    assert max_rel(oracle.conv2d(x, wt, bias) + r, ref) > 1e-2
+
+
+def test_run_conv_bench_output_vs_oracle(dev):
+    """The runConvBench entry point's own fused output (its seeded inputs at
+    the reference SHAPE [1,1280,16,16]) against the oracle composition."""
+    from drawinstant import fused
+    res = fused.run_conv_bench(dev, repeats=1, warm_ms=20.0, return_tensors=True)
+    t = res["tensors"]
+    ref = _silu_res_ref(t["x"], t["w"], t["bias"], t["r"])
+    err = max_rel(t["y"], ref)
+    print(f"[run_conv_bench] max-rel {err:.2e}", flush=True)
+    assert t["y"].shape == (1, 1280, 16, 16)
+    assert err <= 1e-4
+
+
 # ---------------- fp16 MFMA paths ----------------
 
 def _f16(a):

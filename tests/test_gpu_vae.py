@@ -48,8 +48,13 @@ def test_small_decoder_vs_oracle(small, B, h):
     assert got.shape == (B, 3, 8 * h, 8 * h) and e <= 1e-2
 
 
-def test_graph_replay_is_bit_identical(dev, small):
+@pytest.mark.parametrize("check", [False, True])
+def test_graph_replay_is_bit_identical(dev, small, monkeypatch, check):
+    """Replays equal the eager decode; with DI_GRAPH_CHECK=1 the captured
+    graph's nodes and, before each replay, its buffers are validated too."""
     v, _, _ = small
+    if check:
+        monkeypatch.setenv("DI_GRAPH_CHECK", "1")
     z = np.random.default_rng(9).standard_normal((1, 4, 8, 8)).astype(np.float32)
     bz = dev.storage(z)
     bi = dev.create_buffer(3 * 64 * 64 * 4)
