@@ -25,6 +25,9 @@ struct AttnArgs {
   // normalised fp16 outputs [rows][64] and (max, row sum) float pairs, where
   // rows = B * H * Sq enumerates (b, h, q) with q fastest
   uint32_t splits = 1;
+  // key groups inside a workgroup (1 or 2; set by run_attention, only
+  // without a split): see k_flash_attn
+  uint32_t key_groups = 1;
   uint64_t rows = 0;
   f16* part_o = nullptr;
   float* part_ml = nullptr;
@@ -36,6 +39,8 @@ struct Ctx;
 // the attention (and, when split, the merge) on the context's stream.
 int run_attention(Ctx* c, AttnArgs a, uint32_t B);
 uint32_t attn_splits(const Ctx* c, uint32_t B, uint32_t H, uint32_t Sq, uint32_t Skv);
+uint32_t attn_key_groups(const Ctx* c, uint32_t B, uint32_t H, uint32_t Sq, uint32_t Skv,
+                         uint32_t splits);
 // Enqueue with a.splits / a.rows / workspace already set.
 void launch_attention(const AttnArgs& a, uint32_t B, hipStream_t s);
 

@@ -36,6 +36,11 @@
 // descriptor ends at the head's last key: keys past Skv (cross-attention's
 // 77) land as zeros and are masked to -inf.
 //
+// Key groups: where the grid is small (the 32x32 level's 160 workgroups) a
+// workgroup runs two groups of four wavefronts on the same 64 queries, each
+// group walking half of the key tiles with its own K / V buffers, and merges
+// the two (max, row sum, output) triples through LDS at the end.
+//
 // KV split: a wave of 16 queries that walks all keys is the smallest unit of
 // work, and 64x64-latent self-attention has 1280 of them for 1024 SIMDs, so
 // some SIMDs would run two while most run one.  The keys are therefore split
@@ -110,10 +115,19 @@ __device__ __forceinline__ float sum_q4(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-__global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * BUF_BYTES];  // [buf][K | V]
+// KS (1 or 2) key groups of four wavefronts each (KS * 256 threads): the workgroup's
+// 64 queries are shared by every group, group kg walks its own contiguous
+// run of the key tiles with its own pair of K / V buffers, and the groups'
+// (max, row sum, output) are merged through LDS at the end.  KS = 1 is the
+// single-group kernel (which may be split over workgroups and merged by
+// k_attn_combine).
+template <int KS>
+__global__ __launch_bounds__(256 * KS, 4) void k_flash_attn(AttnArgs a, uint32_t nqb) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[KS * 2 * BUF_BYTES];  // [kg][buf][K | V]
 
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = KS == 1 ? tid >> 6 : __builtin_amdgcn_readfirstlane(tid >> 6) & 3u;
+  const uint32_t kg = KS == 1 ? 0u : __builtin_amdgcn_readfirstlane(tid >> 8);
   const uint32_t r = lane & 15, g = lane >> 4;
 
   // XCD-aware numbering: block i runs on XCD i % 8; give XCD x the x-th
@@ -158,7 +172,7 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
         make_rsrc(K + (uint64_t)key0 * a.ldk, (left - 1) * (uint32_t)a.ldk * 2u + D * 2);
     const __amdgpu_buffer_rsrc_t rV =
         make_rsrc(V + (uint64_t)key0 * a.ldv, (left - 1) * (uint32_t)a.ldv * 2u + D * 2);
-    unsigned char* base = smem + decltype(buf_c)::value * BUF_BYTES + wave * 16 * 128;
+    unsigned char* base = smem + (kg * 2 + decltype(buf_c)::value) * BUF_BYTES + wave * 16 * 128;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr)(base + i * 8 * 128), 16, dk[i], 0, 0, 0);
@@ -184,14 +198,22 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
   for (int dt = 0; dt < 4; dt++)
     v_rd[dt] = K_BYTES + v_off(4 * g + (r >> 2), 2 * dt + ((r & 3) >> 1)) + (r & 1) * 8;
 
-  // this workgroup's key tiles [t0, t1)
+  // this workgroup's key tiles [w0, w1); key group kg takes [t0, t1), the
+  // kg-th run of tpg tiles (the host picks KS so that no run is empty).  All
+  // groups make tpg iterations, so every wave meets the same barriers
   const int n_tiles = (int)((a.Skv + BKV - 1) / BKV);
   const int tps = (n_tiles + (int)a.splits - 1) / (int)a.splits;
-  const int t0 = (int)split * tps, t1 = min(t0 + tps, n_tiles);
+  const int w0 = (int)split * tps, w1 = min(w0 + tps, n_tiles);
+  const int tpg = KS == 1 ? w1 - w0 : (w1 - w0 + KS - 1) / KS;
+  const int t0 = w0 + (int)kg * tpg, t1 = KS == 1 ? w1 : min(t0 + tpg, w1);
 
   auto tile = [&](auto cur_c, int t) {
     constexpr int cur = decltype(cur_c)::value;
-    const unsigned char* sb = smem + cur * BUF_BYTES;
+    const unsigned char* sb = smem + (kg * 2 + cur) * BUF_BYTES;
+    if (KS > 1 && t >= t1) {  // this group's run is shorter: only the barrier
+      __syncthreads();
+      return;
+    }
     if (t + 1 < t1) dma_kv(t + 1, Int<cur ^ 1>{});
 
     // S' = K Q'^T - m
@@ -269,15 +291,60 @@ __global__ __launch_bounds__(256, 4) void k_flash_attn(AttnArgs a, uint32_t nqb)
     __syncthreads();
   };
 
-  dma_kv(t0, Int<0>{});
+  if (KS == 1 || t0 < t1) dma_kv(t0, Int<0>{});
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
   // two tiles per iteration so each LDS buffer has fixed offsets
-  for (int t = t0; t < t1; t += 2) {
-    tile(Int<0>{}, t);
-    if (t + 1 < t1) tile(Int<1>{}, t + 1);
+  for (int i = 0; i < tpg; i += 2) {
+    tile(Int<0>{}, t0 + i);
+    if (i + 1 < tpg) tile(Int<1>{}, t0 + i + 1);
   }
   l = sum_q4(l);
+  if constexpr (KS > 1) {
+    // merge the key groups: groups 1..KS-1 leave (m, row sum, unnormalised
+    // O) in LDS, lane by lane (float j of lane l at [slot][j][l]); group 0
+    // rescales every part to the largest max and adds them.  The K / V
+    // buffers are free: every group's last tile ended in a barrier after its
+    // loads completed
+    constexpr int NF = 18;  // o[4] (16 floats), m, l
+    float* xs = reinterpret_cast<float*>(smem);
+    if (kg > 0) {
+      float* dst = xs + ((kg - 1) * 4 + wave) * NF * 64 + lane;
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[(dt * 4 + i) * 64] = o[dt][i];
+      dst[16 * 64] = m;
+      dst[17 * 64] = l;
+    }
+    __syncthreads();
+    if (kg > 0) return;
+    float ms[KS], ls[KS];
+    ms[0] = m;
+    ls[0] = l;
+    float mx = m;
+#pragma unroll
+    for (int k = 1; k < KS; k++) {
+      const float* src = xs + ((k - 1) * 4 + wave) * NF * 64 + lane;
+      ms[k] = src[16 * 64];
+      ls[k] = src[17 * 64];
+      mx = fmaxf(mx, ms[k]);
+    }
+    float wk = __builtin_amdgcn_exp2f(m - mx);
+    l = ls[0] * wk;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) o[dt] *= wk;
+#pragma unroll
+    for (int k = 1; k < KS; k++) {
+      const float* src = xs + ((k - 1) * 4 + wave) * NF * 64 + lane;
+      wk = __builtin_amdgcn_exp2f(ms[k] - mx);
+      l += ls[k] * wk;
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[dt][i] += src[(dt * 4 + i) * 64] * wk;
+    }
+  }
   if (qrow < a.Sq) {
     const float inv = 1.0f / l;
     f16* dst = O + (uint64_t)qrow * a.ldo;
@@ -351,9 +418,34 @@ uint32_t attn_splits(const Ctx* c, uint32_t B, uint32_t H, uint32_t Sq, uint32_t
   return (n_tiles + tps - 1) / tps;
 }
 
+uint32_t attn_key_groups(const Ctx* c, uint32_t B, uint32_t H, uint32_t Sq, uint32_t Skv,
+                         uint32_t splits) {
+  // Two key groups inside a workgroup (64 KiB of LDS: two workgroups per CU)
+  // when the grid stays resident with them and each wave would otherwise
+  // walk 8 or more key tiles: the serial chain halves without a merge
+  // launch.  Measured per launch (one process, interleaved): 32x32-level
+  // self-attention (10 heads, 16 tiles) 10.9 -> 9.1 us, 8 tiles 7.2 ->
+  // 6.6 us; with 2 - 4 tiles (the cross-attentions, the 16x16 level) the
+  // extra waves and the merge cost 0.2 - 0.7 us, and four groups were no
+  // faster than two at 16 tiles and slower at 8.  Larger grids with more
+  // tiles take the key-range split over workgroups instead (attn_splits).
+  if (splits > 1) return 1;
+  const uint32_t blocks = ((Sq + 63) / 64) * H * B, n = (Skv + BKV - 1) / BKV;
+  uint32_t ks = n >= 8 && blocks <= 2u * (uint32_t)c->num_cus ? 2u : 1u;
+  // tuning override: DI_ATTN_KGROUPS=1|2, read per call so that one process
+  // can time both
+  if (const char* env = getenv("DI_ATTN_KGROUPS")) {
+    const uint32_t want = (uint32_t)atoi(env);
+    if ((want == 1 || want == 2) && want <= n) ks = want;
+  }
+  return ks;
+}
+
 void launch_attention(const AttnArgs& a, uint32_t B, hipStream_t s) {
   const uint32_t nqb = (a.Sq + 63) / 64;
-  k_flash_attn<<<dim3(nqb * a.H * B * a.splits), 256, 0, s>>>(a, nqb);
+  const dim3 grid(nqb * a.H * B * a.splits);
+  if (a.splits == 1 && a.key_groups == 2) k_flash_attn<2><<<grid, 512, 0, s>>>(a, nqb);
+  else k_flash_attn<1><<<grid, 256, 0, s>>>(a, nqb);
   const dim3 cg((uint32_t)((a.rows * 8 + 255) / 256));
   switch (a.splits) {
     case 1: break;
@@ -384,6 +476,7 @@ int run_attention(Ctx* c, AttnArgs a, uint32_t B) {
     const uint32_t tps = (n_tiles + sp - 1) / sp;
     a.splits = (n_tiles + tps - 1) / tps;
   }
+  a.key_groups = attn_key_groups(c, B, a.H, a.Sq, a.Skv, a.splits);
   a.rows = (uint64_t)B * a.H * a.Sq;
   void* ws = nullptr;
   uint64_t cap = 0;

@@ -92,6 +92,33 @@ def test_attn_rising_scores_fp16(dev, rng, B, H, Sq, Skv, growth):
     assert _attn_case(dev, rng, B, H, Sq, Skv, BSHD, F16, "di_attn_cross", qkv=(q, k, v)) <= 2e-3
 
 
+@pytest.mark.parametrize("B,H,Sq,Skv,layout", [
+    (1, 3, 128, 499, BSHD),    # 8 key tiles over 2 key groups (4/4), last tile 51 keys
+    (2, 2, 96, 571, BHSD),     # 9 tiles: groups of 5 and 4, partial query block, batch 2
+    (1, 4, 64, 1983, BSHD),    # 31 tiles (16/15), last tile 63 keys
+    (1, 10, 1024, 1024, BSHD), # the 32x32 level in the U-Net's token-major layout: 2 x 8 tiles
+])
+def test_attn_key_groups_fp16(dev, rng, B, H, Sq, Skv, layout):
+    """Small grids with 8 - 31 key tiles split each workgroup's keys over
+    two groups of four wavefronts, merged in LDS: odd tile counts give the
+    groups unequal runs, and the shorter one idles through barriers."""
+    print(f"[attn key groups] B={B} H={H} Sq={Sq} Skv={Skv} layout={layout}", flush=True)
+    assert _attn_case(dev, rng, B, H, Sq, Skv, layout, F16, "di_attn_cross") <= 2e-3
+
+
+@pytest.mark.parametrize("Skv,growth", [(900, 6.0), (571, 12.0)])
+def test_attn_key_groups_rising_scores_fp16(dev, rng, Skv, growth):
+    """Rising key norms inside key groups: each group raises its own running
+    max, and the LDS merge rescales the groups' parts to the largest."""
+    B, H, Sq = 1, 2, 128
+    print(f"[attn key groups rising] Skv={Skv} growth={growth}", flush=True)
+    q = rng.standard_normal((B, Sq, H, 64))
+    ramp = 1.0 + growth * (np.arange(Skv) / max(1, Skv - 1))
+    k = rng.standard_normal((B, Skv, H, 64)) * ramp[None, :, None, None]
+    v = rng.standard_normal((B, Skv, H, 64))
+    assert _attn_case(dev, rng, B, H, Sq, Skv, BSHD, F16, "di_attn_cross", qkv=(q, k, v)) <= 2e-3
+
+
 def test_attn_fp32_tensors_and_explicit_scale(dev, rng):
     assert _attn_case(dev, rng, 1, 4, 200, 200, BHSD, F32, "di_attn_self", scale=0.05) <= 2e-3
 
