@@ -278,6 +278,77 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
   }
 }
 
+// The U-Net's conv_in: 3x3, stride 1, pad 1, from the NCHW fp32 latent
+// (CIN channels, here 4) to NHWC fp16 with the bias added, and the
+// GroupNorm statistics of the stored values per 64-pixel chunk and channel
+// (the layout gemm_tile_stats writes: stats[(chunk * Cout + c) * 2 + {0, 1}],
+// rows summed in order).  K = 9 * CIN is too short for the MFMA paths to pay
+// (the implicit GEMM took 10 us behind a separate NCHW -> NHWC pass, and
+// wrote no statistics, so both GroupNorms that read conv_in's output ran a
+// statistics pass of their own).  Workgroup (chunk, 32-channel slice): lane
+// = pixel, each wave 8 channels; the 36 inputs of a pixel come straight from
+// the NCHW tensor (zero outside the image), the slice's weights through LDS.
+constexpr int CI_CS = 32, CI_CPW = 8, CI_LDY = CI_CS + 8;
+
+template <int CIN>
+__global__ __launch_bounds__(256) void k_conv_in(const float* __restrict__ x,
+                                                 const f16* __restrict__ w,
+                                                 const float* __restrict__ bias,
+                                                 f16* __restrict__ y, float* __restrict__ stats,
+                                                 uint32_t cin_p, uint32_t Cout, uint32_t H,
+                                                 uint32_t W) {
+  __shared__ float sw[CI_CS * 9 * CIN];                        // [co][tap][ci]
+  __shared__ __attribute__((aligned(16))) f16 sy[64 * CI_LDY];  // [pixel][co]
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t chunk = blockIdx.x, c0 = blockIdx.y * CI_CS;
+  const uint32_t HW = H * W, pg = chunk * 64 + lane;  // global pixel (HW % 64 == 0)
+  const uint32_t img = pg / HW, p = pg % HW;
+  const int py = (int)(p / W), px = (int)(p % W);
+  for (uint32_t i = tid; i < CI_CS * 9 * CIN; i += 256) {
+    const uint32_t co = i / (9 * CIN), r = i % (9 * CIN), tap = r / CIN, ci = r % CIN;
+    sw[i] = (float)w[((uint64_t)(c0 + co) * 9 + tap) * cin_p + ci];
+  }
+  float xin[9][CIN];
+#pragma unroll
+  for (int tap = 0; tap < 9; tap++) {
+    const int yy = py + tap / 3 - 1, xx = px + tap % 3 - 1;
+    const bool ok = yy >= 0 && yy < (int)H && xx >= 0 && xx < (int)W;
+#pragma unroll
+    for (int ci = 0; ci < CIN; ci++)
+      xin[tap][ci] = ok ? x[(((uint64_t)img * CIN + ci) * H + yy) * W + xx] : 0.0f;
+  }
+  __syncthreads();
+  const uint32_t cw = wave * CI_CPW;
+#pragma unroll
+  for (int j = 0; j < CI_CPW; j++) {
+    const float* wj = sw + (cw + j) * 9 * CIN;
+    float acc = bias[c0 + cw + j];
+#pragma unroll
+    for (int tap = 0; tap < 9; tap++)
+#pragma unroll
+      for (int ci = 0; ci < CIN; ci++) acc += xin[tap][ci] * wj[tap * CIN + ci];
+    sy[lane * CI_LDY + cw + j] = (f16)acc;
+  }
+  __syncthreads();
+  {
+    const uint32_t pix = tid >> 2, v = tid & 3;  // 64 pixels x 4 vectors of 8
+    *(f16x8*)(y + ((uint64_t)chunk * 64 + pix) * Cout + c0 + v * 8) =
+        *(const f16x8*)&sy[pix * CI_LDY + v * 8];
+  }
+  if (stats && tid < CI_CS) {
+    float s = 0.0f, q = 0.0f;
+    for (int r = 0; r < 64; r++) {
+      const float v = (float)sy[r * CI_LDY + tid];
+      s += v;
+      q += v * v;
+    }
+    float* st = stats + ((uint64_t)chunk * Cout + c0 + tid) * 2;
+    st[0] = s;
+    st[1] = q;
+  }
+}
+
 template <int W>
 void launch_w(const GemmArgs& g, hipStream_t s) {
   const uint32_t tiles = (g.M / CV_BM) * (g.N / CV_BN);
@@ -295,6 +366,18 @@ bool conv3_halo_ok(const GemmArgs& g) {
          (TW == 16 || TW == 32 || TW == 64 || TW == 128) && Wo % TW == 0 &&
          g.Ho % (CV_BM / TW) == 0 && g.M % CV_BM == 0 && g.batch == 1 && g.b_vec_ok &&
          g.a_bytes > 0 && g.b_bytes > 0 && (single || g.a2_bytes > 0) && g.K == 9 * g.Cin;
+}
+
+bool conv_in_direct_ok(uint32_t Cin, uint32_t Cout, uint32_t H, uint32_t W) {
+  return Cin == 4 && Cout % CI_CS == 0 && (H * W) % 64 == 0;
+}
+
+void launch_conv_in(hipStream_t s, const float* x, const f16* w, const float* bias, f16* y,
+                    float* stats, uint32_t B, uint32_t Cin, uint32_t cin_p, uint32_t Cout,
+                    uint32_t H, uint32_t W) {
+  (void)Cin;  // conv_in_direct_ok: 4
+  k_conv_in<4><<<dim3(B * H * W / 64, Cout / CI_CS), 256, 0, s>>>(x, w, bias, y, stats, cin_p,
+                                                                  Cout, H, W);
 }
 
 void launch_conv3_halo(const GemmArgs& g, hipStream_t s) {

@@ -17,6 +17,7 @@
 // every attn2 to_k/to_v pair stacked into one [sum 2C][1024] matrix (all
 // transformers' context projections are one GEMM per step), biases and norm
 // affines fp32.  di_unet_param_info describes each tensor.
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -341,15 +342,21 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   const uint32_t G = cf.groups;
   const uint32_t cin_p = (cf.in_channels + 7) / 8 * 8;
   // inputs: sample NCHW fp32 -> NHWC fp16 (channels padded), context -> fp16
+  // conv_in reads the NCHW latent itself where its direct kernel applies
+  // (DI_CONV_IN_DIRECT=0 selects the layout pass + implicit GEMM, for A/B runs)
+  const char* env_ci = getenv("DI_CONV_IN_DIRECT");
+  const bool ci_direct = (!env_ci || atoi(env_ci) != 0) &&
+                         conv_in_direct_ok(cf.in_channels, cf.block_channels[0], H, W);
   Scratch x16, ctx16, th, temb, tproj;
-  int rc = x16.alloc(c, (uint64_t)B * H * W * cin_p * 2);
+  int rc = ci_direct ? 0 : x16.alloc(c, (uint64_t)B * H * W * cin_p * 2);
   if (!rc) rc = ctx16.alloc(c, (uint64_t)B * Sctx * cf.cross_dim * 2);
   if (!rc) rc = th.alloc(c, (uint64_t)B * cf.time_dim * 4);
   if (!rc) rc = temb.alloc(c, (uint64_t)B * cf.time_dim * 4);
   if (!rc) rc = tproj.alloc(c, (uint64_t)B * u.temb_rows * 4);
   if (rc) return rc;
-  launch_layout(c->stream, sample, DI_F32, DI_NCHW, x16.p, DI_F16, DI_NHWC, B, cf.in_channels, H,
-                W, cin_p);
+  if (!ci_direct)
+    launch_layout(c->stream, sample, DI_F32, DI_NCHW, x16.p, DI_F16, DI_NHWC, B, cf.in_channels,
+                  H, W, cin_p);
   launch_convert(c->stream, context, DI_F32, ctx16.p, DI_F16, (uint64_t)B * Sctx * cf.cross_dim);
   // every transformer's attn2 K / V of the context: one GEMM over the
   // stacked [kv_rows][cross] weights -> kvall [B*Sctx][kv_rows]
@@ -452,7 +459,12 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   Act hcur;
   rc = act_alloc(hcur, hh, ww, ch);
   if (rc) return rc;
-  {
+  if (ci_direct) {
+    launch_conv_in(c->stream, sample, u.h(u.conv_in_w), u.f(u.conv_in_b), hcur.buf.h(),
+                   hcur.st.f(), B, cf.in_channels, cin_p, ch, hh, ww);
+    hcur.so.done = hcur.st.f() != nullptr;
+    st_done(hcur);
+  } else {
     ConvCall cc;
     cc.x = one(x16.h(), cin_p);
     cc.B = B;
