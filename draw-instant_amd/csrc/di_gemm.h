@@ -118,14 +118,13 @@ inline uint32_t gemm_extent(uint64_t bytes) { return bytes < 0x7fff0000ull ? (ui
 // channel chunks writes partials for the split-K reducer).
 bool conv3_halo_ok(const GemmArgs& g);
 void launch_conv3_halo(const GemmArgs& g, hipStream_t s);
-// The U-Net's conv_in as a direct kernel from the NCHW fp32 latent to NHWC
-// fp16 [B*H*W][Cout] (+bias), with GroupNorm statistics per 64-pixel chunk
-// and channel into stats (may be null).  Weights OHWI fp16 with cin_p
-// channels per tap.
+// The U-Net's conv_in as a direct kernel from the NCHW fp32 latent (4
+// channels) to NHWC fp16 [B*H*W][Cout] (+bias), with GroupNorm statistics
+// per 64-pixel chunk and channel into stats (may be null).  Weights OHWI
+// fp16 with the input channels padded to 8 per tap.
 bool conv_in_direct_ok(uint32_t Cin, uint32_t Cout, uint32_t H, uint32_t W);
-void launch_conv_in(hipStream_t s, const float* x, const _Float16* w, const float* bias, _Float16* y,
-                    float* stats, uint32_t B, uint32_t Cin, uint32_t cin_p, uint32_t Cout,
-                    uint32_t H, uint32_t W);
+void launch_conv_in(hipStream_t s, const float* x, const _Float16* w, const float* bias,
+                    _Float16* y, float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W);
 // elem: DI_F16 or DI_F32 operand element type.
 void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s);
 // Whether launch_gemm can produce g.stats for this call: buffer-load fp16

@@ -281,54 +281,92 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
 // The U-Net's conv_in: 3x3, stride 1, pad 1, from the NCHW fp32 latent
 // (CIN channels, here 4) to NHWC fp16 with the bias added, and the
 // GroupNorm statistics of the stored values per 64-pixel chunk and channel
-// (the layout gemm_tile_stats writes: stats[(chunk * Cout + c) * 2 + {0, 1}],
-// rows summed in order).  K = 9 * CIN is too short for the MFMA paths to pay
-// (the implicit GEMM took 10 us behind a separate NCHW -> NHWC pass, and
-// wrote no statistics, so both GroupNorms that read conv_in's output ran a
-// statistics pass of their own).  Workgroup (chunk, 32-channel slice): lane
-// = pixel, each wave 8 channels; the 36 inputs of a pixel come straight from
-// the NCHW tensor (zero outside the image), the slice's weights through LDS.
-constexpr int CI_CS = 32, CI_CPW = 8, CI_LDY = CI_CS + 8;
+// (the layout gemm_tile_stats writes: stats[(chunk * Cout + c) * 2 + {0, 1}]).
+// The implicit GEMM took 10 us behind a separate NCHW -> NHWC pass and wrote
+// no statistics, so both GroupNorms that read conv_in's output ran a
+// statistics pass of their own.  Here the MFMA k index is (tap, channel)
+// with the channels padded to 8 - exactly the OHWI weight layout - so a
+// lane's B fragment is one 16-byte weight vector and its A fragment one
+// tap of one pixel, read from the NCHW tensor (zero outside the image) and
+// rounded to fp16 as the GEMM path's layout pass did; 3 k steps of 4 taps
+// (the last holding tap 8 only).  Workgroup (64-pixel chunk, 32 channels):
+// wave w takes pixels 16w .. 16w + 15, two 16-channel blocks.
+constexpr int CI_CS = 32, CI_LDY = CI_CS + 8;
 
 template <int CIN>
 __global__ __launch_bounds__(256) void k_conv_in(const float* __restrict__ x,
                                                  const f16* __restrict__ w,
                                                  const float* __restrict__ bias,
                                                  f16* __restrict__ y, float* __restrict__ stats,
-                                                 uint32_t cin_p, uint32_t Cout, uint32_t H,
-                                                 uint32_t W) {
-  __shared__ float sw[CI_CS * 9 * CIN];                        // [co][tap][ci]
+                                                 uint32_t Cout, uint32_t H, uint32_t W) {
+  static_assert(CIN <= 8, "weights padded to 8 channels per tap");
   __shared__ __attribute__((aligned(16))) f16 sy[64 * CI_LDY];  // [pixel][co]
+  __shared__ float sst[4][CI_CS][2];                             // per-wave channel sums
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t chunk = blockIdx.x, c0 = blockIdx.y * CI_CS;
-  const uint32_t HW = H * W, pg = chunk * 64 + lane;  // global pixel (HW % 64 == 0)
-  const uint32_t img = pg / HW, p = pg % HW;
+  const uint32_t HW = H * W;
+  // a chunk lies in one image (HW % 64 == 0)
+  const uint32_t img = __builtin_amdgcn_readfirstlane(chunk * 64 / HW);
+  const uint32_t p0 = chunk * 64 - img * HW;
+  const uint32_t r = lane & 15, g = lane >> 4;
+  // A: pixel p0 + 16 wave + r, tap 4 ks + g
+  const uint32_t p = p0 + wave * 16 + r;
   const int py = (int)(p / W), px = (int)(p % W);
-  for (uint32_t i = tid; i < CI_CS * 9 * CIN; i += 256) {
-    const uint32_t co = i / (9 * CIN), r = i % (9 * CIN), tap = r / CIN, ci = r % CIN;
-    sw[i] = (float)w[((uint64_t)(c0 + co) * 9 + tap) * cin_p + ci];
-  }
-  float xin[9][CIN];
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(x + (uint64_t)img * CIN * HW), (short)0, (int)(CIN * HW * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<f16*>(w), (short)0, (int)(Cout * 72 * 2), 0x00020000);
+  float xa[3][CIN];
+  f16x8 bf[3][2];
 #pragma unroll
-  for (int tap = 0; tap < 9; tap++) {
+  for (int ks = 0; ks < 3; ks++) {
+    const int tap = ks * 4 + (int)g;
     const int yy = py + tap / 3 - 1, xx = px + tap % 3 - 1;
-    const bool ok = yy >= 0 && yy < (int)H && xx >= 0 && xx < (int)W;
+    const bool ok = tap < 9 && yy >= 0 && yy < (int)H && xx >= 0 && xx < (int)W;
+    const uint32_t off = ok ? (uint32_t)(yy * (int)W + xx) * 4u : 0x80000000u;
 #pragma unroll
     for (int ci = 0; ci < CIN; ci++)
-      xin[tap][ci] = ok ? x[(((uint64_t)img * CIN + ci) * H + yy) * W + xx] : 0.0f;
+      xa[ks][ci] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, (int)(ci * HW * 4), 0));
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const uint32_t co = c0 + nb * 16 + r;
+      const uint32_t woff = tap < 9 ? (co * 72 + (uint32_t)tap * 8) * 2 : 0x80000000u;
+      bf[ks][nb] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rw, woff, 0, 0));
+    }
   }
-  __syncthreads();
-  const uint32_t cw = wave * CI_CPW;
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-  for (int j = 0; j < CI_CPW; j++) {
-    const float* wj = sw + (cw + j) * 9 * CIN;
-    float acc = bias[c0 + cw + j];
+  for (int ks = 0; ks < 3; ks++) {
+    f16x8 af = {};
 #pragma unroll
-    for (int tap = 0; tap < 9; tap++)
+    for (int ci = 0; ci < CIN; ci++) af[ci] = (f16)xa[ks][ci];
 #pragma unroll
-      for (int ci = 0; ci < CIN; ci++) acc += xin[tap][ci] * wj[tap * CIN + ci];
-    sy[lane * CI_LDY + cw + j] = (f16)acc;
+    for (int nb = 0; nb < 2; nb++)
+      acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[ks][nb], acc[nb], 0, 0, 0);
+  }
+  // C: lane holds pixels 16 wave + 4 g + i, channel 16 nb + r
+#pragma unroll
+  for (int nb = 0; nb < 2; nb++) {
+    const uint32_t cl = nb * 16 + r;
+    const float b = bias[c0 + cl];
+    float s = 0.0f, q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const f16 h = (f16)(acc[nb][i] + b);
+      sy[(wave * 16 + g * 4 + i) * CI_LDY + cl] = h;
+      s += (float)h;
+      q += (float)h * (float)h;
+    }
+    s += __shfl_xor(s, 16);
+    q += __shfl_xor(q, 16);
+    s += __shfl_xor(s, 32);
+    q += __shfl_xor(q, 32);
+    if (g == 0) {
+      sst[wave][cl][0] = s;
+      sst[wave][cl][1] = q;
+    }
   }
   __syncthreads();
   {
@@ -337,15 +375,9 @@ __global__ __launch_bounds__(256) void k_conv_in(const float* __restrict__ x,
         *(const f16x8*)&sy[pix * CI_LDY + v * 8];
   }
   if (stats && tid < CI_CS) {
-    float s = 0.0f, q = 0.0f;
-    for (int r = 0; r < 64; r++) {
-      const float v = (float)sy[r * CI_LDY + tid];
-      s += v;
-      q += v * v;
-    }
-    float* st = stats + ((uint64_t)chunk * Cout + c0 + tid) * 2;
-    st[0] = s;
-    st[1] = q;
+    const float s = (sst[0][tid][0] + sst[1][tid][0]) + (sst[2][tid][0] + sst[3][tid][0]);
+    const float q = (sst[0][tid][1] + sst[1][tid][1]) + (sst[2][tid][1] + sst[3][tid][1]);
+    *(float2*)(stats + ((uint64_t)chunk * Cout + c0 + tid) * 2) = float2{s, q};
   }
 }
 
@@ -373,11 +405,9 @@ bool conv_in_direct_ok(uint32_t Cin, uint32_t Cout, uint32_t H, uint32_t W) {
 }
 
 void launch_conv_in(hipStream_t s, const float* x, const f16* w, const float* bias, f16* y,
-                    float* stats, uint32_t B, uint32_t Cin, uint32_t cin_p, uint32_t Cout,
-                    uint32_t H, uint32_t W) {
-  (void)Cin;  // conv_in_direct_ok: 4
-  k_conv_in<4><<<dim3(B * H * W / 64, Cout / CI_CS), 256, 0, s>>>(x, w, bias, y, stats, cin_p,
-                                                                  Cout, H, W);
+                    float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W) {
+  k_conv_in<4><<<dim3(B * H * W / 64, Cout / CI_CS), 256, 0, s>>>(x, w, bias, y, stats, Cout, H,
+                                                                  W);
 }
 
 void launch_conv3_halo(const GemmArgs& g, hipStream_t s) {

@@ -461,7 +461,7 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   if (rc) return rc;
   if (ci_direct) {
     launch_conv_in(c->stream, sample, u.h(u.conv_in_w), u.f(u.conv_in_b), hcur.buf.h(),
-                   hcur.st.f(), B, cf.in_channels, cin_p, ch, hh, ww);
+                   hcur.st.f(), B, ch, hh, ww);
     hcur.so.done = hcur.st.f() != nullptr;
     st_done(hcur);
   } else {

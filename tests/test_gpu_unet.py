@@ -79,14 +79,14 @@ def test_small_unet_narrow_tile_vs_oracle(dev, rng, monkeypatch):
         u.destroy()
 
 
-@pytest.mark.parametrize("var,tol", [("DI_CONV_IN_DIRECT", 3e-3)])
+@pytest.mark.parametrize("var,tol", [("DI_CONV_IN_DIRECT", 5e-4)])
 @pytest.mark.parametrize("B,H,W", [(1, 16, 16), (2, 8, 24)])
 def test_edge_convs_direct_match_implicit_gemm(dev, rng, monkeypatch, var, tol, B, H, W):
     """The direct conv_in kernel (NCHW fp32 latent in, GroupNorm statistics
     out) against the layout pass + implicit-GEMM conv it replaces, over a
-    whole narrow U-Net step, and both against the oracle.  The direct kernel
-    keeps the fp32 inputs (the other path rounds them to fp16 first), so the
-    two agree to that rounding, not bit for bit."""
+    whole narrow U-Net step, and both against the oracle.  Both round the
+    latent to fp16 and accumulate in fp32, in another order, so they agree
+    to rounding, not bit for bit."""
     from drawinstant.unet import UNet, UNetConfig
     cfg = UNetConfig.small()
     u = UNet(dev, cfg, seed=7)
