@@ -38,15 +38,45 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
   }
 }
 
-// Sum of the split-K partials of 8 columns of row m, in split order.
-__device__ __forceinline__ void sum_splits8(const GemmArgs& g, uint32_t bz, uint32_t m, uint32_t n,
+// The split-K partials of 8 columns of row m: the first 8 splits' loads are
+// issued by splits8_load (with the epilogue operands, before anything is
+// consumed, so one memory round trip covers them all) and summed by
+// splits8_sum in split order, further splits by a loop there.
+struct Parts8 {
+  f32x4 t[8][2];
+};
+
+__device__ __forceinline__ const float* part_row(const GemmArgs& g, uint32_t bz, uint32_t m,
+                                                 uint32_t n) {
+  return g.part + (uint64_t)bz * g.M * g.N + (uint64_t)m * g.N + n;
+}
+
+__device__ __forceinline__ void splits8_load(const GemmArgs& g, const float* p, Parts8& P) {
+  const uint64_t step = (uint64_t)g.batch * g.M * g.N;
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    const uint32_t sp = (uint32_t)u < g.splits ? (uint32_t)u : 0u;
+    P.t[u][0] = ld4(p + sp * step);
+    P.t[u][1] = ld4(p + sp * step + 4);
+  }
+}
+
+__device__ __forceinline__ void splits8_sum(const GemmArgs& g, const float* p, const Parts8& P,
                                             float* out) {
-  const uint64_t mn = (uint64_t)g.M * g.N;
-  const float* p = g.part + (uint64_t)bz * mn + (uint64_t)m * g.N + n;
-  const uint64_t step = (uint64_t)g.batch * mn;
+  const uint64_t step = (uint64_t)g.batch * g.M * g.N;
 #pragma unroll
   for (int j = 0; j < 8; j++) out[j] = 0.0f;
-  for (uint32_t s0 = 0; s0 < g.splits; s0 += 8) {
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    if ((uint32_t)u < g.splits) {  // uniform
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        out[j] += P.t[u][0][j];
+        out[j + 4] += P.t[u][1][j];
+      }
+    }
+  }
+  for (uint32_t s0 = 8; s0 < g.splits; s0 += 8) {
     f32x4 t[8][2];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
@@ -69,33 +99,58 @@ __device__ __forceinline__ void sum_splits8(const GemmArgs& g, uint32_t bz, uint
 
 // One output vector of the split-K reduction + epilogue (vec_epi): row m,
 // output columns c8 .. c8 + 7 (with GEGLU, of the N / 2 combined columns).
-// The stored fp16 values are returned in v as floats.
+// Every load (partials, LayerNorm row statistics and column sums, bias,
+// temb bias, residual) is issued before any is consumed.  The stored fp16
+// values are returned in v as floats.
 __device__ __forceinline__ void splitk_vec8(const GemmArgs& g, uint32_t bz, uint32_t m, uint32_t c8,
                                             float* v) {
   f16* C = (f16*)g.c + (uint64_t)bz * g.sc + (uint64_t)m * g.ldc + c8;
   const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr + (uint64_t)m * g.ldr + c8;
   float x[8];
   float mean = 0.0f, rstd = 0.0f;
-  if (g.ln_rows) ln_coef(g, m, mean, rstd);
+  float2 lv[kLnBatch];
   if (g.act == ACT_GEGLU) {
     const uint32_t nh = (c8 / 16) * 32 + c8 % 16;
-    float gt[8];
-    sum_splits8(g, bz, m, nh, x);
-    sum_splits8(g, bz, m, nh + 16, gt);
+    const float* ph = part_row(g, bz, m, nh);
+    const float* pg = part_row(g, bz, m, nh + 16);
+    Parts8 Ph, Pg;
+    splits8_load(g, ph, Ph);
+    splits8_load(g, pg, Pg);
+    f32x4 sh[2] = {}, sg[2] = {}, bh[2] = {}, bg[2] = {};
+    if (g.bias) {
+      bh[0] = ld4(g.bias + nh);
+      bh[1] = ld4(g.bias + nh + 4);
+      bg[0] = ld4(g.bias + nh + 16);
+      bg[1] = ld4(g.bias + nh + 20);
+    }
+    // the LayerNorm loads last: the compiler may start their reduction inside
+    // this branch, and a wait there must find every other load in flight
     if (g.ln_rows) {
-      const f32x4 sh[2] = {ld4(g.ln_s + nh), ld4(g.ln_s + nh + 4)};
-      const f32x4 sg[2] = {ld4(g.ln_s + nh + 16), ld4(g.ln_s + nh + 20)};
+      sh[0] = ld4(g.ln_s + nh);
+      sh[1] = ld4(g.ln_s + nh + 4);
+      sg[0] = ld4(g.ln_s + nh + 16);
+      sg[1] = ld4(g.ln_s + nh + 20);
+      ln_load(g, m, lv);
+    }
+    float gt[8];
+    splits8_sum(g, ph, Ph, x);
+    splits8_sum(g, pg, Pg, gt);
+    if (g.ln_rows) {
+      ln_reduce(g, m, lv, mean, rstd);
       ln_fold8(x, mean, rstd, sh);
       ln_fold8(gt, mean, rstd, sg);
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const float hv = x[j] * g.alpha + (g.bias ? g.bias[nh + j] : 0.0f);
-      const float gv = gt[j] * g.alpha + (g.bias ? g.bias[nh + 16 + j] : 0.0f);
+      const float hv = x[j] * g.alpha + bh[j >> 2][j & 3];
+      const float gv = gt[j] * g.alpha + bg[j >> 2][j & 3];
       x[j] = hv * gelu_erf_f(gv);
     }
   } else {
-    f32x4 bb[2] = {}, tb[2] = {};
+    const float* pp = part_row(g, bz, m, c8);
+    Parts8 P;
+    splits8_load(g, pp, P);
+    f32x4 bb[2] = {}, tb[2] = {}, ls[2] = {};
     if (g.bias) {
       bb[0] = ld4(g.bias + c8);
       bb[1] = ld4(g.bias + c8 + 4);
@@ -105,18 +160,27 @@ __device__ __forceinline__ void splitk_vec8(const GemmArgs& g, uint32_t bz, uint
       tb[0] = ld4(tp);
       tb[1] = ld4(tp + 4);
     }
-    sum_splits8(g, bz, m, c8, x);
+    f16x8 rv = {};
+    if (g.res) rv = *(const f16x8*)R;
+    // the LayerNorm loads last (see the GEGLU branch)
     if (g.ln_rows) {
-      const f32x4 ls[2] = {ld4(g.ln_s + c8), ld4(g.ln_s + c8 + 4)};
+      ls[0] = ld4(g.ln_s + c8);
+      ls[1] = ld4(g.ln_s + c8 + 4);
+      ln_load(g, m, lv);
+    }
+    splits8_sum(g, pp, P, x);
+    if (g.ln_rows) {
+      ln_reduce(g, m, lv, mean, rstd);
       ln_fold8(x, mean, rstd, ls);
     }
     epi_math8(g, x, bb, tb);
+    if (g.res)
+#pragma unroll
+      for (int j = 0; j < 8; j++) x[j] += (float)rv[j];
   }
-  f16x8 rv = {};
-  if (g.res) rv = *(const f16x8*)R;
   f16x8 o;
 #pragma unroll
-  for (int j = 0; j < 8; j++) o[j] = (f16)(g.res ? x[j] + (float)rv[j] : x[j]);
+  for (int j = 0; j < 8; j++) o[j] = (f16)x[j];
   *(f16x8*)C = o;
 #pragma unroll
   for (int j = 0; j < 8; j++) v[j] = (float)o[j];

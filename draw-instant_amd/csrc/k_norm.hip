@@ -495,39 +495,69 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
   const uint32_t c = c0 + v * 8;
   const uint32_t p0 = blockIdx.x * ppb, p1 = min(p0 + ppb, HW);
   const uint64_t pix0 = (uint64_t)n * HW;
+  // per channel: sums over the image's chunks.  Thread t takes channel quad
+  // t % Q (4 channels x 2 statistics = two 16-byte loads per chunk) and the
+  // chunks k = t / Q, + KL, ... (all loads in flight at once); the KL chunk
+  // lanes are then added in lane order.  The first batch of eight chunks
+  // (all of them at U-Net sizes) is issued before the pixel and gamma / beta
+  // loads in straight-line code, so neither memory round trip waits for the
+  // other; a loop over further chunks would wait for every load at its top.
+  __shared__ float fold[256 * 8];
+  const uint32_t Q = SW / 4, KL = 256 / Q;
+  const uint32_t qd = tid % Q, kl = tid / Q, cq = c0 + qd * 4;
+  const bool sfirst = cq < st.c1;  // 4-channel quads never straddle c1 (c1 % 8 == 0)
+  const uint64_t sld = sfirst ? st.ld1 : st.ld2;
+  const float* sp = (sfirst ? st.s1 : st.s2) + ((uint64_t)n * cpi * sld + (sfirst ? cq : cq - st.c1)) * 2;
+  // Every thread issues these loads (threads without a chunk / pixel share
+  // in-range addresses and drop the results): a load under a branch makes
+  // the compiler wait for all loads where the branch rejoins.
+  f32x4 t0[8][2];
+  {
+    // chunk lanes past KL or past the image's cpi chunks read chunk 0
+    const uint32_t klc = kl < KL ? kl : 0u;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint32_t k = klc + u * KL < cpi ? klc + u * KL : 0u;
+      t0[u][0] = *(const f32x4*)(sp + (uint64_t)k * sld * 2);
+      t0[u][1] = *(const f32x4*)(sp + (uint64_t)k * sld * 2 + 4);
+    }
+  }
+  // loads retire in order: keep the statistics (needed first) ahead
+  sched_fence();
   constexpr int U = 4;
   f16x8 pre[U];
   f32x4 gmv[2], btv[2];
-  if (act) {
+  {
+    const uint32_t lc = act ? lane : 0u;
 #pragma unroll
-    for (int u = 0; u < U; u++) pre[u] = x.load8(pix0 + min(p0 + lane + u * R, p1 - 1), c);
+    for (int u = 0; u < U; u++) pre[u] = x.load8(pix0 + min(p0 + lc + u * R, p1 - 1), c);
     gmv[0] = *(const f32x4*)(gamma + c);
     gmv[1] = *(const f32x4*)(gamma + c + 4);
     btv[0] = *(const f32x4*)(beta + c);
     btv[1] = *(const f32x4*)(beta + c + 4);
   }
-  // per channel: sums over the image's chunks.  Thread t takes channel quad
-  // t % Q (4 channels x 2 statistics = two 16-byte loads per chunk) and the
-  // chunks k = t / Q, + KL, ... (all loads in flight at once); the KL chunk
-  // lanes are then added in lane order.
-  __shared__ float fold[256 * 8];
-  const uint32_t Q = SW / 4, KL = 256 / Q;
+  sched_fence();
   {
-    const uint32_t qd = tid % Q, kl = tid / Q, c = c0 + qd * 4;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // branch-free: a load consumed under a branch is waited for there with
+    // every load issued after it
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const bool use = kl < KL && kl + u * KL < cpi;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        acc[e] += use ? t0[u][0][e] : 0.0f;
+        acc[e + 4] += use ? t0[u][1][e] : 0.0f;
+      }
+    }
     if (kl < KL) {
-      const bool first = c < st.c1;  // 4-channel quads never straddle c1 (c1 % 8 == 0)
-      const float* base = first ? st.s1 : st.s2;
-      const uint64_t ld = first ? st.ld1 : st.ld2;
-      const uint64_t cc = first ? c : c - st.c1;
-      const float* p = base + ((uint64_t)n * cpi * ld + cc) * 2;
-      for (uint32_t k0 = kl; k0 < cpi; k0 += 8 * KL) {
+      for (uint32_t k0 = kl + 8 * KL; k0 < cpi; k0 += 8 * KL) {
         f32x4 t[8][2];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
           const uint32_t k = k0 + u * KL < cpi ? k0 + u * KL : kl;
-          t[u][0] = *(const f32x4*)(p + (uint64_t)k * ld * 2);
-          t[u][1] = *(const f32x4*)(p + (uint64_t)k * ld * 2 + 4);
+          t[u][0] = *(const f32x4*)(sp + (uint64_t)k * sld * 2);
+          t[u][1] = *(const f32x4*)(sp + (uint64_t)k * sld * 2 + 4);
         }
         sched_fence();
 #pragma unroll
