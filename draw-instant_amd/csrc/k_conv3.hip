@@ -71,6 +71,7 @@ template <int W>
 __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
   using G = ConvGeo<W>;
   __shared__ __attribute__((aligned(1024))) char smem[G::SMEM];
+  args_warm(g);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wq = wave & 3, kh = wave >> 2;  // 32-row wave tile, k half

@@ -199,6 +199,7 @@ __device__ __forceinline__ float splitk_colsum64(const float* p, int ld, bool sq
 // Vector split-K reduction + epilogue (vec_epi): one thread per 8 output
 // columns (splitk_vec8).
 __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
+  args_warm(g);
   const uint32_t ncols = g.act == ACT_GEGLU ? g.N / 2 : g.N;
   const uint32_t vpr = ncols / 8;
   const uint64_t total = (uint64_t)g.batch * g.M * vpr;
@@ -216,6 +217,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_vec(GemmArgs g) {
 // owns rows [64y, 64y + 64) x columns [32x, 32x + 32); thread t reduces
 // columns 32x + 8*(t % 4) .. +8 of row 64y + t/4.
 __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
+  args_warm(g);
   constexpr int LDR = 33;
   __shared__ float red[64 * LDR];
   const uint32_t t = threadIdx.x, cv = t % 4, rr = t / 4;
