@@ -124,6 +124,7 @@ __device__ __forceinline__ float sum_q4(float x) {
 template <int KS>
 __global__ __launch_bounds__(256 * KS, 4) void k_flash_attn(AttnArgs a, uint32_t nqb) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[KS * 2 * BUF_BYTES];  // [kg][buf][K | V]
+  kernarg_warm(a);
 
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = KS == 1 ? tid >> 6 : __builtin_amdgcn_readfirstlane(tid >> 6) & 3u;
@@ -369,6 +370,7 @@ __global__ __launch_bounds__(256 * KS, 4) void k_flash_attn(AttnArgs a, uint32_t
 // 16-byte chunk) of a (b, h, q) row; all SP ranges are loaded up front.
 template <int SP>
 __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
+  kernarg_warm(a);
   const uint32_t i = blockIdx.x * 256 + threadIdx.x, row = i >> 3, c = i & 7;
   if (row >= a.rows) return;
   float2 ml[SP];

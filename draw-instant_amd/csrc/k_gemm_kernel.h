@@ -472,19 +472,10 @@ __device__ __forceinline__ void gemm_tile_stats(const GemmArgs& g, const float* 
   }
 }
 
-// Touch one dword of every 64-byte line of the argument block, so all of
-// them are requested from the scalar cache in one round trip at entry; the
-// compiler otherwise loads the fields in dependent batches (three
-// serialised misses before the first operand load).  The empty asm
-// statement (an assembler comment) only keeps the loads alive.
-__device__ __forceinline__ void args_warm(const GemmArgs& g) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(&g);
-  uint32_t t = 0;
-#pragma unroll
-  for (int i = 0; i < (int)(sizeof(GemmArgs) / 4); i += 16) t |= w[i];
-  t |= gridDim.x;  // the launch's hidden arguments follow the block
-  asm volatile("; kernel arguments in the scalar cache %0" ::"s"(t));
-}
+// The argument block (GemmArgs, 328 bytes: six scalar-cache lines) in one
+// round trip at entry, instead of three serialised misses before the first
+// operand load.
+__device__ __forceinline__ void args_warm(const GemmArgs& g) { kernarg_warm(g); }
 
 // ---- the GEMM kernel ----
 // TB: storage type of B.  The fp32 kernels also take fp16 B (weights kept
