@@ -521,7 +521,17 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
   // of the vector epilogue.
   constexpr int kSmemPipe = 2 * (BM + BN) * LDK;
   constexpr int kSmemC = BM * (BN + 4) * 4 / (int)sizeof(T);  // fp32 C tile of the vector epilogue
-  __shared__ __attribute__((aligned(16))) T smem[kSmemPipe > kSmemC ? kSmemPipe : kSmemC];
+  // Side by side: the two k halves stage their fp32 C tiles at once and the
+  // vector epilogue adds them as it reads (one barrier, no read-modify-write
+  // pass), where the second tile costs no workgroup residency (a CU holds
+  // workgroups in two 80 KiB halves of its LDS).  The LayerNorm fold, applied
+  // to the summed tile, keeps the read-modify-write pass.
+  constexpr int kPer80K = (int)(80 * 1024 / sizeof(T));
+  constexpr int kSmem1 = kSmemPipe > kSmemC ? kSmemPipe : kSmemC;
+  constexpr int kSmem2 = kSmemPipe > 2 * kSmemC ? kSmemPipe : 2 * kSmemC;
+  constexpr bool SBS = sizeof(T) == 2 && KS == 2 && EX != EX_LNFOLD && kSmem2 <= kPer80K &&
+                       kPer80K / kSmem2 == kPer80K / kSmem1;
+  __shared__ __attribute__((aligned(16))) T smem[SBS ? kSmem2 : kSmem1];
   // LayerNorm fold: (mean, rstd) of each tile row, then ln_s of each column
   __shared__ __attribute__((aligned(8))) float sLn[EX == EX_LNFOLD ? 2 * BM + BN : 2];
   T (*sA)[BM * LDK] = reinterpret_cast<T (*)[BM * LDK]>(smem);
@@ -944,12 +954,28 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
   if constexpr (sizeof(T) == 2) {
     if (g.vec_epi) {
       constexpr int LDC = BN + 4;
-      static_assert(BM * LDC * 4 <= (int)sizeof(smem), "C tile fits the LDS allocation");
+      static_assert((SBS ? 2 : 1) * BM * LDC * 4 <= (int)sizeof(smem), "C tiles fit the LDS allocation");
       float* sC = reinterpret_cast<float*>(smem);
       // bias / temb bias / residual loads in flight while the tile is staged
       EpiOps<BM, BN, NT> pre;
       epi_prefetch<BM, BN, NT>(g, m0, n0, bz, pre);
       lds_barrier();  // every wave is done reading the last stage
+      if constexpr (SBS) {
+        float* const sCh = sC + kh * (BM * LDC);
+#pragma unroll
+        for (int a = 0; a < TM; a++)
+#pragma unroll
+          for (int b = 0; b < TN; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) sCh[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr] = acc[a][b][i];
+        lds_barrier();
+        gemm_epilogue_vec<BM, BN, LDC, NT, EX, 2>(g, sC, m0, n0, bz, split, &pre, BM * LDC);
+        if (g.stats && splits == 1) {
+          lds_barrier();
+          gemm_tile_stats<BM, BN, LDC, NT>(g, sC, m0, n0);
+        }
+        return;
+      }
       // LayerNorm fold (EX_LNFOLD, launched without split-K): the (mean,
       // rstd) of this thread's accumulator rows and ln_s of its columns
       float2 lmr[EX == EX_LNFOLD ? TM : 1][4];
