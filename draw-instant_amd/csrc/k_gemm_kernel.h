@@ -291,12 +291,15 @@ __device__ __forceinline__ void epi_prefetch(const GemmArgs& g, uint32_t m0, uin
 // where a kernel stages its k parts separately.  Split-K partials are
 // stored as fp32 vectors instead.  All operand loads of a batch of vectors
 // are issued before any is consumed; `pre` holds the first batch's when the
-// kernel prefetched them (epi_prefetch with the same tile).
+// kernel prefetched them (epi_prefetch with the same tile).  EX_LNFOLD with
+// sln: sln holds (mean, rstd) of each tile row, then ln_s of each tile
+// column, and the LayerNorm fold rstd * (sum - mean * ln_s[n]) is applied
+// to the summed tile (without sln the caller has applied it while staging).
 template <int BM, int BN, int LDC, int NT, int EX, int NSUM = 1>
 __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float* sC, uint32_t m0,
                                                   uint32_t n0, uint32_t bz, uint32_t split,
                                                   const EpiOps<BM, BN, NT>* pre = nullptr,
-                                                  int tstride = 0) {
+                                                  int tstride = 0, const float* sln = nullptr) {
   const int tid = threadIdx.x;
   auto tile4 = [&](int i) {
     f32x4 v = ld4(&sC[i]);
@@ -356,6 +359,14 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
         h[j] = tile1(r * LDC + cl + j);
         gt[j] = tile1(r * LDC + cl + 16 + j);
       }
+      if (EX == EX_LNFOLD && sln) {
+        const float2 mr = *(const float2*)&sln[2 * r];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          h[j] = mr.y * (h[j] - mr.x * sln[2 * BM + cl + j]);
+          gt[j] = mr.y * (gt[j] - mr.x * sln[2 * BM + cl + 16 + j]);
+        }
+      }
       // bias only (no bias2 / activation on GEGLU projections)
 #pragma unroll
       for (int j = 0; j < 8; j++) {
@@ -405,6 +416,15 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
         for (int j = 0; j < 4; j++) {
           x[j] = a0[j];
           x[j + 4] = a1[j];
+        }
+        if (EX == EX_LNFOLD && sln) {
+          const float2 mr = *(const float2*)&sln[2 * r];
+          const f32x4 l0 = ld4(&sln[2 * BM + c8]), l1 = ld4(&sln[2 * BM + c8 + 4]);
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            x[j] = mr.y * (x[j] - mr.x * l0[j]);
+            x[j + 4] = mr.y * (x[j + 4] - mr.x * l1[j]);
+          }
         }
         epi_math8(g, x, bb[u], tb[u]);
         f16x8 o;
@@ -524,16 +544,16 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
   // Side by side: the two k halves stage their fp32 C tiles at once and the
   // vector epilogue adds them as it reads (one barrier, no read-modify-write
   // pass), where the second tile costs no workgroup residency (a CU holds
-  // workgroups in two 80 KiB halves of its LDS).  The LayerNorm fold, applied
-  // to the summed tile, keeps the read-modify-write pass.
+  // workgroups in two 80 KiB halves of its LDS).  The LayerNorm fold is then
+  // applied by the vector epilogue to the summed tile.
   constexpr int kPer80K = (int)(80 * 1024 / sizeof(T));
   constexpr int kSmem1 = kSmemPipe > kSmemC ? kSmemPipe : kSmemC;
   constexpr int kSmem2 = kSmemPipe > 2 * kSmemC ? kSmemPipe : 2 * kSmemC;
-  constexpr bool SBS = sizeof(T) == 2 && KS == 2 && EX != EX_LNFOLD && kSmem2 <= kPer80K &&
+  constexpr bool SBS = sizeof(T) == 2 && KS == 2 && kSmem2 <= kPer80K &&
                        kPer80K / kSmem2 == kPer80K / kSmem1;
   __shared__ __attribute__((aligned(16))) T smem[SBS ? kSmem2 : kSmem1];
   // LayerNorm fold: (mean, rstd) of each tile row, then ln_s of each column
-  __shared__ __attribute__((aligned(8))) float sLn[EX == EX_LNFOLD ? 2 * BM + BN : 2];
+  __shared__ __attribute__((aligned(16))) float sLn[EX == EX_LNFOLD ? 2 * BM + BN : 2];
   T (*sA)[BM * LDK] = reinterpret_cast<T (*)[BM * LDK]>(smem);
   T (*sB)[BN * LDK] = reinterpret_cast<T (*)[BN * LDK]>(smem + 2 * BM * LDK);
   // element offset of (row r, k element e) inside one buffer
@@ -969,7 +989,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < 4; i++) sCh[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr] = acc[a][b][i];
         lds_barrier();
-        gemm_epilogue_vec<BM, BN, LDC, NT, EX, 2>(g, sC, m0, n0, bz, split, &pre, BM * LDC);
+        gemm_epilogue_vec<BM, BN, LDC, NT, EX, 2>(g, sC, m0, n0, bz, split, &pre, BM * LDC, sLn);
         if (g.stats && splits == 1) {
           lds_barrier();
           gemm_tile_stats<BM, BN, LDC, NT>(g, sC, m0, n0);
