@@ -32,8 +32,14 @@ __device__ __forceinline__ void kernarg_warm(const T& a) {
   asm volatile("; kernel arguments in the scalar cache %0" ::"s"(t));
 }
 
-// SiLU x/(1+e^-x): UNARY_EXPRS.SiLU wgsl-ops.js:68, fused-resnet.js:162.
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+// SiLU x/(1+e^-x): UNARY_EXPRS.SiLU wgsl-ops.js:68, fused-resnet.js:162.  The
+// quotient is x times the hardware reciprocal (1 ulp; 1 + e^-x >= 1, so no
+// denormal, and an infinite e^-x still gives the limit 0): a correctly
+// rounded division costs ~10 VALU instructions per value, most of the
+// normalise-and-store phase of a GroupNorm apply.
+__device__ __forceinline__ float silu_f(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 
 // erf by Abramowitz & Stegun 7.1.26 (max abs error 1.5e-7), the approximation
 // the reference's GELU and Erf kernels use (wgsl-ops.js:77-81).  t comes from
