@@ -489,8 +489,14 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
   __shared__ float gms[2][kGnSliceMax];
   const uint32_t tid = threadIdx.x, n = blockIdx.z, c0 = blockIdx.y * SW;
   // apply mapping; the first round of pixels and gamma / beta are loaded
-  // before the fold so the two memory round trips overlap
-  const uint32_t NV = SW / 8, R = 256 / NV, v = tid % NV, lane = tid / NV;
+  // before the fold so the two memory round trips overlap.  Quotients of
+  // the thread index by the slice's vector / quad counts come from a float
+  // reciprocal (exact for these sizes: the product stays 0.5 / d away from
+  // an integer, far beyond its rounding error), not from an integer
+  // division sequence: with one wave per SIMD each of those costs ~0.1 us.
+  const uint32_t NV = SW / 8, R = 256 / NV;
+  const uint32_t lane = (uint32_t)(((float)tid + 0.5f) * __builtin_amdgcn_rcpf((float)NV));
+  const uint32_t v = tid - lane * NV;
   const bool act = lane < R;
   const uint32_t c = c0 + v * 8;
   const uint32_t p0 = blockIdx.x * ppb, p1 = min(p0 + ppb, HW);
@@ -504,7 +510,8 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
   // other; a loop over further chunks would wait for every load at its top.
   __shared__ float fold[256 * 8];
   const uint32_t Q = SW / 4, KL = 256 / Q;
-  const uint32_t qd = tid % Q, kl = tid / Q, cq = c0 + qd * 4;
+  const uint32_t kl = (uint32_t)(((float)tid + 0.5f) * __builtin_amdgcn_rcpf((float)Q));
+  const uint32_t qd = tid - kl * Q, cq = c0 + qd * 4;
   const bool sfirst = cq < st.c1;  // 4-channel quads never straddle c1 (c1 % 8 == 0)
   const uint64_t sld = sfirst ? st.ld1 : st.ld2;
   const float* sp = (sfirst ? st.s1 : st.s2) + ((uint64_t)n * cpi * sld + (sfirst ? cq : cq - st.c1)) * 2;
@@ -600,11 +607,16 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
   __syncthreads();
   if (!act) return;
   float a[8], b[8];
+  // groups of the eight channels v * 8 + j: one division, then steps
+  uint32_t gl = (v * 8) / cpg, gr = v * 8 - gl * cpg;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    const uint32_t gl = (v * 8 + j) / cpg;
     a[j] = gms[1][gl] * gmv[j >> 2][j & 3];
     b[j] = btv[j >> 2][j & 3] - gms[0][gl] * a[j];
+    if (++gr == cpg) {
+      gr = 0;
+      gl++;
+    }
   }
   for (uint32_t p = p0 + lane; p < p1; p += U * R) {
     f16x8 t[U];
