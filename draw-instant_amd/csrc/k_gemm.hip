@@ -186,15 +186,6 @@ __device__ __forceinline__ void splitk_vec8(const GemmArgs& g, uint32_t bz, uint
   for (int j = 0; j < 8; j++) v[j] = (float)o[j];
 }
 
-// Column sum of 64 staged values (or of their squares), in row order.
-__device__ __forceinline__ float splitk_colsum64(const float* p, int ld, bool squares) {
-  float a = 0.0f;
-  for (int r = 0; r < 64; r++) {
-    const float x = p[r * ld];
-    a += squares ? __fmul_rn(x, x) : x;
-  }
-  return a;
-}
 
 // Vector split-K reduction + epilogue (vec_epi): one thread per 8 output
 // columns (splitk_vec8).
@@ -228,10 +219,24 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
 #pragma unroll
   for (int j = 0; j < 8; j++) red[rr * LDR + cv * 8 + j] = v[j];
   __syncthreads();
-  if (t < 64) {
-    const uint32_t col = t % 32, st = t / 32;
-    const uint64_t chunk = (uint64_t)bz * ((g.M + 63) / 64) + blockIdx.y;
-    g.stats[(chunk * g.N + blockIdx.x * 32 + col) * 2 + st] = splitk_colsum64(red + col, LDR, st == 1);
+  // column sums (t / 4 < 32) and sums of squares (t / 4 >= 32) of the 64
+  // staged rows: four adjacent lanes take every fourth row and add their
+  // sums by lane swaps in a fixed order (one thread per column spent a
+  // dependent add per row)
+  {
+    const uint32_t item = t / 4, part = t % 4, col = item % 32, st = item / 32;
+    float a = 0.0f;
+#pragma unroll
+    for (uint32_t r = part; r < 64; r += 4) {
+      const float x = red[r * LDR + col];
+      a += st ? __fmul_rn(x, x) : x;
+    }
+    a += __shfl_xor(a, 1);
+    a += __shfl_xor(a, 2);
+    if (part == 0) {
+      const uint64_t chunk = (uint64_t)bz * ((g.M + 63) / 64) + blockIdx.y;
+      g.stats[(chunk * g.N + blockIdx.x * 32 + col) * 2 + st] = a;
+    }
   }
 }
 

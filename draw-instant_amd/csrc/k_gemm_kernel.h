@@ -467,28 +467,40 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
 
 // GroupNorm statistics of an output tile (g.stats): for each 64-row chunk of
 // the tile and each column, the sum and sum of squares of the stored fp16
-// values over the chunk's rows < M, in row order, written to
-// stats[(chunk * N + n) * 2 + {0, 1}] with chunk = global row / 64.  sC holds
-// the stored values (written back by the epilogue).
+// values over the chunk's rows < M, written to stats[(chunk * N + n) * 2 +
+// {0, 1}] with chunk = global row / 64.  sC holds the stored values
+// (written back by the epilogue).  TPI adjacent lanes share a column, each
+// summing every TPI-th row, and add their sums by lane swaps in a fixed
+// order: a lone thread per column spent a dependent add per row, with one
+// or two waves of the workgroup busy.
 template <int BM, int BN, int LDC, int NT>
 __device__ __forceinline__ void gemm_tile_stats(const GemmArgs& g, const float* sC, uint32_t m0,
                                                 uint32_t n0) {
   static_assert(BM % 64 == 0, "whole 64-row chunks");
-  constexpr int NCH = BM / 64;
-  for (int i = threadIdx.x; i < NCH * BN; i += NT) {
-    const int ch = i / BN, n = i % BN;
+  constexpr int NCH = BM / 64, ITEMS = NCH * BN;
+  constexpr int TPI = NT / ITEMS >= 8 ? 8 : NT / ITEMS >= 4 ? 4 : NT / ITEMS >= 2 ? 2 : 1;
+  for (int i = threadIdx.x; i < ITEMS * TPI; i += NT) {  // whole TPI groups
+    const int item = i / TPI, part = i % TPI;
+    const int ch = item / BN, n = item % BN;
     const uint32_t r0 = m0 + ch * 64;
-    if (r0 >= g.M || n0 + n >= g.N) continue;
-    const int rows = (int)min(64u, g.M - r0);
+    const bool ok = r0 < g.M && n0 + n < g.N;
+    const int rows = ok ? (int)min(64u, g.M - r0) : 0;
     float s = 0.0f, q = 0.0f;
-    for (int r = 0; r < rows; r++) {
+    for (int r = part; r < rows; r += TPI) {
       const float v = sC[(ch * 64 + r) * LDC + n];
       s += v;
       q += v * v;
     }
-    float* st = g.stats + ((uint64_t)(r0 / 64) * g.N + n0 + n) * 2;
-    st[0] = s;
-    st[1] = q;
+#pragma unroll
+    for (int o = 1; o < TPI; o <<= 1) {
+      s += __shfl_xor(s, o);
+      q += __shfl_xor(q, o);
+    }
+    if (ok && part == 0) {
+      float* st = g.stats + ((uint64_t)(r0 / 64) * g.N + n0 + n) * 2;
+      st[0] = s;
+      st[1] = q;
+    }
   }
 }
 
