@@ -481,12 +481,18 @@ __global__ __launch_bounds__(256) void k_gn_stats_fold(GnStats st, float* __rest
 
 // cpi: statistics chunks per image in st (HW / 64 as the GEMM epilogue wrote
 // them, or fewer after k_gn_stats_fold).
+// NU: statistics chunks each lane loads in the first, straight-line batch
+// (the host picks the smallest of 1 / 2 / 4 / 8 that covers the image's
+// chunks, since every load issued costs the CU's load path whether or not
+// it is used); chunks beyond NU lanes' worth are taken by a loop.
+template <int NU>
 __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
     NhwcSrc x, GnStats st, const float* __restrict__ gamma, const float* __restrict__ beta,
     f16* __restrict__ y, uint32_t C, uint32_t cpg, uint32_t SW, uint32_t HW, uint32_t ppb,
     float eps, int silu, uint32_t cpi) {
   __shared__ float chs[2][kGnSliceMax];
   __shared__ float gms[2][kGnSliceMax];
+  __shared__ __attribute__((aligned(16))) float sgb[2][kGnSliceMax];  // gamma, beta of the slice
   const uint32_t tid = threadIdx.x, n = blockIdx.z, c0 = blockIdx.y * SW;
   // apply mapping; the first round of pixels and gamma / beta are loaded
   // before the fold so the two memory round trips overlap.  Quotients of
@@ -518,30 +524,31 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
   // Every thread issues these loads (threads without a chunk / pixel share
   // in-range addresses and drop the results): a load under a branch makes
   // the compiler wait for all loads where the branch rejoins.
-  f32x4 t0[8][2];
+  f32x4 t0[NU][2];
   {
     // chunk lanes past KL or past the image's cpi chunks read chunk 0
     const uint32_t klc = kl < KL ? kl : 0u;
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < NU; u++) {
       const uint32_t k = klc + u * KL < cpi ? klc + u * KL : 0u;
       t0[u][0] = *(const f32x4*)(sp + (uint64_t)k * sld * 2);
       t0[u][1] = *(const f32x4*)(sp + (uint64_t)k * sld * 2 + 4);
     }
   }
-  // loads retire in order: keep the statistics (needed first) ahead
+  // gamma / beta of the slice, one quad per thread (threads past SW / 4
+  // repeat quad 0), staged in LDS for the apply instead of every thread
+  // loading its own eight channels: after the statistics, ahead of the
+  // pixels (loads retire in order: the statistics are needed first)
+  const uint32_t gq = tid < SW / 4 ? tid : 0u;
+  const f32x4 gmq = *(const f32x4*)(gamma + c0 + gq * 4);
+  const f32x4 btq = *(const f32x4*)(beta + c0 + gq * 4);
   sched_fence();
   constexpr int U = 4;
   f16x8 pre[U];
-  f32x4 gmv[2], btv[2];
   {
     const uint32_t lc = act ? lane : 0u;
 #pragma unroll
     for (int u = 0; u < U; u++) pre[u] = x.load8(pix0 + min(p0 + lc + u * R, p1 - 1), c);
-    gmv[0] = *(const f32x4*)(gamma + c);
-    gmv[1] = *(const f32x4*)(gamma + c + 4);
-    btv[0] = *(const f32x4*)(beta + c);
-    btv[1] = *(const f32x4*)(beta + c + 4);
   }
   sched_fence();
   {
@@ -549,7 +556,7 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
     // branch-free: a load consumed under a branch is waited for there with
     // every load issued after it
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < NU; u++) {
       const bool use = kl < KL && kl + u * KL < cpi;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -558,7 +565,7 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
       }
     }
     if (kl < KL) {
-      for (uint32_t k0 = kl + 8 * KL; k0 < cpi; k0 += 8 * KL) {
+      for (uint32_t k0 = kl + NU * KL; k0 < cpi; k0 += 8 * KL) {
         f32x4 t[8][2];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
@@ -581,6 +588,10 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
     }
 #pragma unroll
     for (int e = 0; e < 8; e++) fold[tid * 8 + e] = acc[e];
+  }
+  if (tid < SW / 4) {
+    *(f32x4*)&sgb[0][tid * 4] = gmq;
+    *(f32x4*)&sgb[1][tid * 4] = btq;
   }
   __syncthreads();
   // acc layout per quad: (s, q) of channels 4qd .. 4qd+3 interleaved
@@ -611,8 +622,8 @@ __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
   uint32_t gl = (v * 8) / cpg, gr = v * 8 - gl * cpg;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    a[j] = gms[1][gl] * gmv[j >> 2][j & 3];
-    b[j] = btv[j >> 2][j & 3] - gms[0][gl] * a[j];
+    a[j] = gms[1][gl] * sgb[0][v * 8 + j];
+    b[j] = sgb[1][v * 8 + j] - gms[0][gl] * a[j];
     if (++gr == cpg) {
       gr = 0;
       gl++;
@@ -1119,8 +1130,21 @@ bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st_in, c
   if (pbs < 1) pbs = 1;
   const uint32_t ppb = (HW + pbs - 1) / pbs;
   pbs = (HW + ppb - 1) / ppb;
-  k_gn_nhwc_apply_st<<<dim3(pbs, slices, N), 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw,
-                                                          HW, ppb, eps, silu ? 1 : 0, cpi);
+  // statistics chunks per lane: KL lanes per channel quad
+  const uint32_t kl_lanes = 256 / (sw / 4), need = (cpi + kl_lanes - 1) / kl_lanes;
+  const dim3 grid(pbs, slices, N);
+  if (need <= 1)
+    k_gn_nhwc_apply_st<1><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
+                                                eps, silu ? 1 : 0, cpi);
+  else if (need <= 2)
+    k_gn_nhwc_apply_st<2><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
+                                                eps, silu ? 1 : 0, cpi);
+  else if (need <= 4)
+    k_gn_nhwc_apply_st<4><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
+                                                eps, silu ? 1 : 0, cpi);
+  else
+    k_gn_nhwc_apply_st<8><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
+                                                eps, silu ? 1 : 0, cpi);
   return true;
 }
 
