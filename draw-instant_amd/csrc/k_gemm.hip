@@ -12,6 +12,7 @@ namespace {
 
 // Split-K reduction + epilogue: one thread per output element.
 __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
+  args_warm(g);
   const uint32_t ncols = g.act == ACT_GEGLU ? g.N / 2 : g.N;
   const uint64_t total = (uint64_t)g.batch * g.M * ncols;
   const uint64_t mn = (uint64_t)g.M * g.N;
