@@ -227,9 +227,11 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
   {
     const uint32_t item = t / 4, part = t % 4, col = item % 32, st = item / 32;
     float a = 0.0f;
+    // a constant trip count, so the 16 LDS reads are issued together (from a
+    // lane-dependent start the loop stays rolled, one LDS round trip per row)
 #pragma unroll
-    for (uint32_t r = part; r < 64; r += 4) {
-      const float x = red[r * LDR + col];
+    for (uint32_t k = 0; k < 16; k++) {
+      const float x = red[(part + 4 * k) * LDR + col];
       a += st ? __fmul_rn(x, x) : x;
     }
     a += __shfl_xor(a, 1);

@@ -486,8 +486,12 @@ __device__ __forceinline__ void gemm_tile_stats(const GemmArgs& g, const float* 
     const bool ok = r0 < g.M && n0 + n < g.N;
     const int rows = ok ? (int)min(64u, g.M - r0) : 0;
     float s = 0.0f, q = 0.0f;
-    for (int r = part; r < rows; r += TPI) {
-      const float v = sC[(ch * 64 + r) * LDC + n];
+    // a constant trip count (rows past the tile's count add zeros), so the
+    // LDS reads are issued together rather than one round trip per row
+#pragma unroll
+    for (int k = 0; k < 64 / TPI; k++) {
+      const int r = part + k * TPI;
+      const float v = r < rows ? sC[(ch * 64 + r) * LDC + n] : 0.0f;
       s += v;
       q += v * v;
     }
