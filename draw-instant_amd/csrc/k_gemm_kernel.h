@@ -277,12 +277,54 @@ __device__ __forceinline__ void epi_load(const GemmArgs& g, uint32_t m0, uint32_
   }
 }
 
+// GEGLU vector v of a thread: 8 outputs of tile row r from hidden columns
+// cl .. cl + 7 and gate columns cl + 16 .. cl + 23 (32-column groups
+// [16 hidden | 16 gate]), written at output column f
+template <int BN, int NT>
+struct GegluVec {
+  static constexpr int VPRG = BN / 16;
+  int r, cl;
+  __device__ __forceinline__ GegluVec(int v) {
+    const int idx = (int)threadIdx.x + v * NT;
+    r = idx / VPRG;
+    const int q = idx % VPRG;
+    cl = (q >> 1) * 32 + (q & 1) * 8;
+  }
+};
+
+// All of a thread's GEGLU operand loads (hidden / gate bias, residual) into
+// o.bb / o.tb / o.rr, one entry per vector (BM * BN / 16 / NT of them, at
+// most EpiOps' batch), at clamped in-range addresses
+template <int BM, int BN, int NT>
+__device__ __forceinline__ void epi_load_geglu(const GemmArgs& g, uint32_t m0, uint32_t n0,
+                                               uint32_t bz, EpiOps<BM, BN, NT>& o) {
+  using O = EpiOps<BM, BN, NT>;
+  constexpr int VPRG = BN / 16, NVG = (BM * VPRG + NT - 1) / NT;
+  static_assert(NVG <= O::CH, "GEGLU vectors fit the operand batch");
+  const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr;
+#pragma unroll
+  for (int v = 0; v < NVG; v++) {
+    const GegluVec<BN, NT> e(v);
+    const uint32_t m = m0 + e.r, nh = n0 + e.cl;
+    const bool ok = (int)threadIdx.x + v * NT < BM * VPRG && m < g.M && nh < g.N;
+    const uint32_t nhc = ok ? nh : n0, f = (nhc / 32) * 16 + (nhc % 32);
+    if (g.bias) {
+      o.bb[v][0] = ld4(g.bias + nhc);
+      o.bb[v][1] = ld4(g.bias + nhc + 4);
+      o.tb[v][0] = ld4(g.bias + nhc + 16);
+      o.tb[v][1] = ld4(g.bias + nhc + 20);
+    }
+    if (g.res) o.rr[v] = *(const f16x8*)(R + (uint64_t)(ok ? m : m0) * g.ldr + f);
+  }
+}
+
 // First-batch operands for gemm_epilogue_vec, or nothing when that
-// epilogue will not use them (split-K partials, GEGLU's own layout).
+// epilogue will not use them (split-K partials).
 template <int BM, int BN, int NT>
 __device__ __forceinline__ void epi_prefetch(const GemmArgs& g, uint32_t m0, uint32_t n0, uint32_t bz,
                                              EpiOps<BM, BN, NT>& o) {
-  if (g.splits <= 1 && g.act != ACT_GEGLU) epi_load<BM, BN, NT>(g, m0, n0, bz, 0, o);
+  if (g.splits > 1 || g.act == ACT_GEGLU) return;
+  epi_load<BM, BN, NT>(g, m0, n0, bz, 0, o);
 }
 
 // Writes (GEGLU-combined when act == GEGLU) results for the rows/columns of
@@ -307,12 +349,6 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     for (int t = 1; t < NSUM; t++) v += ld4(&sC[i + t * tstride]);
     return v;
   };
-  auto tile1 = [&](int i) {
-    float v = sC[i];
-#pragma unroll
-    for (int t = 1; t < NSUM; t++) v += sC[i + t * tstride];
-    return v;
-  };
   if (g.splits > 1) {
     constexpr int VPR4 = BN / 4;
     constexpr int NV = (BM * VPR4 + NT - 1) / NT;
@@ -329,38 +365,36 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     return;
   }
   f16* C = (f16*)g.c + (uint64_t)bz * g.sc;
-  const f16* R = (const f16*)g.res + (uint64_t)bz * g.sr;
   if (g.act == ACT_GEGLU) {
     // 32-column groups [16 hidden | 16 gate]; a vector is 8 outputs from
-    // hidden columns cl..cl+7 and gate columns cl+16..cl+23.
+    // hidden columns cl..cl+7 and gate columns cl+16..cl+23.  Its operands
+    // were prefetched (or are loaded here, all before any is consumed).
     constexpr int VPRG = BN / 16;
     constexpr int NV = (BM * VPRG + NT - 1) / NT;
+    EpiOps<BM, BN, NT> ops;
+    epi_load_geglu<BM, BN, NT>(g, m0, n0, bz, ops);
 #pragma unroll
     for (int v = 0; v < NV; v++) {
-      const int idx = tid + v * NT;
-      if (idx >= BM * VPRG) break;
-      const int r = idx / VPRG, q = idx % VPRG, cl = (q >> 1) * 32 + (q & 1) * 8;
+      const GegluVec<BN, NT> e(v);
+      const int r = e.r, cl = e.cl;
       const uint32_t m = m0 + r, nh = n0 + cl;
-      const bool ok = m < g.M && nh < g.N;
-      const uint32_t nhc = ok ? nh : n0;
-      f32x4 bh[2] = {}, bg[2] = {};
-      if (g.bias) {
-        bh[0] = ld4(g.bias + nhc);
-        bh[1] = ld4(g.bias + nhc + 4);
-        bg[0] = ld4(g.bias + nhc + 16);
-        bg[1] = ld4(g.bias + nhc + 20);
-      }
+      const bool ok = tid + v * NT < BM * VPRG && m < g.M && nh < g.N;
       const uint32_t f = (nh / 32) * 16 + (nh % 32);
-      f16x8 rv = {};
-      if (g.res) rv = *(const f16x8*)(R + (uint64_t)(ok ? m : m0) * g.ldr + (ok ? f : 0));
       float h[8], gt[8];
+      const int rt = tid + v * NT < BM * VPRG ? r : 0;
+      {
+        const int i = rt * LDC + cl;
+        const f32x4 h0 = tile4(i), h1 = tile4(i + 4), g0 = tile4(i + 16), g1 = tile4(i + 20);
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        h[j] = tile1(r * LDC + cl + j);
-        gt[j] = tile1(r * LDC + cl + 16 + j);
+        for (int j = 0; j < 4; j++) {
+          h[j] = h0[j];
+          h[j + 4] = h1[j];
+          gt[j] = g0[j];
+          gt[j + 4] = g1[j];
+        }
       }
       if (EX == EX_LNFOLD && sln) {
-        const float2 mr = *(const float2*)&sln[2 * r];
+        const float2 mr = *(const float2*)&sln[2 * rt];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           h[j] = mr.y * (h[j] - mr.x * sln[2 * BM + cl + j]);
@@ -370,10 +404,10 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
       // bias only (no bias2 / activation on GEGLU projections)
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float hv = h[j] * g.alpha + (g.bias ? bh[j >> 2][j & 3] : 0.0f);
-        const float gv = gt[j] * g.alpha + (g.bias ? bg[j >> 2][j & 3] : 0.0f);
+        const float hv = h[j] * g.alpha + (g.bias ? ops.bb[v][j >> 2][j & 3] : 0.0f);
+        const float gv = gt[j] * g.alpha + (g.bias ? ops.tb[v][j >> 2][j & 3] : 0.0f);
         h[j] = hv * gelu_erf_f(gv);
-        if (g.res) h[j] += (float)rv[j];
+        if (g.res) h[j] += (float)ops.rr[v][j];
       }
       if (ok) {
         f16x8 o;
