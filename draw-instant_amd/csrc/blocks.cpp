@@ -23,13 +23,18 @@ namespace di {
 
 namespace {
 
-int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rst = nullptr) {
+int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rst = nullptr,
+        GnFuseOut* gn = nullptr) {
   const GemmPlan plan = gemm_plan(g, DI_F16, c->num_cus);
   const int tile = plan.tile;
   g.splits = plan.splits;
   g.stats = nullptr;
   g.rstats = nullptr;
-  if (st && st->p) {
+  if (gn) gn->done = splitk_gn_ok(g, gn->f);
+  if (st) st->done = false;
+  if (gn && gn->done) {
+    // the reducer writes GN(output) only: no raw output, no statistics
+  } else if (st && st->p) {
     st->done = gemm_stats_ok(g, DI_F16, a_mode, B_NK, tile);
     if (st->done) g.stats = st->p;
   }
@@ -55,7 +60,8 @@ int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rs
     if (rc) return rc;
     g.part = (float*)ws;
   }
-  launch_gemm(g, DI_F16, a_mode, B_NK, tile, c->stream);
+  if (gn && gn->done) g.part_cpg = g.N / gn->f.groups;
+  launch_gemm(g, DI_F16, a_mode, B_NK, tile, c->stream, gn && gn->done ? &gn->f : nullptr);
   return DI_OK;
 }
 
@@ -80,6 +86,13 @@ int gn_nhwc(Ctx* c, NhwcSrc x, const float* g, const float* b, f16* y, uint32_t 
 }
 
 NhwcSrc single(const f16* p, uint32_t C) { return NhwcSrc{p, p, C, C, C}; }
+
+// DI_GN_REDUCE_FUSE=0 keeps conv1's GroupNorm as its own apply launch
+// (comparison runs; read at every block call, so a test can switch it)
+bool gn2_off() {
+  const char* e = getenv("DI_GN_REDUCE_FUSE");
+  return e && e[0] == '0';
+}
 
 }  // namespace
 
@@ -123,7 +136,7 @@ int conv_nhwc(Ctx* c, const ConvCall& cc) {
   } else {
     g.ldc = cc.ldc ? cc.ldc : cc.Cout;
   }
-  return run(c, g, A_CONV_NHWC, cc.stats);
+  return run(c, g, A_CONV_NHWC, cc.stats, nullptr, cc.gn);
 }
 
 int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const f16* w,
@@ -185,12 +198,25 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
   c1.y = t2.h();
   StatsOut so2{st2 ? t2st.f() : nullptr};
   c1.stats = &so2;
+  // GN2 + SiLU applied by conv1's split-K reducer where the plan splits
+  GnFuseOut gn2;
+  gn2.f.gamma = w.n2_g;
+  gn2.f.beta = w.n2_b;
+  gn2.f.y = t3.h();
+  gn2.f.ldy = s.Cout;
+  gn2.f.groups = s.groups;
+  gn2.f.hw = HW;
+  gn2.f.eps = s.eps;
+  gn2.f.silu = 1;
+  if (!gn2_off()) c1.gn = &gn2;
   rc = conv_nhwc(c, c1);
   if (rc) return rc;
-  const GnStats s2{t2st.f(), t2st.f(), s.Cout, s.Cout, s.Cout};
-  rc = gn_nhwc(c, single(t2.h(), s.Cout), w.n2_g, w.n2_b, t3.h(), s.B, s.Cout, s.groups, HW,
-               s.eps, true, so2.done ? &s2 : nullptr);
-  if (rc) return rc;
+  if (!gn2.done) {
+    const GnStats s2{t2st.f(), t2st.f(), s.Cout, s.Cout, s.Cout};
+    rc = gn_nhwc(c, single(t2.h(), s.Cout), w.n2_g, w.n2_b, t3.h(), s.B, s.Cout, s.groups, HW,
+                 s.eps, true, so2.done ? &s2 : nullptr);
+    if (rc) return rc;
+  }
   const f16* res = nullptr;
   uint64_t ldr = s.Cout;
   if (w.sk_w) {

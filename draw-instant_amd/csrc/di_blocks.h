@@ -6,6 +6,7 @@
 #include <cstdint>
 
 #include "di_device.h"
+#include "di_gemm.h"
 #include "di_internal.h"
 #include "di_kernels.h"
 
@@ -19,6 +20,15 @@ namespace di {
 // (it cannot on every path, e.g. K % 64 != 0).
 struct StatsOut {
   float* p = nullptr;
+  bool done = false;
+};
+
+// Request for a split-K conv's reducer to apply the GroupNorm (+SiLU) that
+// is the output's only consumer (GnFuse); done reports whether it did (the
+// plan may not split, or the shape may not fit the fused reducer), in which
+// case the raw output and its statistics were written as usual.
+struct GnFuseOut {
+  GnFuse f;
   bool done = false;
 };
 
@@ -158,6 +168,7 @@ struct ConvCall {
   uint64_t ldc = 0;
   int y_nchw_f32 = 0;
   StatsOut* stats = nullptr;  // GroupNorm statistics of y (GemmArgs::stats), optional
+  GnFuseOut* gn = nullptr;    // GroupNorm of y applied by a split-K reducer, optional
 };
 int conv_nhwc(Ctx* c, const ConvCall& cc);
 

@@ -79,6 +79,10 @@ struct GemmArgs {
   int c_nchw = 0;     // store C[(img*N + n)*c_hw + p] with m = img*c_hw + p
   uint32_t c_hw = 1;
   float* part = nullptr;  // split-K partials [splits][batch][M][N]
+  // part_cpg > 0: partials in column groups of part_cpg (4 | part_cpg,
+  // part_cpg | N), [splits][batch][N / part_cpg][M][part_cpg], so that one
+  // group's values are contiguous (the GroupNorm-fused reducer's layout)
+  uint32_t part_cpg = 0;
   // Optional GroupNorm statistics of the stored output (see gemm_stats_ok):
   // per 64-row chunk of the M rows and per column, (sum, sum of squares) at
   // stats[((bz * ceil(M/64) + m/64) * N + n) * 2].
@@ -125,8 +129,29 @@ void launch_conv3_halo(const GemmArgs& g, hipStream_t s);
 bool conv_in_direct_ok(uint32_t Cin, uint32_t Cout, uint32_t H, uint32_t W);
 void launch_conv_in(hipStream_t s, const float* x, const _Float16* w, const float* bias,
                     _Float16* y, float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W);
-// elem: DI_F16 or DI_F32 operand element type.
-void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s);
+// GroupNorm (+SiLU) of a split-K conv's output applied by its reducer: the
+// output rows are hw-pixel images of N channels in `groups` groups;
+// y[rows][ldy] = GN(out) (+SiLU) in fp16 is the only thing written (no raw
+// output, no statistics).  For a conv whose output feeds that GroupNorm
+// and nothing else (a ResNet's conv1).
+struct GnFuse {
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  void* y = nullptr;
+  uint64_t ldy = 0;
+  uint32_t groups = 0, hw = 0;
+  float eps = 0.0f;
+  int silu = 0;
+};
+// Whether the fused reducer takes this call (g with its plan's splits):
+// batch 1, split-K with a built (hw / 64, split count) pair, bias and a
+// per-image temb bias, no residual or activation, 4 | channels per group
+// <= 40, hw a multiple of 64 (64 to 1024 pixels).
+bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f);
+// elem: DI_F16 or DI_F32 operand element type.  gn: see GnFuse (only with
+// g.splits > 1 and splitk_gn_ok).
+void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s,
+                 const GnFuse* gn = nullptr);
 // Whether launch_gemm can produce g.stats for this call: buffer-load fp16
 // path with the vector epilogue, no GEGLU, batch 1, and N % 32 == 0 when
 // split-K is used.

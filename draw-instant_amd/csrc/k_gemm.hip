@@ -243,6 +243,144 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
   }
 }
 
+// Split-K reduction fused with the GroupNorm (+SiLU) of its output (GnFuse):
+// workgroup (group, image) sums the partials of the group's cpg channels
+// over the image's HW = 64 IM rows in split order and applies x * alpha +
+// bias + temb bias as the vector reducer does (the same fp16 values), then
+// takes the group's mean and variance of those fp16 values
+// (E[x^2] - E[x]^2, clamped at 0: GroupNorm's statistics) inside the
+// workgroup and writes only GN(x) (+SiLU).  Thread t of RS Q (<= 640):
+// channel quad q = t % Q (Q = cpg / 4), rows t / Q + RS i, i < IM (HW = RS
+// IM), from partials the GEMM stored in column groups of cpg, so a wave
+// reads 1 KB contiguous per load.  The split count S
+// is a template parameter: the IM x S partial loads are straight-line code
+// in batches of at most 24, each batch issued before any of it is added (a
+// loop over splits would make the compiler wait for every load at its top).
+template <int IM, int S>
+__global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, uint32_t Q,
+                                                          uint32_t RS) {
+  args_warm(g);
+  kernarg_warm(f);
+  __shared__ float red[2][10];
+  const uint32_t tid = threadIdx.x, grp = blockIdx.x, n = blockIdx.y;
+  // tid / Q from a float reciprocal: exact for tid < 1024 (the product stays
+  // 0.5 / Q away from an integer, far beyond its rounding error)
+  const uint32_t r0 = (uint32_t)(((float)tid + 0.5f) * __builtin_amdgcn_rcpf((float)Q));
+  const uint32_t q = tid - r0 * Q, c = grp * Q * 4 + q * 4;
+  const uint64_t row0 = (uint64_t)n * (RS * IM) + r0;
+  // per-channel operands first: loads retire in order, and these are needed
+  // only after the partials
+  const f32x4 bb = ld4(g.bias + c);
+  const f32x4 tb = ld4(g.bias2 + (uint64_t)n * g.ld_b2 + c);
+  const f32x4 gm = ld4(f.gamma + c);
+  const f32x4 bt = ld4(f.beta + c);
+  // partials in column groups (part_cpg = cpg): the group's image block is
+  // contiguous, thread t reads quads t, t + RS Q, ... of it
+  const float* p = g.part + ((uint64_t)grp * g.M + row0) * (Q * 4) + q * 4;
+  const uint64_t sstep = (uint64_t)g.M * g.N, rstep = (uint64_t)RS * Q * 4;
+  constexpr int NL = IM * S, NB = NL <= 24 ? NL : IM >= 8 ? 16 : 24;
+  f32x4 acc[IM];
+#pragma unroll
+  for (int i = 0; i < IM; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b0 = 0; b0 < NL; b0 += NB) {
+    f32x4 t[NB];
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+      const int j = b0 + u;  // split j / IM of row step j % IM: splits in order per row
+      if (j < NL) t[u] = ld4(p + (uint64_t)(j / IM) * sstep + (uint64_t)(j % IM) * rstep);
+    }
+    // the whole batch is issued before the scheduler may start its adds
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+      const int j = b0 + u;
+      if (j < NL) acc[j % IM] += t[u];
+    }
+  }
+  f16x4 h[IM];
+  float sum = 0.0f, sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < IM; i++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float v = acc[i][j] * g.alpha;
+      v += bb[j];
+      v += tb[j];
+      h[i][j] = (f16)v;
+      const float x = (float)h[i][j];
+      sum += x;
+      sq += __fmul_rn(x, x);
+    }
+  }
+  sum = wave_sum(sum);
+  sq = wave_sum(sq);
+  if (tid % 64 == 0) {
+    red[0][tid / 64] = sum;
+    red[1][tid / 64] = sq;
+  }
+  __syncthreads();
+  float ps = 0.0f, pq = 0.0f;
+  for (uint32_t w = 0; w < blockDim.x / 64; w++) {
+    ps += red[0][w];
+    pq += red[1][w];
+  }
+  const float L = (float)(Q * 4) * (float)(RS * IM);
+  const float mean = ps / L;
+  const float var = fmaxf(pq / L - mean * mean, 0.0f);
+  const float rstd = 1.0f / sqrtf(var + f.eps);
+  float a[4], b[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    a[j] = rstd * gm[j];
+    b[j] = bt[j] - mean * a[j];
+  }
+  f16* y = (f16*)f.y + row0 * f.ldy + c;
+#pragma unroll
+  for (int i = 0; i < IM; i++) {
+    f16x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float r = (float)h[i][j] * a[j] + b[j];
+      o[j] = (f16)(f.silu ? silu_f(r) : r);
+    }
+    *(f16x4*)(y + (uint64_t)i * RS * f.ldy) = o;
+  }
+}
+
+// (row steps, split count) pairs the fused reducer is built for
+#define DI_RGN_CASES(X)                                                                   \
+  X(1, 2) X(1, 3) X(1, 4) X(1, 5) X(1, 6) X(1, 8) X(1, 12) X(2, 2) X(2, 3) X(2, 4) X(2, 5) \
+  X(2, 6) X(2, 8) X(2, 12) X(4, 2) X(4, 3) X(4, 4) X(4, 5) X(4, 6) X(4, 8) X(4, 12)       \
+  X(8, 2) X(8, 3) X(8, 4) X(8, 5) X(8, 6) X(16, 2) X(16, 3) X(16, 4)
+
+bool splitk_gn_built(uint32_t im, uint32_t splits) {
+#define DI_RGN_HAS(IMV, SV) if (im == IMV && splits == SV) return true;
+  DI_RGN_CASES(DI_RGN_HAS)
+#undef DI_RGN_HAS
+  return false;
+}
+
+// Rows per step of the fused reducer: the most (a multiple of 64 dividing
+// hw) with at most 640 threads.
+uint32_t splitk_gn_rs(uint32_t q, uint32_t hw) {
+  uint32_t rs = 64;
+  while (2 * rs * q <= 640 && hw % (2 * rs) == 0) rs *= 2;
+  return rs;
+}
+
+void launch_splitk_reduce_gn(const GemmArgs& g, const GnFuse& f, hipStream_t s) {
+  const uint32_t q = g.N / f.groups / 4, rs = splitk_gn_rs(q, f.hw), im = f.hw / rs;
+  const dim3 grid(f.groups, g.M / f.hw), block(rs * q);
+#define DI_RGN_LAUNCH(IMV, SV)                                        \
+  if (im == IMV && g.splits == SV) {                                  \
+    k_splitk_reduce_gn<IMV, SV><<<grid, block, 0, s>>>(g, f, q, rs);  \
+    return;                                                           \
+  }
+  DI_RGN_CASES(DI_RGN_LAUNCH)
+#undef DI_RGN_LAUNCH
+}
+
 const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64, 64, 128, 64, 64, 128, 128, 64, 128, 64};
 const uint32_t kTileN[TILE_COUNT] = {64, 64, 128, 128, 160, 160, 64, 64, 128, 128, 64, 128, 64, 64, 32};
 // Relative per-CU MFMA efficiency of each tile shape (the 2x2 wavefront tile
@@ -463,7 +601,21 @@ uint32_t gemm_rstats_tiles(const GemmArgs& g, int tile_cfg) {
   return (g.N + kTileN[tile_cfg] - 1) / kTileN[tile_cfg];
 }
 
-void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s) {
+bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f) {
+  if (g.splits <= 1 || g.batch != 1 || !f.groups || !f.hw || !f.gamma || !f.beta || !f.y)
+    return false;
+  const uint32_t cpg = g.N / f.groups;
+  return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && f.hw % 64 == 0 &&
+         splitk_gn_built(f.hw / splitk_gn_rs(cpg / 4, f.hw), g.splits) && g.M % f.hw == 0 &&
+         g.bias && g.bias2 && g.rows_b2 == f.hw && g.ld_b2 % 4 == 0 && !g.res &&
+         g.act == ACT_NONE && !g.c_f32 && !g.c_nchw && f.ldy % 4 == 0 &&
+         ((uintptr_t)f.y & 7) == 0 && ((uintptr_t)g.bias & 15) == 0 &&
+         ((uintptr_t)g.bias2 & 15) == 0 && ((uintptr_t)f.gamma & 15) == 0 &&
+         ((uintptr_t)f.beta & 15) == 0;
+}
+
+void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hipStream_t s,
+                 const GnFuse* gn) {
   // k_split in elements, multiple of the stage depth
   const uint32_t bk = elem == DI_F32 ? 32 : 64;
   if (g.splits < 1) g.splits = 1;
@@ -505,7 +657,9 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
   } else {
     gemm_slow(g, elem, a_mode, b_mode, tile_cfg, s);
   }
-  if (g.splits > 1 && g.stats) {
+  if (g.splits > 1 && gn) {
+    launch_splitk_reduce_gn(g, *gn, s);  // g.part_cpg set by the caller
+  } else if (g.splits > 1 && g.stats) {
     k_splitk_reduce_stats<<<dim3(g.N / 32, (g.M + 63) / 64, g.batch), 256, 0, s>>>(g);
   } else if (g.splits > 1) {
     uint32_t ncols = g.act == ACT_GEGLU ? g.N / 2 : g.N;

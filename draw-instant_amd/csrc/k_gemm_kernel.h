@@ -277,6 +277,17 @@ __device__ __forceinline__ void epi_load(const GemmArgs& g, uint32_t m0, uint32_
   }
 }
 
+// Offset of partial (m, n) within one split's [M][N] block: row-major, or in
+// column groups of g.part_cpg (GemmArgs::part_cpg).  The group index comes
+// from a float reciprocal: exact for n < 2^21 (the product stays 0.5 /
+// part_cpg away from an integer, far beyond its rounding error).
+__device__ __forceinline__ uint64_t part_offset(const GemmArgs& g, uint32_t m, uint32_t n) {
+  if (!g.part_cpg) return (uint64_t)m * g.N + n;
+  const uint32_t gi =
+      (uint32_t)(((float)n + 0.5f) * __builtin_amdgcn_rcpf((float)g.part_cpg));
+  return ((uint64_t)gi * g.M + m) * g.part_cpg + (n - gi * g.part_cpg);
+}
+
 // GEGLU vector v of a thread: 8 outputs of tile row r from hidden columns
 // cl .. cl + 7 and gate columns cl + 16 .. cl + 23 (32-column groups
 // [16 hidden | 16 gate]), written at output column f
@@ -359,7 +370,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
       if (idx < BM * VPR4) {
         const int r = idx / VPR4, c4 = (idx % VPR4) * 4;
         const uint32_t m = m0 + r, n = n0 + c4;
-        if (m < g.M && n < g.N) *(f32x4*)&P[(uint64_t)m * g.N + n] = tile4(r * LDC + c4);
+        if (m < g.M && n < g.N) *(f32x4*)&P[part_offset(g, m, n)] = tile4(r * LDC + c4);
       }
     }
     return;
@@ -1120,7 +1131,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           uint32_t m = m0 + wm0 + a * 16 + rq + i;
-          if (m < g.M && n < g.N) P[(uint64_t)m * g.N + n] = acc[a][b][i];
+          if (m < g.M && n < g.N) P[part_offset(g, m, n)] = acc[a][b][i];
         }
       }
     return;

@@ -67,6 +67,8 @@ def _tf_sd(rng, p, c, cross):
     (1, 1280, 1280, 16, 16, False), # fused-resnet.js SHAPE (no temb, identity skip)
     (2, 640, 640, 16, 16, True),    # batch 2
     (1, 1280, 1280, 8, 8, True),    # 8x8: split-K conv1 with GroupNorm in the reducer
+    (2, 1280, 1280, 8, 8, True),    # the same, two images (one reducer workgroup row each)
+    (1, 1280, 1280, 16, 16, True),  # 16x16: conv1 split 5, GN2 + SiLU applied by its reducer
 ])
 def test_resnet_block(dev, rng, B, cin, cout, H, W, temb):
     from drawinstant import blocks
@@ -85,6 +87,43 @@ def test_resnet_block(dev, rng, B, cin, cout, H, W, temb):
     err = rel_l2(got, ref)
     print(f"   rel-L2 {err:.2e} max-abs {np.max(np.abs(got - ref)):.2e}", flush=True)
     assert err <= 1e-2
+    w.destroy()
+
+
+@pytest.mark.parametrize("B,cin,cout,H,W", [
+    (1, 1280, 1280, 8, 8),    # conv1 split 12: one row-step of 64 pixels per thread
+    (2, 1280, 1280, 16, 16),  # split 5, four row-steps, two images
+    (1, 320, 640, 32, 32),    # 20 channels per group, sixteen row-steps
+    (1, 2560, 1280, 8, 8),    # up-block input width (K = 23040)
+])
+def test_resnet_gn_reducer_matches_apply(dev, rng, monkeypatch, B, cin, cout, H, W):
+    """conv1's GroupNorm2 + SiLU applied by its split-K reducer against the
+    same block with the separate statistics + apply launches
+    (DI_GN_REDUCE_FUSE=0): the fp16 conv1 values are the same, only the
+    order of the statistics' fp32 sums differs, so the block outputs agree
+    to fp16 rounding."""
+    from drawinstant import blocks
+    print(f"[resnet gn reducer] B={B} {cin}->{cout} {H}x{W}", flush=True)
+    sd = _res_sd(rng, "r", cin, cout, 1280)
+    x = _q(rng.standard_normal((B, cin, H, W)))
+    t = rng.standard_normal((B, 1280)).astype(np.float32)
+    w = blocks.upload_resnet(dev, sd, "r")
+    bx = dev.storage(x.transpose(0, 2, 3, 1).astype(np.float16))
+    bt = dev.storage(t)
+    outs = []
+    for mode in ("1", "0"):
+        monkeypatch.setenv("DI_GN_REDUCE_FUSE", mode)
+        y = dev.create_buffer(B * H * W * cout * 2)
+        blocks.resnet_block(dev, w, bx, bt, y, B, cin, cout, H, W, 1280)
+        outs.append(dev.download(y, np.float16).astype(np.float32))
+    fused, sep = outs
+    err = rel_l2(fused, sep)
+    scale = float(np.max(np.abs(sep)))
+    print(f"   rel-L2 {err:.2e} max-abs {np.max(np.abs(fused - sep)):.2e} (max |y| {scale:.2f})",
+          flush=True)
+    assert np.all(np.isfinite(fused))
+    assert err <= 1e-3
+    assert np.max(np.abs(fused - sep)) <= 4e-3 * max(scale, 1.0)
     w.destroy()
 
 
