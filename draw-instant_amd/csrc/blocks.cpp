@@ -170,7 +170,8 @@ int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const
 }
 
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, const float* temb,
-                   uint32_t ld_temb, f16* out, const GnStats* x_st, StatsOut* out_st) {
+                   uint32_t ld_temb, f16* out, const GnStats* x_st, StatsOut* out_st,
+                   GnFuseOut* out_gn) {
   const uint32_t HW = s.H * s.W;
   const uint64_t rows = (uint64_t)s.B * HW;
   // conv1 hands GN2 the statistics of its output (no partial pass)
@@ -254,11 +255,14 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
   c2.ldr = ldr;
   c2.y = out;
   c2.stats = out_st;
+  if (out_gn) out_gn->done = false;
+  if (out_gn && !gn2_off()) c2.gn = out_gn;
   return conv_nhwc(c, c2);
 }
 
 int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s, const f16* x,
-                        const f16* context, f16* out, const GnStats* x_st, StatsOut* out_st) {
+                        const f16* context, f16* out, const GnStats* x_st, StatsOut* out_st,
+                        const f16* x_gn) {
   const uint32_t HW = s.H * s.W, C = s.C;
   const uint64_t rows = (uint64_t)s.B * HW;
   Scratch t, h, n, qkv, a, q, kv, gg, rs;
@@ -276,7 +280,10 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
   if (rc) return rc;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
   // GN (eps 1e-6 in diffusers Transformer2DModel) -> proj_in
-  rc = gn_nhwc(c, single(x, C), w.n_g, w.n_b, t.h(), s.B, C, s.groups, HW, s.gn_eps, false, x_st);
+  if (!x_gn) {
+    rc = gn_nhwc(c, single(x, C), w.n_g, w.n_b, t.h(), s.B, C, s.groups, HW, s.gn_eps, false, x_st);
+    x_gn = t.h();
+  }
   // a producer of h writes its row statistics when the next LayerNorm is folded
   RowStatsOut ro{rs.f(), rs_bytes};
   auto ro_for = [&](const float* fs) {
@@ -284,7 +291,7 @@ int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s
     return fs ? &ro : nullptr;
   };
   if (!rc)
-    rc = linear_f16(c, t.h(), C, rows, C, w.pin_w, C, w.pin_b, ACT_NONE, nullptr, 0, h.h(), C,
+    rc = linear_f16(c, x_gn, C, rows, C, w.pin_w, C, w.pin_b, ACT_NONE, nullptr, 0, h.h(), C,
                     nullptr, ro_for(w.qkv_s));
   if (rc) return rc;
   // y = LayerNorm(h) @ W^T (+ bias / act).  With folded weights (fs set)

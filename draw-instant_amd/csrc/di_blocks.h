@@ -105,10 +105,12 @@ struct ResnetShape {
 // x_st: GroupNorm statistics of x from its producer (null: GN1 computes
 // them); out_st: if non-null, asks for out's statistics ([B*HW/64][Cout]
 // pairs, see GnStats; needs HW % 64 == 0) and reports whether they were
-// written.
+// written.  out_gn: if non-null, asks conv2's split-K reducer to apply the
+// next block's GroupNorm to out as well (GnFuse with raw = 1) and reports
+// whether it did; out's statistics are then not written.
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x,
                    const float* temb, uint32_t ld_temb, f16* out, const GnStats* x_st = nullptr,
-                   StatsOut* out_st = nullptr);
+                   StatsOut* out_st = nullptr, GnFuseOut* out_gn = nullptr);
 
 struct TransformerW {
   const float *n_g = nullptr, *n_b = nullptr;       // GroupNorm
@@ -150,9 +152,10 @@ struct TransformerShape {
 
 // out = proj_out(block(proj_in(GN(x)))) + x; context fp16 [B][Sctx][cross].
 // x_st / out_st: GroupNorm statistics of x and out, as for resnet_forward.
+// x_gn: GN(x) already computed by x's producer (then x_st is not used).
 int transformer_forward(Ctx* c, const TransformerW& w, const TransformerShape& s, const f16* x,
                         const f16* context, f16* out, const GnStats* x_st = nullptr,
-                        StatsOut* out_st = nullptr);
+                        StatsOut* out_st = nullptr, const f16* x_gn = nullptr);
 
 // NHWC conv through the implicit-GEMM kernel (fp16 in, fp16 or NCHW fp32 out).
 struct ConvCall {

@@ -131,9 +131,11 @@ void launch_conv_in(hipStream_t s, const float* x, const _Float16* w, const floa
                     _Float16* y, float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W);
 // GroupNorm (+SiLU) of a split-K conv's output applied by its reducer: the
 // output rows are hw-pixel images of N channels in `groups` groups;
-// y[rows][ldy] = GN(out) (+SiLU) in fp16 is the only thing written (no raw
-// output, no statistics).  For a conv whose output feeds that GroupNorm
-// and nothing else (a ResNet's conv1).
+// y[rows][ldy] = GN(out) (+SiLU) in fp16, and the output itself only when
+// raw is set (no statistics either way).  For a conv whose output feeds
+// that GroupNorm (a ResNet's conv1: raw = 0) or that GroupNorm and
+// consumers of the raw output that need no statistics (a ResNet's conv2
+// whose output enters a transformer: raw = 1).
 struct GnFuse {
   const float* gamma = nullptr;
   const float* beta = nullptr;
@@ -142,11 +144,13 @@ struct GnFuse {
   uint32_t groups = 0, hw = 0;
   float eps = 0.0f;
   int silu = 0;
+  int raw = 0;
 };
 // Whether the fused reducer takes this call (g with its plan's splits):
-// batch 1, split-K with a built (hw / 64, split count) pair, bias and a
-// per-image temb bias, no residual or activation, 4 | channels per group
-// <= 40, hw a multiple of 64 (64 to 1024 pixels).
+// batch 1, split-K with a built (rows per thread, split count) pair, a
+// bias, optionally a per-image temb bias and an fp16 residual, no
+// activation, 4 | channels per group <= 40, hw a multiple of 64 (64 to 1024
+// pixels; at most 256 with raw).
 bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f);
 // elem: DI_F16 or DI_F32 operand element type.  gn: see GnFuse (only with
 // g.splits > 1 and splitk_gn_ok).

@@ -245,18 +245,19 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
 
 // Split-K reduction fused with the GroupNorm (+SiLU) of its output (GnFuse):
 // workgroup (group, image) sums the partials of the group's cpg channels
-// over the image's HW = 64 IM rows in split order and applies x * alpha +
-// bias + temb bias as the vector reducer does (the same fp16 values), then
-// takes the group's mean and variance of those fp16 values
-// (E[x^2] - E[x]^2, clamped at 0: GroupNorm's statistics) inside the
-// workgroup and writes only GN(x) (+SiLU).  Thread t of RS Q (<= 640):
+// over the image's HW = RS IM rows in split order and applies x * alpha +
+// bias (+ temb bias) (+ residual, RES) as the vector reducer does (the same
+// fp16 values, stored as the output when f.raw), then takes the group's
+// mean and variance of those fp16 values (E[x^2] - E[x]^2, clamped at 0:
+// GroupNorm's statistics) inside the workgroup and writes GN(x) (+SiLU)
+// to f.y.  Thread t of RS Q (<= 640):
 // channel quad q = t % Q (Q = cpg / 4), rows t / Q + RS i, i < IM (HW = RS
 // IM), from partials the GEMM stored in column groups of cpg, so a wave
 // reads 1 KB contiguous per load.  The split count S
 // is a template parameter: the IM x S partial loads are straight-line code
 // in batches of at most 24, each batch issued before any of it is added (a
 // loop over splits would make the compiler wait for every load at its top).
-template <int IM, int S>
+template <int IM, int S, bool RES>
 __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, uint32_t Q,
                                                           uint32_t RS) {
   args_warm(g);
@@ -268,12 +269,19 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
   const uint32_t r0 = (uint32_t)(((float)tid + 0.5f) * __builtin_amdgcn_rcpf((float)Q));
   const uint32_t q = tid - r0 * Q, c = grp * Q * 4 + q * 4;
   const uint64_t row0 = (uint64_t)n * (RS * IM) + r0;
-  // per-channel operands first: loads retire in order, and these are needed
-  // only after the partials
+  // per-channel and residual operands first: loads retire in order, and
+  // these are needed only after the partials (without a temb bias the bias
+  // is loaded twice rather than a load under a branch)
   const f32x4 bb = ld4(g.bias + c);
-  const f32x4 tb = ld4(g.bias2 + (uint64_t)n * g.ld_b2 + c);
+  const f32x4 tb = ld4(g.bias2 ? g.bias2 + (uint64_t)n * g.ld_b2 + c : g.bias + c);
   const f32x4 gm = ld4(f.gamma + c);
   const f32x4 bt = ld4(f.beta + c);
+  f16x4 rr[RES ? IM : 1];
+  if constexpr (RES) {
+    const f16* R = (const f16*)g.res + row0 * g.ldr + c;
+#pragma unroll
+    for (int i = 0; i < IM; i++) rr[i] = *(const f16x4*)(R + (uint64_t)i * RS * g.ldr);
+  }
   // partials in column groups (part_cpg = cpg): the group's image block is
   // contiguous, thread t reads quads t, t + RS Q, ... of it
   const float* p = g.part + ((uint64_t)grp * g.M + row0) * (Q * 4) + q * 4;
@@ -306,7 +314,8 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
     for (int j = 0; j < 4; j++) {
       float v = acc[i][j] * g.alpha;
       v += bb[j];
-      v += tb[j];
+      if (g.bias2) v += tb[j];
+      if constexpr (RES) v += (float)rr[i][j];
       h[i][j] = (f16)v;
       const float x = (float)h[i][j];
       sum += x;
@@ -334,6 +343,11 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
   for (int j = 0; j < 4; j++) {
     a[j] = rstd * gm[j];
     b[j] = bt[j] - mean * a[j];
+  }
+  if (f.raw) {
+    f16* C = (f16*)g.c + row0 * g.ldc + c;
+#pragma unroll
+    for (int i = 0; i < IM; i++) *(f16x4*)(C + (uint64_t)i * RS * g.ldc) = h[i];
   }
   f16* y = (f16*)f.y + row0 * f.ldy + c;
 #pragma unroll
@@ -372,10 +386,13 @@ uint32_t splitk_gn_rs(uint32_t q, uint32_t hw) {
 void launch_splitk_reduce_gn(const GemmArgs& g, const GnFuse& f, hipStream_t s) {
   const uint32_t q = g.N / f.groups / 4, rs = splitk_gn_rs(q, f.hw), im = f.hw / rs;
   const dim3 grid(f.groups, g.M / f.hw), block(rs * q);
-#define DI_RGN_LAUNCH(IMV, SV)                                        \
-  if (im == IMV && g.splits == SV) {                                  \
-    k_splitk_reduce_gn<IMV, SV><<<grid, block, 0, s>>>(g, f, q, rs);  \
-    return;                                                           \
+#define DI_RGN_LAUNCH(IMV, SV)                                                \
+  if (im == IMV && g.splits == SV) {                                          \
+    if (g.res)                                                                \
+      k_splitk_reduce_gn<IMV, SV, true><<<grid, block, 0, s>>>(g, f, q, rs);  \
+    else                                                                      \
+      k_splitk_reduce_gn<IMV, SV, false><<<grid, block, 0, s>>>(g, f, q, rs); \
+    return;                                                                   \
   }
   DI_RGN_CASES(DI_RGN_LAUNCH)
 #undef DI_RGN_LAUNCH
@@ -604,10 +621,16 @@ uint32_t gemm_rstats_tiles(const GemmArgs& g, int tile_cfg) {
 bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f) {
   if (g.splits <= 1 || g.batch != 1 || !f.groups || !f.hw || !f.gamma || !f.beta || !f.y)
     return false;
+  // keeping the raw output (a residual read and a second store per value)
+  // pays at 16 x 16 and below: at 32 x 32 the fused conv2 reducer took
+  // 11.2 us against 5.0 + 5.0 us for the reducer and apply it replaces
+  if (f.raw && f.hw > 256) return false;
   const uint32_t cpg = g.N / f.groups;
   return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && f.hw % 64 == 0 &&
          splitk_gn_built(f.hw / splitk_gn_rs(cpg / 4, f.hw), g.splits) && g.M % f.hw == 0 &&
-         g.bias && g.bias2 && g.rows_b2 == f.hw && g.ld_b2 % 4 == 0 && !g.res &&
+         g.bias && (!g.bias2 || (g.rows_b2 == f.hw && g.ld_b2 % 4 == 0)) &&
+         (!g.res || (!g.res_f32 && g.ldr % 4 == 0 && ((uintptr_t)g.res & 7) == 0)) &&
+         (!f.raw || (g.c && g.ldc % 4 == 0 && ((uintptr_t)g.c & 7) == 0)) &&
          g.act == ACT_NONE && !g.c_f32 && !g.c_nchw && f.ldy % 4 == 0 &&
          ((uintptr_t)f.y & 7) == 0 && ((uintptr_t)g.bias & 15) == 0 &&
          ((uintptr_t)g.bias2 & 15) == 0 && ((uintptr_t)f.gamma & 15) == 0 &&

@@ -432,22 +432,42 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   auto st_done = [](Act& a) { a.has_st = a.so.done; };
   auto st_of = [](const Act& a) { return GnStats{a.st.f(), a.st.f(), a.c, a.c, a.c}; };
   auto resnet = [&](const ResIdx& r, NhwcSrc x, const GnStats* xs, uint32_t hh, uint32_t ww,
-                    Act& y) {
+                    Act& y, GnFuseOut* og = nullptr) {
     ResnetShape s{B, hh, ww, r.cin, r.cout, G, cf.resnet_eps};
     const int r2 = resnet_forward(c, res_w(u, r), s, x, tproj.f() + r.temb_row, u.temb_rows,
-                                  y.buf.h(), xs, st_out(y));
+                                  y.buf.h(), xs, st_out(y), og);
     st_done(y);
     return r2;
   };
-  auto transformer = [&](const TfIdx& t, const Act& x, uint32_t hh, uint32_t ww, Act& y) {
+  auto transformer = [&](const TfIdx& t, const Act& x, uint32_t hh, uint32_t ww, Act& y,
+                         const f16* xg = nullptr) {
     TransformerShape s{B, hh, ww, t.c, Sctx, cf.cross_dim, G, cf.transformer_gn_eps, cf.ln_eps};
     TransformerW w = tf_w(u, t);
     w.kv_pre = kvall.h() + t.kv_row;
     w.kv_ld = u.kv_rows;
     const GnStats xs = st_of(x);
     const int r2 = transformer_forward(c, w, s, x.buf.h(), ctx16.h(), y.buf.h(),
-                                       x.has_st ? &xs : nullptr, st_out(y));
+                                       x.has_st ? &xs : nullptr, st_out(y), xg);
     st_done(y);
+    return r2;
+  };
+  // A ResNet output that enters a transformer: the transformer's GroupNorm
+  // requested from the ResNet's conv2 reducer (GnFuse, raw output kept),
+  // into gbuf; o.done reports whether it ran (else the transformer applies
+  // it from the output's statistics)
+  auto tf_gn = [&](const TfIdx& t, uint32_t hh, uint32_t ww, uint32_t ch, Scratch& gbuf,
+                   GnFuseOut& o) {
+    const int r2 = gbuf.alloc(c, (uint64_t)B * hh * ww * ch * 2);
+    const TransformerW w = tf_w(u, t);
+    o.f.gamma = w.n_g;
+    o.f.beta = w.n_b;
+    o.f.y = gbuf.h();
+    o.f.ldy = ch;
+    o.f.groups = G;
+    o.f.hw = hh * ww;
+    o.f.eps = cf.transformer_gn_eps;
+    o.f.silu = 0;
+    o.f.raw = 1;
     return r2;
   };
   auto one = [](const f16* p, uint32_t ch) { return NhwcSrc{p, p, ch, ch, ch}; };
@@ -488,13 +508,19 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
       const ResIdx& r = lv.res[j];
       Act nxt;
       const GnStats xs = st_of(hcur);
+      Scratch gbuf;
+      GnFuseOut og;
+      const bool tf = !lv.tf.empty();
       rc = act_alloc(nxt, hh, ww, r.cout);
-      if (!rc) rc = resnet(r, one(hcur.buf.h(), ch), hcur.has_st ? &xs : nullptr, hh, ww, nxt);
+      if (!rc && tf) rc = tf_gn(lv.tf[j], hh, ww, r.cout, gbuf, og);
+      if (!rc)
+        rc = resnet(r, one(hcur.buf.h(), ch), hcur.has_st ? &xs : nullptr, hh, ww, nxt,
+                    tf ? &og : nullptr);
       if (rc) return rc;
-      if (!lv.tf.empty()) {
+      if (tf) {
         Act t2;
         rc = act_alloc(t2, hh, ww, r.cout);
-        if (!rc) rc = transformer(lv.tf[j], nxt, hh, ww, t2);
+        if (!rc) rc = transformer(lv.tf[j], nxt, hh, ww, t2, og.done ? gbuf.h() : nullptr);
         if (rc) return rc;
         nxt = std::move(t2);
       }
@@ -533,10 +559,15 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   Act m1, m2, m3;
   const Act& mid_in = skips.back();
   const GnStats ms = st_of(mid_in);
+  Scratch mgbuf;
+  GnFuseOut mog;
   rc = act_alloc(m1, hh, ww, ch);
-  if (!rc) rc = resnet(u.mid_res[0], one(mid_in.buf.h(), ch), mid_in.has_st ? &ms : nullptr, hh, ww, m1);
+  if (!rc) rc = tf_gn(u.mid_tf, hh, ww, ch, mgbuf, mog);
+  if (!rc)
+    rc = resnet(u.mid_res[0], one(mid_in.buf.h(), ch), mid_in.has_st ? &ms : nullptr, hh, ww, m1,
+                &mog);
   if (!rc) rc = act_alloc(m2, hh, ww, ch);
-  if (!rc) rc = transformer(u.mid_tf, m1, hh, ww, m2);
+  if (!rc) rc = transformer(u.mid_tf, m1, hh, ww, m2, mog.done ? mgbuf.h() : nullptr);
   const GnStats m2s = st_of(m2);
   if (!rc) rc = act_alloc(m3, hh, ww, ch);
   if (!rc) rc = resnet(u.mid_res[1], one(m2.buf.h(), ch), m2.has_st ? &m2s : nullptr, hh, ww, m3);
@@ -554,19 +585,24 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
       Act sk = std::move(skips.back());
       skips.pop_back();
       Act nxt;
+      Scratch gbuf;
+      GnFuseOut og;
+      const bool tf = !lv.tf.empty();
       rc = act_alloc(nxt, hh, ww, r.cout);
+      if (!rc && tf) rc = tf_gn(lv.tf[j], hh, ww, r.cout, gbuf, og);
       if (rc) return rc;
       NhwcSrc cat{hcur.buf.h(), sk.buf.h(), ch, ch, sk.c};
       const GnStats cs{hcur.st.f(), sk.st.f(), ch, ch, sk.c};
-      rc = resnet(r, cat, hcur.has_st && sk.has_st ? &cs : nullptr, hh, ww, nxt);
+      rc = resnet(r, cat, hcur.has_st && sk.has_st ? &cs : nullptr, hh, ww, nxt,
+                  tf ? &og : nullptr);
       if (rc) return rc;
       sk.buf.release();
       sk.st.release();
       ch = r.cout;
-      if (!lv.tf.empty()) {
+      if (tf) {
         Act t2;
         rc = act_alloc(t2, hh, ww, ch);
-        if (!rc) rc = transformer(lv.tf[j], nxt, hh, ww, t2);
+        if (!rc) rc = transformer(lv.tf[j], nxt, hh, ww, t2, og.done ? gbuf.h() : nullptr);
         if (rc) return rc;
         nxt = std::move(t2);
       }

@@ -176,6 +176,23 @@ def test_sd21_step_b4_batch_independent(sd21, rng):
     assert err <= 1e-2
 
 
+def test_sd21_gn_in_reducers_matches_separate(sd21, rng, monkeypatch):
+    """cfg5 at B=1 with the GroupNorms that split-K reducers apply (each
+    ResNet's GN2 in conv1's reducer; a transformer's GN in the conv2 reducer
+    of the ResNet before it) against the same step with every GroupNorm as
+    its own apply launch (DI_GN_REDUCE_FUSE=0).  The fp16 values the
+    GroupNorms read are the same; only the fp32 summation order of their
+    statistics differs."""
+    x, ctx = _inputs(rng, 1, 64, 64, 77, 1024)
+    fused = sd21(x, 999.0, ctx)
+    monkeypatch.setenv("DI_GN_REDUCE_FUSE", "0")
+    sep = sd21(x, 999.0, ctx)
+    err = rel_l2(fused, sep)
+    print(f"[sd21 gn reducers] rel-L2 {err:.2e} max-abs {np.max(np.abs(fused - sep)):.2e}",
+          flush=True)
+    assert np.isfinite(fused).all() and err <= 2e-3
+
+
 def test_sd21_graph_replay_matches_eager(dev, sd21, rng):
     """Eager twice is bit-identical; the captured graph replayed several times,
     with eager work and synchronisation in between, matches eager exactly."""
