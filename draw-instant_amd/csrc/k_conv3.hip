@@ -294,13 +294,32 @@ __global__ __launch_bounds__(CV_NT) void k_conv3_halo(GemmArgs g) {
 // wave w takes pixels 16w .. 16w + 15, two 16-channel blocks.
 constexpr int CI_CS = 32, CI_LDY = CI_CS + 8;
 
+// With cn > 0 the grid has one more row of workgroups (blockIdx.y = Cout /
+// CI_CS) that converts cn fp32 values cx -> fp16 cy (the U-Net's context;
+// cn % 8 == 0, 16-byte aligned), so that conversion costs no launch of its
+// own.
 template <int CIN>
 __global__ __launch_bounds__(256) void k_conv_in(const float* __restrict__ x,
                                                  const f16* __restrict__ w,
                                                  const float* __restrict__ bias,
                                                  f16* __restrict__ y, float* __restrict__ stats,
-                                                 uint32_t Cout, uint32_t H, uint32_t W) {
+                                                 uint32_t Cout, uint32_t H, uint32_t W,
+                                                 const float* __restrict__ cx,
+                                                 f16* __restrict__ cy, uint32_t cn) {
   static_assert(CIN <= 8, "weights padded to 8 channels per tap");
+  if (cn && blockIdx.y == Cout / CI_CS) {
+    for (uint32_t i = (blockIdx.x * 256 + threadIdx.x) * 8; i < cn; i += gridDim.x * 256 * 8) {
+      const f32x4 a = *(const f32x4*)(cx + i), b = *(const f32x4*)(cx + i + 4);
+      f16x8 o;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        o[j] = (f16)a[j];
+        o[j + 4] = (f16)b[j];
+      }
+      *(f16x8*)(cy + i) = o;
+    }
+    return;
+  }
   __shared__ __attribute__((aligned(16))) f16 sy[64 * CI_LDY];  // [pixel][co]
   __shared__ float sst[4][CI_CS][2];                             // per-wave channel sums
   const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -405,10 +424,17 @@ bool conv_in_direct_ok(uint32_t Cin, uint32_t Cout, uint32_t H, uint32_t W) {
   return Cin == 4 && Cout % CI_CS == 0 && (H * W) % 64 == 0;
 }
 
+bool conv_in_convert_ok(const float* cx, const void* cy, uint64_t cn) {
+  return cn > 0 && cn % 8 == 0 && cn < (1ull << 31) && ((uintptr_t)cx & 15) == 0 &&
+         ((uintptr_t)cy & 15) == 0;
+}
+
 void launch_conv_in(hipStream_t s, const float* x, const f16* w, const float* bias, f16* y,
-                    float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W) {
-  k_conv_in<4><<<dim3(B * H * W / 64, Cout / CI_CS), 256, 0, s>>>(x, w, bias, y, stats, Cout, H,
-                                                                  W);
+                    float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W,
+                    const float* cx, f16* cy, uint64_t cn) {
+  const bool conv = conv_in_convert_ok(cx, cy, cn);
+  k_conv_in<4><<<dim3(B * H * W / 64, Cout / CI_CS + (conv ? 1 : 0)), 256, 0, s>>>(
+      x, w, bias, y, stats, Cout, H, W, cx, cy, conv ? (uint32_t)cn : 0u);
 }
 
 void launch_conv3_halo(const GemmArgs& g, hipStream_t s) {

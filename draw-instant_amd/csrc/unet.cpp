@@ -357,17 +357,24 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   if (!ci_direct)
     launch_layout(c->stream, sample, DI_F32, DI_NCHW, x16.p, DI_F16, DI_NHWC, B, cf.in_channels,
                   H, W, cin_p);
-  launch_convert(c->stream, context, DI_F32, ctx16.p, DI_F16, (uint64_t)B * Sctx * cf.cross_dim);
+  // the context's fp32 -> fp16 conversion rides in conv_in's launch where
+  // the direct conv_in runs (then the K / V GEMM below follows conv_in)
+  const uint64_t ctx_n = (uint64_t)B * Sctx * cf.cross_dim;
+  const bool ctx_in_conv_in = ci_direct && conv_in_convert_ok(context, ctx16.p, ctx_n);
+  if (!ctx_in_conv_in) launch_convert(c->stream, context, DI_F32, ctx16.p, DI_F16, ctx_n);
   // every transformer's attn2 K / V of the context: one GEMM over the
   // stacked [kv_rows][cross] weights -> kvall [B*Sctx][kv_rows]
   Scratch kvall;
-  if (u.kv_rows) {
-    rc = kvall.alloc(c, (uint64_t)B * Sctx * u.kv_rows * 2);
-    if (!rc)
-      rc = linear_f16(c, ctx16.h(), cf.cross_dim, B * Sctx, cf.cross_dim, (const f16*)u.arena[AR_KV16],
-                      u.kv_rows, nullptr, ACT_NONE, nullptr, 0, kvall.h(), u.kv_rows);
-    if (rc) return rc;
-  }
+  if (u.kv_rows) rc = kvall.alloc(c, (uint64_t)B * Sctx * u.kv_rows * 2);
+  if (rc) return rc;
+  auto kv_gemm = [&]() {
+    if (!u.kv_rows) return (int)DI_OK;
+    return linear_f16(c, ctx16.h(), cf.cross_dim, B * Sctx, cf.cross_dim,
+                      (const f16*)u.arena[AR_KV16], u.kv_rows, nullptr, ACT_NONE, nullptr, 0,
+                      kvall.h(), u.kv_rows);
+  };
+  if (!ctx_in_conv_in) rc = kv_gemm();
+  if (rc) return rc;
   // time embedding: sinusoid -> linear_1 + SiLU -> linear_2 -> every
   // ResNet's time_emb_proj(SiLU(temb)) in one GEMV
   GemvArgs g1;
@@ -480,10 +487,16 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   rc = act_alloc(hcur, hh, ww, ch);
   if (rc) return rc;
   if (ci_direct) {
-    launch_conv_in(c->stream, sample, u.h(u.conv_in_w), u.f(u.conv_in_b), hcur.buf.h(),
-                   hcur.st.f(), B, ch, hh, ww);
+    if (ctx_in_conv_in)
+      launch_conv_in(c->stream, sample, u.h(u.conv_in_w), u.f(u.conv_in_b), hcur.buf.h(),
+                     hcur.st.f(), B, ch, hh, ww, context, ctx16.h(), ctx_n);
+    else
+      launch_conv_in(c->stream, sample, u.h(u.conv_in_w), u.f(u.conv_in_b), hcur.buf.h(),
+                     hcur.st.f(), B, ch, hh, ww);
     hcur.so.done = hcur.st.f() != nullptr;
     st_done(hcur);
+    if (ctx_in_conv_in) rc = kv_gemm();
+    if (rc) return rc;
   } else {
     ConvCall cc;
     cc.x = one(x16.h(), cin_p);
