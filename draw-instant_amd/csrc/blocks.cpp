@@ -61,6 +61,10 @@ int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rs
     g.part = (float*)ws;
   }
   if (gn && gn->done) g.part_cpg = g.N / gn->f.groups;
+  if (g.splits <= 1) {
+    DI_REQUIRE(!g.part_only && !g.part_slots, DI_EINVAL,
+               "shared partial slots need a plan that splits (M=%u N=%u K=%u)", g.M, g.N, g.K);
+  }
   launch_gemm(g, DI_F16, a_mode, B_NK, tile, c->stream, gn && gn->done ? &gn->f : nullptr);
   return DI_OK;
 }
@@ -87,6 +91,13 @@ int gn_nhwc(Ctx* c, NhwcSrc x, const float* g, const float* b, f16* y, uint32_t 
 
 NhwcSrc single(const f16* p, uint32_t C) { return NhwcSrc{p, p, C, C, C}; }
 
+// DI_SK_PARTIALS=0 keeps a ResNet's 1x1 shortcut as its own GEMM + reducer
+// (comparison runs; read at every block call)
+bool sk_partials_off() {
+  const char* e = getenv("DI_SK_PARTIALS");
+  return e && e[0] == '0';
+}
+
 // DI_GN_REDUCE_FUSE=0 keeps conv1's GroupNorm as its own apply launch
 // (comparison runs; read at every block call, so a test can switch it)
 bool gn2_off() {
@@ -96,7 +107,7 @@ bool gn2_off() {
 
 }  // namespace
 
-int conv_nhwc(Ctx* c, const ConvCall& cc) {
+GemmArgs conv_args(const ConvCall& cc) {
   GemmArgs g;
   g.a = cc.x.p1;
   g.a2 = cc.x.p2;
@@ -136,6 +147,19 @@ int conv_nhwc(Ctx* c, const ConvCall& cc) {
   } else {
     g.ldc = cc.ldc ? cc.ldc : cc.Cout;
   }
+  g.part_slot0 = cc.part_slot0;
+  g.part_slots = cc.part_slots;
+  g.part_cpg = cc.part_cpg;
+  g.part_only = cc.part_only;
+  return g;
+}
+
+GemmPlan conv_plan(Ctx* c, const ConvCall& cc) {
+  return gemm_plan(conv_args(cc), DI_F16, c->num_cus);
+}
+
+int conv_nhwc(Ctx* c, const ConvCall& cc) {
+  GemmArgs g = conv_args(cc);
   return run(c, g, A_CONV_NHWC, cc.stats, nullptr, cc.gn);
 }
 
@@ -218,11 +242,20 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
                  s.eps, true, so2.done ? &s2 : nullptr);
     if (rc) return rc;
   }
-  const f16* res = nullptr;
-  uint64_t ldr = s.Cout;
+  ConvCall c2;
+  c2.x = single(t3.h(), s.Cout);
+  c2.B = s.B;
+  c2.H = s.H;
+  c2.W = s.W;
+  c2.Cin = s.Cout;
+  c2.Cout = s.Cout;
+  c2.w = w.c2_w;
+  c2.bias = w.c2_b;
+  c2.y = out;
+  c2.stats = out_st;
+  if (out_gn) out_gn->done = false;
+  if (out_gn && !gn2_off()) c2.gn = out_gn;
   if (w.sk_w) {
-    rc = sk.alloc(c, rows * s.Cout * 2);
-    if (rc) return rc;
     ConvCall k1;
     k1.x = x;
     k1.B = s.B;
@@ -234,29 +267,38 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
     k1.pad = 0;
     k1.w = w.sk_w;
     k1.bias = w.sk_b;
+    // Both split: the shortcut writes its partials into slots after
+    // conv2's, launches no reducer, and conv2's reducer sums every slot
+    // with the summed bias (conv2 + shortcut = one sum over both k ranges)
+    const GemmPlan pk = conv_plan(c, k1), p2 = conv_plan(c, c2);
+    if (w.c2sk_b && !sk_partials_off() && pk.splits > 1 && p2.splits > 1) {
+      const uint32_t slots = pk.splits + p2.splits;
+      c2.bias = w.c2sk_b;
+      c2.part_slots = slots;
+      if (c2.gn) {
+        // the fused GroupNorm reducer reads the partials in column groups
+        GemmArgs g2 = conv_args(c2);
+        g2.splits = p2.splits;
+        if (splitk_gn_ok(g2, c2.gn->f)) k1.part_cpg = s.Cout / c2.gn->f.groups;
+      }
+      k1.part_slot0 = p2.splits;
+      k1.part_slots = slots;
+      k1.part_only = 1;
+      rc = conv_nhwc(c, k1);
+      if (rc) return rc;
+      return conv_nhwc(c, c2);
+    }
+    rc = sk.alloc(c, rows * s.Cout * 2);
+    if (rc) return rc;
     k1.y = sk.h();
     rc = conv_nhwc(c, k1);
     if (rc) return rc;
-    res = sk.h();
+    c2.res = sk.h();
+    c2.ldr = s.Cout;
   } else {
-    res = x.p1;  // Cin == Cout: identity skip, single source
-    ldr = x.ld1;
+    c2.res = x.p1;  // Cin == Cout: identity skip, single source
+    c2.ldr = x.ld1;
   }
-  ConvCall c2;
-  c2.x = single(t3.h(), s.Cout);
-  c2.B = s.B;
-  c2.H = s.H;
-  c2.W = s.W;
-  c2.Cin = s.Cout;
-  c2.Cout = s.Cout;
-  c2.w = w.c2_w;
-  c2.bias = w.c2_b;
-  c2.res = res;
-  c2.ldr = ldr;
-  c2.y = out;
-  c2.stats = out_st;
-  if (out_gn) out_gn->done = false;
-  if (out_gn && !gn2_off()) c2.gn = out_gn;
   return conv_nhwc(c, c2);
 }
 

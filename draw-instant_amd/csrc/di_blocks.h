@@ -92,6 +92,9 @@ struct ResnetW {
   const float* c2_b = nullptr;
   const f16* sk_w = nullptr;  // 1x1 [Cout][Cin], null when Cin == Cout
   const float* sk_b = nullptr;
+  // c2_b + sk_b (optional): lets conv2's split-K reducer sum the shortcut's
+  // partials with its own, so the shortcut needs no reducer of its own
+  const float* c2sk_b = nullptr;
 };
 
 struct ResnetShape {
@@ -172,8 +175,15 @@ struct ConvCall {
   int y_nchw_f32 = 0;
   StatsOut* stats = nullptr;  // GroupNorm statistics of y (GemmArgs::stats), optional
   GnFuseOut* gn = nullptr;    // GroupNorm of y applied by a split-K reducer, optional
+  // shared split-K partial slots (GemmArgs::part_slot0 / part_slots /
+  // part_only / part_cpg); only with a plan that splits
+  uint32_t part_slot0 = 0, part_slots = 0, part_cpg = 0;
+  int part_only = 0;
 };
 int conv_nhwc(Ctx* c, const ConvCall& cc);
+// The GEMM arguments conv_nhwc launches with, and their plan.
+GemmArgs conv_args(const ConvCall& cc);
+GemmPlan conv_plan(Ctx* c, const ConvCall& cc);
 
 // Linear on token rows: y = act(x w^T + b) (+ res); fp16.  stats: optional
 // GroupNorm statistics of y (GemmArgs::stats).

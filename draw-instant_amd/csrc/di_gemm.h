@@ -83,6 +83,13 @@ struct GemmArgs {
   // part_cpg | N), [splits][batch][N / part_cpg][M][part_cpg], so that one
   // group's values are contiguous (the GroupNorm-fused reducer's layout)
   uint32_t part_cpg = 0;
+  // Partials shared with another launch (a ResNet's 1x1 shortcut and its
+  // conv2): this launch writes slots part_slot0 + split of a buffer of
+  // part_slots slots ([part_slots][batch][M][N]; 0: its own splits);
+  // part_only = 1 launches no reducer (a later launch's reducer sums every
+  // slot), else the reducer sums all part_slots slots.
+  uint32_t part_slot0 = 0, part_slots = 0;
+  int part_only = 0;
   // Optional GroupNorm statistics of the stored output (see gemm_stats_ok):
   // per 64-row chunk of the M rows and per column, (sum, sum of squares) at
   // stats[((bz * ceil(M/64) + m/64) * N + n) * 2].

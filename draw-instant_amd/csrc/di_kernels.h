@@ -22,6 +22,8 @@ void launch_layout(hipStream_t s, const void* src, int sdt, int slay, void* dst,
 void launch_fill_normal(hipStream_t s, void* dst, int dt, uint64_t n, uint64_t seed,
                         float mean, float std);
 void launch_fill_const(hipStream_t s, void* dst, int dt, uint64_t n, float v);
+// y = a + b, n fp32 values.
+void launch_add_f32(hipStream_t s, const float* a, const float* b, float* y, uint64_t n);
 // Row softmax of [rows][inner] (in place allowed).
 void launch_softmax(hipStream_t s, const void* x, void* y, uint32_t inner, uint32_t rows, int dt);
 // fp16 per-batch matrix transpose: y[b][c][r] = x[b * sx + r * ldx + c] for

@@ -349,6 +349,14 @@ __global__ void k_reduce_mean(const T* __restrict__ x, T* __restrict__ y, uint32
 
 }  // namespace
 
+// y = a + b over n fp32 values (derived parameters, e.g. summed biases)
+__global__ void k_add_f32(const float* __restrict__ a, const float* __restrict__ b,
+                          float* __restrict__ y, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x)
+    y[i] = a[i] + b[i];
+}
+
 void launch_convert(hipStream_t s, const void* src, int sdt, void* dst, int ddt, uint64_t n) {
   unsigned g = grid_for(n, 4);
   if (sdt == DI_F32 && ddt == DI_F16)
@@ -398,6 +406,10 @@ void launch_fill_const(hipStream_t s, void* dst, int dt, uint64_t n, float v) {
   unsigned g = grid_for(n);
   if (dt == DI_F32) k_fill_const<float><<<g, kBlock, 0, s>>>((float*)dst, n, v);
   else k_fill_const<f16><<<g, kBlock, 0, s>>>((f16*)dst, n, v);
+}
+
+void launch_add_f32(hipStream_t s, const float* a, const float* b, float* y, uint64_t n) {
+  k_add_f32<<<grid_for(n), kBlock, 0, s>>>(a, b, y, n);
 }
 
 }  // namespace di

@@ -565,7 +565,8 @@ void launch_repack_oihw_ohwi(hipStream_t s, const void* w, int wdt, void* out, u
 }
 
 uint64_t gemm_ws_bytes(const GemmArgs& g) {
-  return g.splits > 1 ? (uint64_t)g.splits * g.batch * g.M * g.N * sizeof(float) : 0;
+  const uint64_t slots = g.part_slots ? g.part_slots : g.splits;
+  return g.splits > 1 ? slots * g.batch * g.M * g.N * sizeof(float) : 0;
 }
 
 bool gemm_fast_ok(const GemmArgs& g, int elem, int a_mode, int b_mode) {
@@ -625,9 +626,9 @@ bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f) {
   // pays at 16 x 16 and below: at 32 x 32 the fused conv2 reducer took
   // 11.2 us against 5.0 + 5.0 us for the reducer and apply it replaces
   if (f.raw && f.hw > 256) return false;
-  const uint32_t cpg = g.N / f.groups;
+  const uint32_t cpg = g.N / f.groups, slots = g.part_slots ? g.part_slots : g.splits;
   return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && f.hw % 64 == 0 &&
-         splitk_gn_built(f.hw / splitk_gn_rs(cpg / 4, f.hw), g.splits) && g.M % f.hw == 0 &&
+         splitk_gn_built(f.hw / splitk_gn_rs(cpg / 4, f.hw), slots) && g.M % f.hw == 0 &&
          g.bias && (!g.bias2 || (g.rows_b2 == f.hw && g.ld_b2 % 4 == 0)) &&
          (!g.res || (!g.res_f32 && g.ldr % 4 == 0 && ((uintptr_t)g.res & 7) == 0)) &&
          (!f.raw || (g.c && g.ldc % 4 == 0 && ((uintptr_t)g.c & 7) == 0)) &&
@@ -680,6 +681,8 @@ void launch_gemm(GemmArgs g, int elem, int a_mode, int b_mode, int tile_cfg, hip
   } else {
     gemm_slow(g, elem, a_mode, b_mode, tile_cfg, s);
   }
+  if (g.splits > 1 && g.part_only) return;  // a later launch's reducer sums the slots
+  if (g.splits > 1 && g.part_slots) g.splits = g.part_slots;  // the reducers sum every slot
   if (g.splits > 1 && gn) {
     launch_splitk_reduce_gn(g, *gn, s);  // g.part_cpg set by the caller
   } else if (g.splits > 1 && g.stats) {

@@ -363,7 +363,7 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
   if (g.splits > 1) {
     constexpr int VPR4 = BN / 4;
     constexpr int NV = (BM * VPR4 + NT - 1) / NT;
-    float* P = g.part + ((uint64_t)split * g.batch + bz) * (uint64_t)g.M * g.N;
+    float* P = g.part + ((uint64_t)(split + g.part_slot0) * g.batch + bz) * (uint64_t)g.M * g.N;
 #pragma unroll
     for (int v = 0; v < NV; v++) {
       const int idx = tid + v * NT;
@@ -1122,7 +1122,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
         for (int i = 0; i < 4; i++) acc[a][b][i] += sC[(wm0 + a * 16 + rq + i) * LDC + wn0 + b * 16 + fr];
   }
   if (splits > 1) {
-    float* P = g.part + ((uint64_t)split * g.batch + bz) * (uint64_t)g.M * g.N;
+    float* P = g.part + ((uint64_t)(split + g.part_slot0) * g.batch + bz) * (uint64_t)g.M * g.N;
 #pragma unroll
     for (int a = 0; a < TM; a++)
 #pragma unroll

@@ -59,6 +59,8 @@ struct ResIdx {
   uint32_t cin, cout;
   int n1g, n1b, c1w, c1b, n2g, n2b, c2w, c2b, skw = -1, skb = -1, tw, tb;
   uint64_t temb_row;  // row offset inside the stacked time_emb_proj matrix
+  // with a shortcut: conv2's bias + the shortcut's, derived in AR_LN32
+  uint64_t fb_c2sk = 0;
 };
 
 struct TfIdx {
@@ -161,7 +163,11 @@ ResIdx add_resnet(UNet& u, const std::string& p, uint32_t cin, uint32_t cout) {
   u.temb_rows += cout;
   add_norm(u, p + ".norm2", cout, &r.n2g, &r.n2b);
   add_conv(u, p + ".conv2", cout, cout, 3, &r.c2w, &r.c2b);
-  if (cin != cout) add_conv(u, p + ".conv_shortcut", cout, cin, 1, &r.skw, &r.skb);
+  if (cin != cout) {
+    add_conv(u, p + ".conv_shortcut", cout, cin, 1, &r.skw, &r.skb);
+    r.fb_c2sk = (u.arena_elems[AR_LN32] + 3) / 4 * 4;
+    u.arena_elems[AR_LN32] = r.fb_c2sk + cout;
+  }
   return r;
 }
 
@@ -271,6 +277,7 @@ ResnetW res_w(const UNet& u, const ResIdx& r) {
   if (r.skw >= 0) {
     w.sk_w = u.h(r.skw);
     w.sk_b = u.f(r.skb);
+    if (u.ln_folded) w.c2sk_b = (const float*)u.arena[AR_LN32] + r.fb_c2sk;
   }
   return w;
 }
@@ -315,7 +322,8 @@ TransformerW tf_w(const UNet& u, const TfIdx& t) {
   return w;
 }
 
-// Derives every transformer's folded projections from the parameters.
+// Derives every transformer's folded projections and the summed conv2 +
+// shortcut biases of the ResNets from the parameters.
 void fold_layer_norms(hipStream_t s, UNet& u) {
   f16* fw = (f16*)u.arena[AR_LNW16];
   float* ff = (float*)u.arena[AR_LN32];
@@ -333,6 +341,15 @@ void fold_layer_norms(hipStream_t s, UNet& u) {
   one(u.mid_tf);
   for (const Level& l : u.up)
     for (const TfIdx& t : l.tf) one(t);
+  // summed conv2 + shortcut biases of the ResNets with a shortcut
+  auto res = [&](const ResIdx& r) {
+    if (r.skw >= 0) launch_add_f32(s, u.f(r.c2b), u.f(r.skb), ff + r.fb_c2sk, r.cout);
+  };
+  for (const Level& l : u.down)
+    for (const ResIdx& r : l.res) res(r);
+  for (const ResIdx& r : u.mid_res) res(r);
+  for (const Level& l : u.up)
+    for (const ResIdx& r : l.res) res(r);
 }
 
 // One denoise step (enqueue only).

@@ -193,6 +193,22 @@ def test_sd21_gn_in_reducers_matches_separate(sd21, rng, monkeypatch):
     assert np.isfinite(fused).all() and err <= 2e-3
 
 
+def test_sd21_shortcut_partials_match_separate(sd21, rng, monkeypatch):
+    """cfg5 at B=1 with each split-K ResNet shortcut's partials summed by its
+    conv2's reducer (with the summed bias) against the same step with the
+    shortcut as its own GEMM + reducer writing an fp16 tensor that conv2
+    adds (DI_SK_PARTIALS=0).  The two differ by that tensor's fp16 rounding
+    and the order of the fp32 sums."""
+    x, ctx = _inputs(rng, 1, 64, 64, 77, 1024)
+    fused = sd21(x, 999.0, ctx)
+    monkeypatch.setenv("DI_SK_PARTIALS", "0")
+    sep = sd21(x, 999.0, ctx)
+    err = rel_l2(fused, sep)
+    print(f"[sd21 shortcut partials] rel-L2 {err:.2e} max-abs {np.max(np.abs(fused - sep)):.2e}",
+          flush=True)
+    assert np.isfinite(fused).all() and err <= 2e-3
+
+
 def test_sd21_graph_replay_matches_eager(dev, sd21, rng):
     """Eager twice is bit-identical; the captured graph replayed several times,
     with eager work and synchronisation in between, matches eager exactly."""
