@@ -33,7 +33,9 @@ int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rs
   if (gn) gn->done = splitk_gn_ok(g, gn->f);
   if (st) st->done = false;
   if (gn && gn->done) {
-    // the reducer writes GN(output) only: no raw output, no statistics
+    // the reducer writes GN(output) (and the raw output and its statistics
+    // where the request asks: gn->f.raw / gn->f.stats)
+    if (st) st->done = gn->f.stats != nullptr && gn->f.stats == st->p;
   } else if (st && st->p) {
     st->done = gemm_stats_ok(g, DI_F16, a_mode, B_NK, tile);
     if (st->done) g.stats = st->p;
@@ -98,13 +100,6 @@ bool sk_partials_off() {
   return e && e[0] == '0';
 }
 
-// DI_GN_REDUCE_FUSE=0 keeps conv1's GroupNorm as its own apply launch
-// (comparison runs; read at every block call, so a test can switch it)
-bool gn2_off() {
-  const char* e = getenv("DI_GN_REDUCE_FUSE");
-  return e && e[0] == '0';
-}
-
 }  // namespace
 
 GemmArgs conv_args(const ConvCall& cc) {
@@ -158,6 +153,13 @@ GemmPlan conv_plan(Ctx* c, const ConvCall& cc) {
   return gemm_plan(conv_args(cc), DI_F16, c->num_cus);
 }
 
+// DI_GN_REDUCE_FUSE=0 keeps every GroupNorm as its own apply launch
+// (comparison runs; read at every block call, so a test can switch it)
+bool gn_reduce_fuse_off() {
+  const char* e = getenv("DI_GN_REDUCE_FUSE");
+  return e && e[0] == '0';
+}
+
 int conv_nhwc(Ctx* c, const ConvCall& cc) {
   GemmArgs g = conv_args(cc);
   return run(c, g, A_CONV_NHWC, cc.stats, nullptr, cc.gn);
@@ -195,21 +197,24 @@ int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const
 
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, const float* temb,
                    uint32_t ld_temb, f16* out, const GnStats* x_st, StatsOut* out_st,
-                   GnFuseOut* out_gn) {
+                   GnFuseOut* out_gn, const f16* x_gn) {
   const uint32_t HW = s.H * s.W;
   const uint64_t rows = (uint64_t)s.B * HW;
   // conv1 hands GN2 the statistics of its output (no partial pass)
   const bool st2 = HW % 64 == 0;
   Scratch t1, t2, t3, sk, t2st;
-  int rc = t1.alloc(c, rows * s.Cin * 2);
+  int rc = x_gn ? 0 : t1.alloc(c, rows * s.Cin * 2);
   if (!rc) rc = t2.alloc(c, rows * s.Cout * 2);
   if (!rc) rc = t3.alloc(c, rows * s.Cout * 2);
   if (!rc && st2) rc = t2st.alloc(c, gn_stats_floats(rows, s.Cout) * sizeof(float));
   if (rc) return rc;
-  rc = gn_nhwc(c, x, w.n1_g, w.n1_b, t1.h(), s.B, s.Cin, s.groups, HW, s.eps, true, x_st);
-  if (rc) return rc;
+  if (!x_gn) {
+    rc = gn_nhwc(c, x, w.n1_g, w.n1_b, t1.h(), s.B, s.Cin, s.groups, HW, s.eps, true, x_st);
+    if (rc) return rc;
+    x_gn = t1.h();
+  }
   ConvCall c1;
-  c1.x = single(t1.h(), s.Cin);
+  c1.x = single(x_gn, s.Cin);
   c1.B = s.B;
   c1.H = s.H;
   c1.W = s.W;
@@ -233,7 +238,7 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
   gn2.f.hw = HW;
   gn2.f.eps = s.eps;
   gn2.f.silu = 1;
-  if (!gn2_off()) c1.gn = &gn2;
+  if (!gn_reduce_fuse_off()) c1.gn = &gn2;
   rc = conv_nhwc(c, c1);
   if (rc) return rc;
   if (!gn2.done) {
@@ -254,7 +259,7 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
   c2.y = out;
   c2.stats = out_st;
   if (out_gn) out_gn->done = false;
-  if (out_gn && !gn2_off()) c2.gn = out_gn;
+  if (out_gn && !gn_reduce_fuse_off()) c2.gn = out_gn;
   if (w.sk_w) {
     ConvCall k1;
     k1.x = x;

@@ -110,10 +110,13 @@ struct ResnetShape {
 // pairs, see GnStats; needs HW % 64 == 0) and reports whether they were
 // written.  out_gn: if non-null, asks conv2's split-K reducer to apply the
 // next block's GroupNorm to out as well (GnFuse with raw = 1) and reports
-// whether it did; out's statistics are then not written.
+// whether it did; out's statistics are then written only where
+// out_gn->f.stats is out_st's buffer.  x_gn: GN1(x) + SiLU already computed
+// by x's producer (then x_st is not used).
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x,
                    const float* temb, uint32_t ld_temb, f16* out, const GnStats* x_st = nullptr,
-                   StatsOut* out_st = nullptr, GnFuseOut* out_gn = nullptr);
+                   StatsOut* out_st = nullptr, GnFuseOut* out_gn = nullptr,
+                   const f16* x_gn = nullptr);
 
 struct TransformerW {
   const float *n_g = nullptr, *n_b = nullptr;       // GroupNorm
@@ -181,6 +184,8 @@ struct ConvCall {
   int part_only = 0;
 };
 int conv_nhwc(Ctx* c, const ConvCall& cc);
+// DI_GN_REDUCE_FUSE=0: no GroupNorm applied by a split-K reducer.
+bool gn_reduce_fuse_off();
 // The GEMM arguments conv_nhwc launches with, and their plan.
 GemmArgs conv_args(const ConvCall& cc);
 GemmPlan conv_plan(Ctx* c, const ConvCall& cc);

@@ -156,12 +156,17 @@ struct GnFuse {
   float eps = 0.0f;
   int silu = 0;
   int raw = 0;
+  // with raw: also the GroupNorm statistics of the stored output in the
+  // GemmArgs::stats layout (per 64-row chunk and channel), for other
+  // GroupNorms that read it; null: none
+  float* stats = nullptr;
 };
 // Whether the fused reducer takes this call (g with its plan's splits):
 // batch 1, split-K with a built (rows per thread, split count) pair, a
 // bias, optionally a per-image temb bias and an fp16 residual, no
 // activation, 4 | channels per group <= 40, hw a multiple of 64 (64 to 1024
-// pixels; at most 256 with raw).
+// pixels; at most 256 with raw; statistics only with raw and 40 channels per
+// group).
 bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f);
 // elem: DI_F16 or DI_F32 operand element type.  gn: see GnFuse (only with
 // g.splits > 1 and splitk_gn_ok).

@@ -263,6 +263,7 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
   args_warm(g);
   kernarg_warm(f);
   __shared__ float red[2][10];
+  __shared__ __attribute__((aligned(16))) float sst[64 * 40];  // one chunk, f.stats only
   const uint32_t tid = threadIdx.x, grp = blockIdx.x, n = blockIdx.y;
   // tid / Q from a float reciprocal: exact for tid < 1024 (the product stays
   // 0.5 / Q away from an integer, far beyond its rounding error)
@@ -327,6 +328,34 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
   if (tid % 64 == 0) {
     red[0][tid / 64] = sum;
     red[1][tid / 64] = sq;
+  }
+  if (f.stats) {
+    // per 64-row chunk and channel (sum, sum of squares) of the stored
+    // values, the GemmArgs::stats layout (only with RS = 64: chunk i of the
+    // image is row step i).  Chunk by chunk through LDS: 8 adjacent lanes
+    // per (channel, statistic) each take every eighth row, added by lane
+    // swaps in a fixed order.
+    const uint32_t cpg = Q * 4, task = tid >> 3, part = tid & 7;
+    const uint32_t st = (uint32_t)(((float)task + 0.5f) * __builtin_amdgcn_rcpf((float)cpg));
+    const uint32_t ch = task - st * cpg;
+#pragma unroll
+    for (int i = 0; i < IM; i++) {
+      *(f32x4*)&sst[r0 * cpg + q * 4] =
+          f32x4{(float)h[i][0], (float)h[i][1], (float)h[i][2], (float)h[i][3]};
+      __syncthreads();
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float x = sst[(part + 8 * k) * cpg + ch];
+        a += st ? __fmul_rn(x, x) : x;
+      }
+      a += __shfl_xor(a, 1);
+      a += __shfl_xor(a, 2);
+      a += __shfl_xor(a, 4);
+      if (part == 0)
+        f.stats[(((uint64_t)n * IM + i) * g.N + grp * cpg + ch) * 2 + st] = a;
+      __syncthreads();
+    }
   }
   __syncthreads();
   float ps = 0.0f, pq = 0.0f;
@@ -626,6 +655,10 @@ bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f) {
   // pays at 16 x 16 and below: at 32 x 32 the fused conv2 reducer took
   // 11.2 us against 5.0 + 5.0 us for the reducer and apply it replaces
   if (f.raw && f.hw > 256) return false;
+  // statistics of the stored values: 64-row steps, 16 cpg threads
+  if (f.stats && (!f.raw || splitk_gn_rs(g.N / f.groups / 4, f.hw) != 64 ||
+                  ((uintptr_t)f.stats & 7) != 0))
+    return false;
   const uint32_t cpg = g.N / f.groups, slots = g.part_slots ? g.part_slots : g.splits;
   return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && f.hw % 64 == 0 &&
          splitk_gn_built(f.hw / splitk_gn_rs(cpg / 4, f.hw), slots) && g.M % f.hw == 0 &&

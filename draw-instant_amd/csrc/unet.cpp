@@ -456,11 +456,30 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   auto st_done = [](Act& a) { a.has_st = a.so.done; };
   auto st_of = [](const Act& a) { return GnStats{a.st.f(), a.st.f(), a.c, a.c, a.c}; };
   auto resnet = [&](const ResIdx& r, NhwcSrc x, const GnStats* xs, uint32_t hh, uint32_t ww,
-                    Act& y, GnFuseOut* og = nullptr) {
+                    Act& y, GnFuseOut* og = nullptr, const f16* xg = nullptr) {
     ResnetShape s{B, hh, ww, r.cin, r.cout, G, cf.resnet_eps};
     const int r2 = resnet_forward(c, res_w(u, r), s, x, tproj.f() + r.temb_row, u.temb_rows,
-                                  y.buf.h(), xs, st_out(y), og);
+                                  y.buf.h(), xs, st_out(y), og, xg);
     st_done(y);
+    return r2;
+  };
+  // An output that is the next ResNet's input and a skip: that ResNet's
+  // GN1 + SiLU requested from the producer's split-K reducer, which then
+  // also stores the raw output and its statistics (for the up path's
+  // concatenated GroupNorm), into gbuf; o.done reports whether it ran
+  auto res_gn = [&](const ResIdx& r, uint32_t hh, uint32_t ww, Act& y, Scratch& gbuf,
+                    GnFuseOut& o) {
+    const int r2 = gbuf.alloc(c, (uint64_t)B * hh * ww * r.cin * 2);
+    o.f.gamma = u.f(r.n1g);
+    o.f.beta = u.f(r.n1b);
+    o.f.y = gbuf.h();
+    o.f.ldy = r.cin;
+    o.f.groups = G;
+    o.f.hw = hh * ww;
+    o.f.eps = cf.resnet_eps;
+    o.f.silu = 1;
+    o.f.raw = 1;
+    o.f.stats = y.st.f();
     return r2;
   };
   auto transformer = [&](const TfIdx& t, const Act& x, uint32_t hh, uint32_t ww, Act& y,
@@ -532,6 +551,9 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   }
   // down path: conv_in's output, every resnet(+transformer) output and every
   // downsampler output become skips; the current tensor is always the last one
+  // GN1(hcur) + SiLU when hcur's producer applied it (gin_ok)
+  Scratch gin;
+  bool gin_ok = false;
   for (int i = 0; i < 4; i++) {
     Level& lv = u.down[i];
     for (size_t j = 0; j < lv.res.size(); j++) {
@@ -541,12 +563,24 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
       Scratch gbuf;
       GnFuseOut og;
       const bool tf = !lv.tf.empty();
+      // without a transformer the output is the next ResNet's input (the
+      // level's next one, or after the last level's last the mid block's)
+      const ResIdx* rn = tf ? nullptr
+                         : j + 1 < lv.res.size()              ? &lv.res[j + 1]
+                         : i == 3 && lv.sample_w < 0         ? &u.mid_res[0]
+                                                               : nullptr;
       rc = act_alloc(nxt, hh, ww, r.cout);
       if (!rc && tf) rc = tf_gn(lv.tf[j], hh, ww, r.cout, gbuf, og);
+      if (!rc && rn && nxt.st.f()) rc = res_gn(*rn, hh, ww, nxt, gbuf, og);  // (gated in the block)
       if (!rc)
         rc = resnet(r, one(hcur.buf.h(), ch), hcur.has_st ? &xs : nullptr, hh, ww, nxt,
-                    tf ? &og : nullptr);
+                    tf || (rn && nxt.st.f()) ? &og : nullptr, gin_ok ? gin.h() : nullptr);
       if (rc) return rc;
+      gin_ok = false;
+      if (rn && og.done) {
+        gin = std::move(gbuf);
+        gin_ok = true;
+      }
       if (tf) {
         Act t2;
         rc = act_alloc(t2, hh, ww, r.cout);
@@ -575,9 +609,23 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
       cc.bias = u.f(lv.sample_b);
       cc.y = ds.buf.h();
       cc.stats = st_out(ds);
+      // the next level's first ResNet's GN1 from the downsampler's reducer
+      Scratch gbuf;
+      GnFuseOut og;
+      const ResIdx* rn = i + 1 < 4 && !u.down[i + 1].res.empty() ? &u.down[i + 1].res[0] : nullptr;
+      if (rn && ds.st.f() && !gn_reduce_fuse_off()) {
+        rc = res_gn(*rn, h2, w2, ds, gbuf, og);
+        if (rc) return rc;
+        cc.gn = &og;
+      }
       rc = conv_nhwc(c, cc);
       if (rc) return rc;
       st_done(ds);
+      gin_ok = false;
+      if (rn && og.done) {
+        gin = std::move(gbuf);
+        gin_ok = true;
+      }
       skips.push_back(std::move(hcur));
       hcur = std::move(ds);
       hh = h2;
@@ -595,7 +643,9 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   if (!rc) rc = tf_gn(u.mid_tf, hh, ww, ch, mgbuf, mog);
   if (!rc)
     rc = resnet(u.mid_res[0], one(mid_in.buf.h(), ch), mid_in.has_st ? &ms : nullptr, hh, ww, m1,
-                &mog);
+                &mog, gin_ok ? gin.h() : nullptr);
+  gin_ok = false;
+  gin.release();
   if (!rc) rc = act_alloc(m2, hh, ww, ch);
   if (!rc) rc = transformer(u.mid_tf, m1, hh, ww, m2, mog.done ? mgbuf.h() : nullptr);
   const GnStats m2s = st_of(m2);

@@ -93,7 +93,7 @@ def test_resnet_block(dev, rng, B, cin, cout, H, W, temb):
 @pytest.mark.parametrize("B,cin,cout,H,W", [
     (1, 1280, 1280, 8, 8),    # conv1 split 12: one row-step of 64 pixels per thread
     (2, 1280, 1280, 16, 16),  # split 5, four row-steps, two images
-    (1, 320, 640, 32, 32),    # 20 channels per group, sixteen row-steps
+    (1, 640, 640, 32, 32),    # 20 channels per group: 128-row steps, eight of them, split 2
     (1, 2560, 1280, 8, 8),    # up-block input width (K = 23040)
 ])
 def test_resnet_gn_reducer_matches_apply(dev, rng, monkeypatch, B, cin, cout, H, W):

@@ -190,7 +190,10 @@ def test_sd21_gn_in_reducers_matches_separate(sd21, rng, monkeypatch):
     err = rel_l2(fused, sep)
     print(f"[sd21 gn reducers] rel-L2 {err:.2e} max-abs {np.max(np.abs(fused - sep)):.2e}",
           flush=True)
-    assert np.isfinite(fused).all() and err <= 2e-3
+    # measured 1.4e-3: rounding differences carried through ~50 fp16 layers,
+    # the same size as the whole step's distance to fp32 (1.7e-3); a wrong
+    # group, channel or statistic would be O(1)
+    assert np.isfinite(fused).all() and err <= 5e-3
 
 
 def test_sd21_shortcut_partials_match_separate(sd21, rng, monkeypatch):
@@ -206,7 +209,8 @@ def test_sd21_shortcut_partials_match_separate(sd21, rng, monkeypatch):
     err = rel_l2(fused, sep)
     print(f"[sd21 shortcut partials] rel-L2 {err:.2e} max-abs {np.max(np.abs(fused - sep)):.2e}",
           flush=True)
-    assert np.isfinite(fused).all() and err <= 2e-3
+    # measured 1.4e-3 (see the GroupNorm comparison above)
+    assert np.isfinite(fused).all() and err <= 5e-3
 
 
 def test_sd21_graph_replay_matches_eager(dev, sd21, rng):
