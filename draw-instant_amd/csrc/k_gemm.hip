@@ -391,11 +391,12 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
   }
 }
 
-// (row steps, split count) pairs the fused reducer is built for
+// (row steps, split count) pairs the fused reducer is built for (16 row
+// steps would spill its accumulators to scratch)
 #define DI_RGN_CASES(X)                                                                   \
   X(1, 2) X(1, 3) X(1, 4) X(1, 5) X(1, 6) X(1, 8) X(1, 12) X(2, 2) X(2, 3) X(2, 4) X(2, 5) \
   X(2, 6) X(2, 8) X(2, 12) X(4, 2) X(4, 3) X(4, 4) X(4, 5) X(4, 6) X(4, 8) X(4, 12)       \
-  X(8, 2) X(8, 3) X(8, 4) X(8, 5) X(8, 6) X(16, 2) X(16, 3) X(16, 4)
+  X(8, 2) X(8, 3) X(8, 4) X(8, 5) X(8, 6)
 
 bool splitk_gn_built(uint32_t im, uint32_t splits) {
 #define DI_RGN_HAS(IMV, SV) if (im == IMV && splits == SV) return true;

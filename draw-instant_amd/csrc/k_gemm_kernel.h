@@ -277,15 +277,21 @@ __device__ __forceinline__ void epi_load(const GemmArgs& g, uint32_t m0, uint32_
   }
 }
 
-// Offset of partial (m, n) within one split's [M][N] block: row-major, or in
-// column groups of g.part_cpg (GemmArgs::part_cpg).  The group index comes
-// from a float reciprocal: exact for n < 2^21 (the product stays 0.5 /
-// part_cpg away from an integer, far beyond its rounding error).
-__device__ __forceinline__ uint64_t part_offset(const GemmArgs& g, uint32_t m, uint32_t n) {
-  if (!g.part_cpg) return (uint64_t)m * g.N + n;
+// Column n's place in one split's [M][N] block of partials: partial (m, n)
+// sits at m * stride + offset, row-major (stride N, offset n) or in column
+// groups of g.part_cpg (GemmArgs::part_cpg).  Callers take it once per
+// column, outside their row loops.  The group index comes from a float
+// reciprocal: exact for n < 2^21 (the product stays 0.5 / part_cpg away
+// from an integer, far beyond its rounding error).
+struct PartCol {
+  uint32_t stride;
+  uint64_t offset;
+};
+__device__ __forceinline__ PartCol part_col(const GemmArgs& g, uint32_t n) {
+  if (!g.part_cpg) return PartCol{g.N, n};
   const uint32_t gi =
       (uint32_t)(((float)n + 0.5f) * __builtin_amdgcn_rcpf((float)g.part_cpg));
-  return ((uint64_t)gi * g.M + m) * g.part_cpg + (n - gi * g.part_cpg);
+  return PartCol{g.part_cpg, (uint64_t)gi * g.M * g.part_cpg + (n - gi * g.part_cpg)};
 }
 
 // GEGLU vector v of a thread: 8 outputs of tile row r from hidden columns
@@ -364,13 +370,28 @@ __device__ __forceinline__ void gemm_epilogue_vec(const GemmArgs& g, const float
     constexpr int VPR4 = BN / 4;
     constexpr int NV = (BM * VPR4 + NT - 1) / NT;
     float* P = g.part + ((uint64_t)(split + g.part_slot0) * g.batch + bz) * (uint64_t)g.M * g.N;
+    if constexpr (NT % VPR4 == 0) {
+      // a thread keeps one 4-column slot for all its vectors
+      const int c4 = (tid % VPR4) * 4, r0 = tid / VPR4;
+      const uint32_t n = n0 + c4;
+      const PartCol pc = part_col(g, n);
 #pragma unroll
-    for (int v = 0; v < NV; v++) {
-      const int idx = tid + v * NT;
-      if (idx < BM * VPR4) {
-        const int r = idx / VPR4, c4 = (idx % VPR4) * 4;
-        const uint32_t m = m0 + r, n = n0 + c4;
-        if (m < g.M && n < g.N) *(f32x4*)&P[part_offset(g, m, n)] = tile4(r * LDC + c4);
+      for (int v = 0; v < NV; v++) {
+        const int r = r0 + v * (NT / VPR4);
+        const uint32_t m = m0 + r;
+        if (r < BM && m < g.M && n < g.N)
+          *(f32x4*)&P[(uint64_t)m * pc.stride + pc.offset] = tile4(r * LDC + c4);
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const int idx = tid + v * NT;
+        if (idx < BM * VPR4) {
+          const int r = idx / VPR4, c4 = (idx % VPR4) * 4;
+          const uint32_t m = m0 + r, n = n0 + c4;
+          const PartCol pc = part_col(g, n);
+          if (m < g.M && n < g.N) *(f32x4*)&P[(uint64_t)m * pc.stride + pc.offset] = tile4(r * LDC + c4);
+        }
       }
     }
     return;
@@ -1128,10 +1149,11 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm(GemmArgs g) {
 #pragma unroll
       for (int b = 0; b < TN; b++) {
         uint32_t n = n0 + wn0 + b * 16 + fr;
+        const PartCol pc = part_col(g, n);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           uint32_t m = m0 + wm0 + a * 16 + rq + i;
-          if (m < g.M && n < g.N) P[part_offset(g, m, n)] = acc[a][b][i];
+          if (m < g.M && n < g.N) P[(uint64_t)m * pc.stride + pc.offset] = acc[a][b][i];
         }
       }
     return;
