@@ -165,8 +165,7 @@ struct GnFuse {
 // batch 1, split-K with a built (rows per thread, split count) pair, a
 // bias, optionally a per-image temb bias and an fp16 residual, no
 // activation, 4 | channels per group <= 40, hw a multiple of 64 (64 to 1024
-// pixels; at most 256 with raw; statistics only with raw and 40 channels per
-// group).
+// pixels; at most 256 with raw; statistics only with raw).
 bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f);
 // elem: DI_F16 or DI_F32 operand element type.  gn: see GnFuse (only with
 // g.splits > 1 and splitk_gn_ok).

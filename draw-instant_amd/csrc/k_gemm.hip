@@ -331,13 +331,16 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
   }
   if (f.stats) {
     // per 64-row chunk and channel (sum, sum of squares) of the stored
-    // values, the GemmArgs::stats layout (only with RS = 64: chunk i of the
-    // image is row step i).  Chunk by chunk through LDS: 8 adjacent lanes
-    // per (channel, statistic) each take every eighth row, added by lane
-    // swaps in a fixed order.
+    // values, the GemmArgs::stats layout: row step i holds the image's
+    // chunks i * RS / 64 .. + RS / 64 - 1.  Step by step through LDS
+    // ([RS][cpg] floats, RS * cpg = 16 * blockDim <= 64 * 40): 8 adjacent
+    // lanes per (chunk, statistic, channel) each take every eighth row of
+    // the chunk, added by lane swaps in a fixed order (RS cpg / 32 tasks
+    // x 8 lanes = every thread).
     const uint32_t cpg = Q * 4, task = tid >> 3, part = tid & 7;
-    const uint32_t st = (uint32_t)(((float)task + 0.5f) * __builtin_amdgcn_rcpf((float)cpg));
-    const uint32_t ch = task - st * cpg;
+    const uint32_t cs = (uint32_t)(((float)task + 0.5f) * __builtin_amdgcn_rcpf((float)cpg));
+    const uint32_t ch = task - cs * cpg, lc = cs >> 1, st = cs & 1;
+    const uint64_t chunk0 = (uint64_t)n * (RS * IM / 64) + lc;
 #pragma unroll
     for (int i = 0; i < IM; i++) {
       *(f32x4*)&sst[r0 * cpg + q * 4] =
@@ -346,14 +349,14 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
       float a = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; k++) {
-        const float x = sst[(part + 8 * k) * cpg + ch];
+        const float x = sst[(lc * 64 + part + 8 * k) * cpg + ch];
         a += st ? __fmul_rn(x, x) : x;
       }
       a += __shfl_xor(a, 1);
       a += __shfl_xor(a, 2);
       a += __shfl_xor(a, 4);
       if (part == 0)
-        f.stats[(((uint64_t)n * IM + i) * g.N + grp * cpg + ch) * 2 + st] = a;
+        f.stats[((chunk0 + (uint64_t)i * (RS / 64)) * g.N + grp * cpg + ch) * 2 + st] = a;
       __syncthreads();
     }
   }
@@ -656,10 +659,8 @@ bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f) {
   // pays at 16 x 16 and below: at 32 x 32 the fused conv2 reducer took
   // 11.2 us against 5.0 + 5.0 us for the reducer and apply it replaces
   if (f.raw && f.hw > 256) return false;
-  // statistics of the stored values: 64-row steps, 16 cpg threads
-  if (f.stats && (!f.raw || splitk_gn_rs(g.N / f.groups / 4, f.hw) != 64 ||
-                  ((uintptr_t)f.stats & 7) != 0))
-    return false;
+  // statistics of the stored values only with the raw output
+  if (f.stats && (!f.raw || ((uintptr_t)f.stats & 7) != 0)) return false;
   const uint32_t cpg = g.N / f.groups, slots = g.part_slots ? g.part_slots : g.splits;
   return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && f.hw % 64 == 0 &&
          splitk_gn_built(f.hw / splitk_gn_rs(cpg / 4, f.hw), slots) && g.M % f.hw == 0 &&
