@@ -71,8 +71,12 @@ int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rs
   return DI_OK;
 }
 
+// side / side_done: a GEMV for the apply launch to run as well (see
+// launch_group_norm_nhwc_st); side_done reports whether it did.
 int gn_nhwc(Ctx* c, NhwcSrc x, const float* g, const float* b, f16* y, uint32_t N, uint32_t C,
-            uint32_t G, uint32_t HW, float eps, bool silu, const GnStats* st = nullptr) {
+            uint32_t G, uint32_t HW, float eps, bool silu, const GnStats* st = nullptr,
+            const GemvArgs* side = nullptr, bool* side_done = nullptr) {
+  if (side_done) *side_done = false;
   if (st) {
     float* fold = nullptr;
     if (const uint64_t nf = gn_fold_ws_floats(N, C, HW)) {
@@ -81,8 +85,11 @@ int gn_nhwc(Ctx* c, NhwcSrc x, const float* g, const float* b, f16* y, uint32_t 
       if (rc) return rc;
       fold = (float*)ws;
     }
-    if (launch_group_norm_nhwc_st(c->stream, x, *st, g, b, y, N, C, G, HW, eps, silu, fold))
+    if (launch_group_norm_nhwc_st(c->stream, x, *st, g, b, y, N, C, G, HW, eps, silu, fold,
+                                  side)) {
+      if (side_done) *side_done = side && gn_side_gemv_ok(*side);
       return DI_OK;
+    }
   }
   void* ws = nullptr;
   int rc = workspace(c, gn_nhwc_ws_floats(N, C, G, HW) * sizeof(float), &ws);
@@ -197,7 +204,7 @@ int linear_f16(Ctx* c, const f16* x, uint64_t ldx, uint32_t M, uint32_t K, const
 
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, const float* temb,
                    uint32_t ld_temb, f16* out, const GnStats* x_st, StatsOut* out_st,
-                   GnFuseOut* out_gn, const f16* x_gn) {
+                   GnFuseOut* out_gn, const f16* x_gn, const GemvArgs* gn1_side) {
   const uint32_t HW = s.H * s.W;
   const uint64_t rows = (uint64_t)s.B * HW;
   // conv1 hands GN2 the statistics of its output (no partial pass)
@@ -208,11 +215,14 @@ int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x, co
   if (!rc) rc = t3.alloc(c, rows * s.Cout * 2);
   if (!rc && st2) rc = t2st.alloc(c, gn_stats_floats(rows, s.Cout) * sizeof(float));
   if (rc) return rc;
+  bool side_done = false;
   if (!x_gn) {
-    rc = gn_nhwc(c, x, w.n1_g, w.n1_b, t1.h(), s.B, s.Cin, s.groups, HW, s.eps, true, x_st);
+    rc = gn_nhwc(c, x, w.n1_g, w.n1_b, t1.h(), s.B, s.Cin, s.groups, HW, s.eps, true, x_st,
+                 gn1_side, &side_done);
     if (rc) return rc;
     x_gn = t1.h();
   }
+  if (gn1_side && !side_done) launch_gemv(*gn1_side, DI_F16, c->stream);  // before conv1 reads it
   ConvCall c1;
   c1.x = single(x_gn, s.Cin);
   c1.B = s.B;

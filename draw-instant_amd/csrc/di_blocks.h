@@ -112,11 +112,13 @@ struct ResnetShape {
 // next block's GroupNorm to out as well (GnFuse with raw = 1) and reports
 // whether it did; out's statistics are then written only where
 // out_gn->f.stats is out_st's buffer.  x_gn: GN1(x) + SiLU already computed
-// by x's producer (then x_st is not used).
+// by x's producer (then x_st is not used).  gn1_side: an fp16-weight GEMV
+// (producing temb) that GN1's apply launch runs as well where it can, and
+// that is otherwise launched on its own before conv1.
 int resnet_forward(Ctx* c, const ResnetW& w, const ResnetShape& s, NhwcSrc x,
                    const float* temb, uint32_t ld_temb, f16* out, const GnStats* x_st = nullptr,
                    StatsOut* out_st = nullptr, GnFuseOut* out_gn = nullptr,
-                   const f16* x_gn = nullptr);
+                   const f16* x_gn = nullptr, const GemvArgs* gn1_side = nullptr);
 
 struct TransformerW {
   const float *n_g = nullptr, *n_b = nullptr;       // GroupNorm

@@ -6,6 +6,8 @@
 
 #include <cstdint>
 
+#include "di_tembed.h"
+
 namespace di {
 
 enum AMode { A_DENSE = 0, A_CONV_NHWC = 1, A_CONV_NCHW = 2 };
@@ -136,10 +138,15 @@ void launch_conv3_halo(const GemmArgs& g, hipStream_t s);
 bool conv_in_direct_ok(uint32_t Cin, uint32_t Cout, uint32_t H, uint32_t W);
 // cx / cy / cn: optionally also convert cn fp32 values cx -> fp16 cy in the
 // same launch (taken when conv_in_convert_ok; the caller converts otherwise).
+// gv: optionally also run that GEMV (the timestep sinusoid's first linear,
+// taken when conv_in_gemv_ok; blocks past conv_in's own rows compute it,
+// and the caller launches it otherwise).
 bool conv_in_convert_ok(const float* cx, const void* cy, uint64_t cn);
+bool conv_in_gemv_ok(const GemvArgs& g);
 void launch_conv_in(hipStream_t s, const float* x, const _Float16* w, const float* bias,
                     _Float16* y, float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W,
-                    const float* cx = nullptr, _Float16* cy = nullptr, uint64_t cn = 0);
+                    const float* cx = nullptr, _Float16* cy = nullptr, uint64_t cn = 0,
+                    const GemvArgs* gv = nullptr);
 // GroupNorm (+SiLU) of a split-K conv's output applied by its reducer: the
 // output rows are hw-pixel images of N channels in `groups` groups;
 // y[rows][ldy] = GN(out) (+SiLU) in fp16, and the output itself only when

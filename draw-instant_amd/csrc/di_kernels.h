@@ -9,6 +9,7 @@
 
 #include "di_device.h"
 #include "di_internal.h"
+#include "di_tembed.h"
 
 namespace di {
 
@@ -71,9 +72,14 @@ struct GnStats {
 // GroupNorm apply from producer statistics (one kernel, no partial pass);
 // returns false when the shape is not supported (the caller then runs
 // launch_group_norm_nhwc).
+// side: a GEMV run by extra workgroups of the same launch (B <= 2, fp16
+// weights, K <= 1536, no sinusoid: gn_side_gemv_ok); if it does not qualify
+// the caller launches it.
+bool gn_side_gemv_ok(const GemvArgs& g);
 bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st, const float* gamma,
                                const float* beta, void* y, uint32_t N, uint32_t C, uint32_t G,
-                               uint32_t HW, float eps, bool silu, float* fold_ws = nullptr);
+                               uint32_t HW, float eps, bool silu, float* fold_ws = nullptr,
+                               const GemvArgs* side = nullptr);
 // Floats of fold_ws for an [N][HW][C] input (0: no pre-fold at this size).
 // With fold_ws, statistics of large images are first summed to ~128 chunks
 // per image, so the apply workgroups do not each re-read all HW / 64.

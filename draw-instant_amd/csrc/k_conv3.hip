@@ -39,6 +39,7 @@
 // epilogue writes fp32 partials for the GEMM's split-K reducer.
 #include <type_traits>
 
+#include "di_gemv_dev.h"
 #include "di_kernels.h"
 #include "k_conv3_sched.h"
 #include "k_gemm_kernel.h"
@@ -296,8 +297,10 @@ constexpr int CI_CS = 32, CI_LDY = CI_CS + 8;
 
 // With cn > 0 the grid has one more row of workgroups (blockIdx.y = Cout /
 // CI_CS) that converts cn fp32 values cx -> fp16 cy (the U-Net's context;
-// cn % 8 == 0, 16-byte aligned), so that conversion costs no launch of its
-// own.
+// cn % 8 == 0, 16-byte aligned), and with gv.N > 0 rows from gv_row0 on run
+// the timestep sinusoid's first GEMV gv (fp16 weights, B K <= kCiGemvX), so
+// neither costs a launch of its own.
+constexpr uint32_t kCiGemvX = 2560;
 template <int CIN>
 __global__ __launch_bounds__(256) void k_conv_in(const float* __restrict__ x,
                                                  const f16* __restrict__ w,
@@ -305,8 +308,14 @@ __global__ __launch_bounds__(256) void k_conv_in(const float* __restrict__ x,
                                                  f16* __restrict__ y, float* __restrict__ stats,
                                                  uint32_t Cout, uint32_t H, uint32_t W,
                                                  const float* __restrict__ cx,
-                                                 f16* __restrict__ cy, uint32_t cn) {
+                                                 f16* __restrict__ cy, uint32_t cn, GemvArgs gv,
+                                                 uint32_t gv_row0) {
   static_assert(CIN <= 8, "weights padded to 8 channels per tap");
+  if (gv.N && blockIdx.y >= gv_row0) {
+    __shared__ float gxs[kCiGemvX];
+    gemv_vec_block<f16, 3, 1, 8, true>(gv, gxs, (blockIdx.y - gv_row0) * gridDim.x + blockIdx.x);
+    return;
+  }
   if (cn && blockIdx.y == Cout / CI_CS) {
     for (uint32_t i = (blockIdx.x * 256 + threadIdx.x) * 8; i < cn; i += gridDim.x * 256 * 8) {
       const f32x4 a = *(const f32x4*)(cx + i), b = *(const f32x4*)(cx + i + 4);
@@ -429,12 +438,23 @@ bool conv_in_convert_ok(const float* cx, const void* cy, uint64_t cn) {
          ((uintptr_t)cy & 15) == 0;
 }
 
+bool conv_in_gemv_ok(const GemvArgs& g) {
+  return g.vec_ok && g.x_mode == GEMV_X_SINUSOID && g.N > 0 && g.K % 8 == 0 && g.K <= 64 * 8 * 3 &&
+         g.B >= 1 && g.B <= 8 && (uint64_t)g.B * g.K <= kCiGemvX;
+}
+
 void launch_conv_in(hipStream_t s, const float* x, const f16* w, const float* bias, f16* y,
                     float* stats, uint32_t B, uint32_t Cout, uint32_t H, uint32_t W,
-                    const float* cx, f16* cy, uint64_t cn) {
+                    const float* cx, f16* cy, uint64_t cn, const GemvArgs* gv) {
   const bool conv = conv_in_convert_ok(cx, cy, cn);
-  k_conv_in<4><<<dim3(B * H * W / 64, Cout / CI_CS + (conv ? 1 : 0)), 256, 0, s>>>(
-      x, w, bias, y, stats, Cout, H, W, cx, cy, conv ? (uint32_t)cn : 0u);
+  const uint32_t gx = B * H * W / 64, rows = Cout / CI_CS + (conv ? 1 : 0);
+  GemvArgs none;
+  none.N = 0;
+  const bool side = gv && conv_in_gemv_ok(*gv);
+  const uint32_t grows = side ? (gemv_side_blocks(gv->N, 1) + gx - 1) / gx : 0;
+  k_conv_in<4><<<dim3(gx, rows + grows), 256, 0, s>>>(x, w, bias, y, stats, Cout, H, W, cx, cy,
+                                                      conv ? (uint32_t)cn : 0u, side ? *gv : none,
+                                                      rows);
 }
 
 void launch_conv3_halo(const GemmArgs& g, hipStream_t s) {

@@ -25,6 +25,7 @@
 #include <mutex>
 
 #include "di_device.h"
+#include "di_gemv_dev.h"
 #include "di_kernels.h"
 
 namespace di {
@@ -448,6 +449,7 @@ constexpr int kGnSliceMax = 128;
 // pixels) are pre-folded to about kGnFoldTarget chunks
 constexpr uint32_t kGnFoldMin = 256, kGnFoldTarget = 128;
 constexpr uint32_t kGnApplyWgs = 256;
+constexpr uint32_t kGnSideX = 2560;  // B * K floats of a side-job GEMV's input
 
 // Pre-fold of producer statistics for large images: every apply workgroup
 // otherwise re-reads all HW / 64 chunks of its channel slice (2 MB per
@@ -485,11 +487,22 @@ __global__ __launch_bounds__(256) void k_gn_stats_fold(GnStats st, float* __rest
 // (the host picks the smallest of 1 / 2 / 4 / 8 that covers the image's
 // chunks, since every load issued costs the CU's load path whether or not
 // it is used); chunks beyond NU lanes' worth are taken by a loop.
-template <int NU>
+// SIDE: z-planes past the batch's run the GEMV gv (B <= 2 rows of K <=
+// 1280, eight weight rows per wavefront: every ResNet's time_emb_proj of a
+// U-Net step) as a side job, which saves that GEMV a launch of its own.
+template <int NU, bool SIDE>
 __global__ __launch_bounds__(256) void k_gn_nhwc_apply_st(
     NhwcSrc x, GnStats st, const float* __restrict__ gamma, const float* __restrict__ beta,
     f16* __restrict__ y, uint32_t C, uint32_t cpg, uint32_t SW, uint32_t HW, uint32_t ppb,
-    float eps, int silu, uint32_t cpi) {
+    float eps, int silu, uint32_t cpi, uint32_t N, GemvArgs gv) {
+  if constexpr (SIDE) {
+    if (blockIdx.z >= N) {
+      __shared__ float gxs[kGnSideX];
+      gemv_vec_block<f16, 3, 8, 2, false>(
+          gv, gxs, ((blockIdx.z - N) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x);
+      return;
+    }
+  }
   __shared__ float chs[2][kGnSliceMax];
   __shared__ float gms[2][kGnSliceMax];
   __shared__ __attribute__((aligned(16))) float sgb[2][kGnSliceMax];  // gamma, beta of the slice
@@ -1098,9 +1111,15 @@ uint64_t gn_fold_ws_floats(uint32_t N, uint32_t C, uint32_t HW) {
   return (uint64_t)N * ((cpi + F - 1) / F) * C * 2;
 }
 
+bool gn_side_gemv_ok(const GemvArgs& g) {
+  return g.vec_ok && g.x_mode != GEMV_X_SINUSOID && g.N > 0 && g.K % 8 == 0 &&
+         g.K <= 64 * 8 * 3 && g.B >= 1 && g.B <= 2 && (uint64_t)g.B * g.K <= kGnSideX;
+}
+
 bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st_in, const float* gamma,
                                const float* beta, void* y, uint32_t N, uint32_t C, uint32_t G,
-                               uint32_t HW, float eps, bool silu, float* fold_ws) {
+                               uint32_t HW, float eps, bool silu, float* fold_ws,
+                               const GemvArgs* side) {
   uint32_t sw = 0;
   if (!gn_stats_slice(C, G, HW, &sw) || x.c1 % 8 != 0 || (st_in.c1 < C && st_in.c1 % 8 != 0))
     return false;
@@ -1132,19 +1151,32 @@ bool launch_group_norm_nhwc_st(hipStream_t s, NhwcSrc x, const GnStats& st_in, c
   pbs = (HW + ppb - 1) / ppb;
   // statistics chunks per lane: KL lanes per channel quad
   const uint32_t kl_lanes = 256 / (sw / 4), need = (cpi + kl_lanes - 1) / kl_lanes;
-  const dim3 grid(pbs, slices, N);
-  if (need <= 1)
-    k_gn_nhwc_apply_st<1><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
-                                                eps, silu ? 1 : 0, cpi);
-  else if (need <= 2)
-    k_gn_nhwc_apply_st<2><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
-                                                eps, silu ? 1 : 0, cpi);
-  else if (need <= 4)
-    k_gn_nhwc_apply_st<4><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
-                                                eps, silu ? 1 : 0, cpi);
-  else
-    k_gn_nhwc_apply_st<8><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, HW, ppb,
-                                                eps, silu ? 1 : 0, cpi);
+  // a side-job GEMV takes whole extra z-planes of pbs x slices blocks
+  const bool sj = side && gn_side_gemv_ok(*side);
+  const uint32_t plane = pbs * slices;
+  const uint32_t zs = sj ? (gemv_side_blocks(side->N, 8) + plane - 1) / plane : 0;
+  const dim3 grid(pbs, slices, N + zs);
+  GemvArgs none;
+  none.N = 0;
+  const GemvArgs& gv = sj ? *side : none;
+#define DI_GN_ST(NUV)                                                                            \
+  if (sj)                                                                                        \
+    k_gn_nhwc_apply_st<NUV, true><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G, sw, \
+                                                       HW, ppb, eps, silu ? 1 : 0, cpi, N, gv);  \
+  else                                                                                           \
+    k_gn_nhwc_apply_st<NUV, false><<<grid, 256, 0, s>>>(x, st, gamma, beta, (f16*)y, C, C / G,    \
+                                                        sw, HW, ppb, eps, silu ? 1 : 0, cpi, N,  \
+                                                        gv);
+  if (need <= 1) {
+    DI_GN_ST(1)
+  } else if (need <= 2) {
+    DI_GN_ST(2)
+  } else if (need <= 4) {
+    DI_GN_ST(4)
+  } else {
+    DI_GN_ST(8)
+  }
+#undef DI_GN_ST
   return true;
 }
 

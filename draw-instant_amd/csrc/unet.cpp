@@ -406,7 +406,9 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   g1.B = B;
   g1.N = cf.time_dim;
   g1.K = cf.block_channels[0];
-  launch_gemv(g1, DI_F16, c->stream);
+  // the first GEMV rides in conv_in's launch where the direct conv_in runs;
+  // the other two follow conv_in then
+  const bool g1_side = ctx_in_conv_in && conv_in_gemv_ok(g1);
   GemvArgs g2;
   g2.x = th.f();
   g2.ldx = cf.time_dim;
@@ -418,7 +420,6 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   g2.B = B;
   g2.N = cf.time_dim;
   g2.K = cf.time_dim;
-  launch_gemv(g2, DI_F16, c->stream);
   GemvArgs g3;
   g3.x_mode = GEMV_X_SILU;
   g3.x = temb.f();
@@ -431,7 +432,11 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   g3.B = B;
   g3.N = u.temb_rows;
   g3.K = cf.time_dim;
-  launch_gemv(g3, DI_F16, c->stream);
+  if (!g1_side) {
+    launch_gemv(g1, DI_F16, c->stream);
+    launch_gemv(g2, DI_F16, c->stream);
+    launch_gemv(g3, DI_F16, c->stream);
+  }
 
   // An activation and, when its level allows (HW % 64 == 0), the GroupNorm
   // statistics its producer wrote (every GN input here is the output of a
@@ -455,11 +460,16 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   auto st_out = [](Act& a) { return a.so.p ? &a.so : (StatsOut*)nullptr; };
   auto st_done = [](Act& a) { a.has_st = a.so.done; };
   auto st_of = [](const Act& a) { return GnStats{a.st.f(), a.st.f(), a.c, a.c, a.c}; };
+  // the time_emb_proj GEMV (g3) still to run before the first conv1 reads
+  // tproj: the first ResNet's GN1 launch takes it (or launches it)
+  const GemvArgs* g3_pending = nullptr;
   auto resnet = [&](const ResIdx& r, NhwcSrc x, const GnStats* xs, uint32_t hh, uint32_t ww,
                     Act& y, GnFuseOut* og = nullptr, const f16* xg = nullptr) {
     ResnetShape s{B, hh, ww, r.cin, r.cout, G, cf.resnet_eps};
+    const GemvArgs* side = g3_pending;
+    g3_pending = nullptr;
     const int r2 = resnet_forward(c, res_w(u, r), s, x, tproj.f() + r.temb_row, u.temb_rows,
-                                  y.buf.h(), xs, st_out(y), og, xg);
+                                  y.buf.h(), xs, st_out(y), og, xg, side);
     st_done(y);
     return r2;
   };
@@ -525,7 +535,8 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
   if (ci_direct) {
     if (ctx_in_conv_in)
       launch_conv_in(c->stream, sample, u.h(u.conv_in_w), u.f(u.conv_in_b), hcur.buf.h(),
-                     hcur.st.f(), B, ch, hh, ww, context, ctx16.h(), ctx_n);
+                     hcur.st.f(), B, ch, hh, ww, context, ctx16.h(), ctx_n,
+                     g1_side ? &g1 : nullptr);
     else
       launch_conv_in(c->stream, sample, u.h(u.conv_in_w), u.f(u.conv_in_b), hcur.buf.h(),
                      hcur.st.f(), B, ch, hh, ww);
@@ -533,6 +544,10 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
     st_done(hcur);
     if (ctx_in_conv_in) rc = kv_gemm();
     if (rc) return rc;
+    if (g1_side) {
+      launch_gemv(g2, DI_F16, c->stream);
+      g3_pending = &g3;
+    }
   } else {
     ConvCall cc;
     cc.x = one(x16.h(), cin_p);
@@ -632,6 +647,8 @@ int unet_step(Ctx* c, UNet& u, const float* sample, const float* tsteps, const f
       ww = w2;
     }
   }
+  if (g3_pending) launch_gemv(*g3_pending, DI_F16, c->stream);  // (no down-path ResNet)
+  g3_pending = nullptr;
   skips.push_back(std::move(hcur));
   // mid block on the last skip (which the first up resnet consumes again)
   Act m1, m2, m3;
