@@ -57,7 +57,13 @@ struct Ctx {
   // of the free list; the capturing owner takes them over.
   bool hold_releases = false;
   std::vector<std::pair<void*, uint64_t>> held;
+  // GroupNorm statistics exchange area (k_norm.hip), zeroed at creation and
+  // kept for the context's life: its counters must only ever grow
+  void* gn_xchg = nullptr;
 };
+
+// bytes of a context's GroupNorm exchange area (k_norm.hip)
+uint64_t gn_xchg_bytes();
 
 // ---- error reporting (thread-local message, status code returned) ----
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));

@@ -7,14 +7,17 @@
 // beta[c], optionally followed by SiLU y/(1+e^-y).  Partial sums are fp32.
 //
 // Work decomposition is MI355X-first instead of the reference's one
-// workgroup per group (32 workgroups for 256 CUs, serial reductions): every
-// group norm is two kernels with no inter-workgroup communication,
+// workgroup per group (32 workgroups for 256 CUs, serial reductions): a
+// group norm is either two kernels with no inter-workgroup communication,
 //  1. partial sums: ~1024 workgroups each reduce a slice of the input to
 //     (sum, sumsq) per group and write them to a workspace, no atomics;
 //  2. fold + apply: every workgroup folds the partials it needs in one fixed
-//     order (so all workgroups agree bit-for-bit), then normalises its slice.
-// Deterministic and safe under graph replay.  X is read twice; the second
-// read is usually served by the 256 MB Infinity Cache.
+//     order (so all workgroups agree bit-for-bit), then normalises its slice
+// (X read twice; the second read is usually served by the 256 MB Infinity
+// Cache), or, for NCHW tensors of up to 64 groups, one kernel whose slices
+// exchange their partial sums through epoch-tagged words (k_gn_nchw_xchg),
+// or one kernel whose workgroups each re-read their whole group
+// (k_gn_nchw_fused).  All are deterministic and safe under graph replay.
 //
 // Latency, not bandwidth, bounds these kernels at U-Net sizes (2.5-10 MB per
 // call), so each issues all of a round's loads (x, partials, gamma/beta)
@@ -292,6 +295,173 @@ __global__ __launch_bounds__(kFusedT) void k_gn_nchw_fused(
         }
         store_vec<T, VEC>(y + gbase + e, o);
       }
+    }
+  }
+}
+
+// Single-launch NCHW GroupNorm whose workgroups read only their own slice and
+// exchange the slice statistics.  kXS workgroups per group, each holding its
+// slice (<= kXU rounds of kXT vectors) in registers:
+//  1. at entry, one fetch-add on the group's arrival counter (agent scope,
+//     relaxed) returns o; every launch adds exactly kXS per group and the
+//     context's launches are stream-ordered, so o / kXS + 1 is an epoch that
+//     all workgroups of this launch share and no earlier launch used;
+//  2. the slice's (sum, sumsq) are reduced in a fixed order and published as
+//     two 64-bit words {epoch, float bits} with relaxed agent-scope atomic
+//     stores: each word is read whole or not at all, so no fence orders them;
+//  3. one wave polls the group's 2 kXS words (relaxed agent-scope atomic
+//     loads) until every word carries this epoch, at most `spin` polls;
+//  4. the kXS partials are summed in slice order by every workgroup alike,
+//     so the S slices normalise with bit-identical statistics.
+// Should a slice not arrive within `spin` polls (a workgroup not resident,
+// or spin = 0), the workgroup recomputes every slice's partials itself from
+// the input with the same thread mapping and reduction order - the same
+// bits, from one group's worth of extra reads - so the kernel always ends.
+// The exchange area (zeroed at context creation) holds per group kXS x 2
+// words and the counter; concurrent launches on one context would race,
+// which the context's single stream rules out.
+constexpr int kXT = 256;           // threads per workgroup
+constexpr uint32_t kXS = 8;        // workgroups (slices) per group; divides 2^32
+constexpr uint32_t kXWords = 32;   // 64-bit words per group record (256 B)
+constexpr uint32_t kXGroups = 64;  // groups the exchange area serves
+static_assert(2 * kXS + 1 <= kXWords && 2 * kXS <= 64, "slot words and counter in one record");
+
+template <typename T, int VEC, int U>
+__device__ __forceinline__ void xslice_load(const T* __restrict__ x, uint32_t lo, uint32_t hi,
+                                            float (&v)[U][VEC]) {
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t e = lo + (u * kXT + threadIdx.x) * VEC;
+    load_vec<T, VEC>(x + (e < hi ? e : 0u), v[u]);
+  }
+}
+
+// (sum, sumsq) of the slice [lo, hi) held in v, in a fixed order; valid in
+// thread 0.  Contains a barrier.
+template <int VEC, int U>
+__device__ __forceinline__ float2 xslice_partial(const float (&v)[U][VEC], uint32_t lo,
+                                                 uint32_t hi, float* sh) {
+  float ts = 0.0f, tq = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const bool ok = lo + (u * kXT + threadIdx.x) * VEC < hi;
+#pragma unroll
+    for (int j = 0; j < VEC; j++) {
+      const float f = ok ? v[u][j] : 0.0f;
+      ts += f;
+      tq += f * f;
+    }
+  }
+  block_sum2(ts, tq, sh);
+  return float2{ts, tq};
+}
+
+template <typename T, int VEC, int U>
+__global__ __launch_bounds__(kXT) void k_gn_nchw_xchg(
+    const T* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    T* __restrict__ y, uint64_t* __restrict__ xchg, uint32_t G, uint32_t cpg, uint32_t HW,
+    uint32_t chunk, float eps, int silu, uint32_t spin) {
+  __shared__ float sh[16];
+  __shared__ float sv[2 * kXS];
+  __shared__ uint32_t s_o;
+  __shared__ int s_ok;
+  __shared__ float s_mean, s_rstd;
+  const uint32_t tid = threadIdx.x;
+  // the kXS slices of a group on one XCD (blocks are dealt round-robin over
+  // the 8 XCDs): their polls and re-reads stay in one L2
+  const uint32_t NT = gridDim.x, bid = blockIdx.x, xcd = bid & 7u, idx = bid >> 3;
+  const uint32_t per = NT >> 3, extra = NT & 7u;
+  const uint32_t w = xcd < extra ? xcd * (per + 1) + idx : extra * (per + 1) + (xcd - extra) * per + idx;
+  const uint32_t ng = w / kXS, s = w % kXS;
+  const uint32_t L = cpg * HW;
+  uint64_t* const rec = xchg + (uint64_t)ng * kXWords;
+  uint32_t* const arrive = reinterpret_cast<uint32_t*>(rec + 2 * kXS);
+  const T* const xg = x + (uint64_t)ng * L;
+  auto bounds = [&](uint32_t j, uint32_t& lo, uint32_t& hi) {
+    lo = min(j * chunk, L);
+    hi = min(lo + chunk, L);
+  };
+  uint32_t lo, hi;
+  bounds(s, lo, hi);
+  const uint32_t c0 = (ng % G) * cpg;
+  float v[U][VEC], gm[U], bt[U];
+  xslice_load<T, VEC, U>(xg, lo, hi, v);
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t e = lo + (u * kXT + tid) * VEC;
+    const uint32_t c = c0 + (e < hi ? e : 0u) / HW;
+    gm[u] = gamma[c];
+    bt[u] = beta[c];
+  }
+  sched_fence();
+  // after the slice's loads: the atomic's round trip overlaps them (its
+  // result is waited for at once, which would hold back loads issued later)
+  if (tid == 0) s_o = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float2 p = xslice_partial<VEC, U>(v, lo, hi, sh);  // barrier: s_o visible
+  const uint64_t ep = (uint64_t)(s_o / kXS + 1u) << 32;
+  if (tid == 0) {
+    __hip_atomic_store(rec + 2 * s, ep | __float_as_uint(p.x), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rec + 2 * s + 1, ep | __float_as_uint(p.y), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (tid < kWave) {
+    const uint32_t lane = tid;
+    uint64_t word = ep;
+    bool all = false;
+    for (uint32_t it = 0; it < spin; it++) {
+      if (lane < 2 * kXS)
+        word = __hip_atomic_load(rec + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      all = __all((word & 0xffffffff00000000ull) == ep);
+      if (all) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (lane < 2 * kXS) sv[lane] = __uint_as_float((uint32_t)word);
+    if (lane == 0) s_ok = all ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_ok) {
+    // recompute every slice's partials exactly as its own workgroup does
+    for (uint32_t j = 0; j < kXS; j++) {
+      uint32_t l2, h2;
+      bounds(j, l2, h2);
+      float t[U][VEC];
+      xslice_load<T, VEC, U>(xg, l2, h2, t);
+      sched_fence();
+      const float2 q = xslice_partial<VEC, U>(t, l2, h2, sh);
+      if (tid == 0) {
+        sv[2 * j] = q.x;
+        sv[2 * j + 1] = q.y;
+      }
+      __syncthreads();  // sh is reused by the next slice
+    }
+  }
+  if (tid == 0) {
+    float a = 0.0f, b = 0.0f;
+    for (uint32_t j = 0; j < kXS; j++) {
+      a += sv[2 * j];
+      b += sv[2 * j + 1];
+    }
+    const float mean = a / (float)L;
+    const float var = fmaxf(b / (float)L - mean * mean, 0.0f);
+    s_mean = mean;
+    s_rstd = 1.0f / sqrtf(var + eps);
+  }
+  __syncthreads();
+  const float mean = s_mean, rstd = s_rstd;
+  T* const yg = y + (uint64_t)ng * L;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t e = lo + (u * kXT + tid) * VEC;
+    if (e < hi) {
+      const float a = rstd * gm[u], sb = bt[u] - mean * a;
+      float o[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; j++) {
+        const float z = v[u][j] * a + sb;
+        o[j] = silu ? silu_f(z) : z;
+      }
+      store_vec<T, VEC>(yg + e, o);
     }
   }
 }
@@ -1011,6 +1181,37 @@ bool gn_fused(hipStream_t st, const T* x, const float* gamma, const float* beta,
   return true;
 }
 
+// The exchange kernel for NG <= kXGroups groups whose slices fit kXU rounds
+// of kXT vectors; false: nothing launched.  Read at every call (tests switch
+// them between calls): DI_GN_XCHG=0 turns the kernel off, DI_GN_XCHG_SPIN
+// sets the poll limit (0 forces the recomputing path).
+constexpr uint32_t kXU = 8;
+template <typename T, int VEC>
+bool gn_xchg(Ctx* c, const T* x, const float* gamma, const float* beta, T* y, uint32_t NG,
+             uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu) {
+  const char* e_on = getenv("DI_GN_XCHG");
+  const char* e_spin = getenv("DI_GN_XCHG_SPIN");
+  const uint32_t spin = e_spin ? (uint32_t)strtoul(e_spin, nullptr, 10) : 20000u;
+  const uint32_t L = cpg * HW;
+  if ((e_on && !atoi(e_on)) || !c->gn_xchg || NG == 0 || NG > kXGroups || L < kXS * kXT) return false;
+  uint32_t chunk = (L + kXS - 1) / kXS;
+  chunk = (chunk + VEC - 1) / VEC * VEC;
+  const uint32_t rounds = (chunk + kXT * VEC - 1) / (kXT * VEC);
+  if (rounds > kXU) return false;
+  uint64_t* const xa = (uint64_t*)c->gn_xchg;
+#define DI_GN_XCHG_U(u)                                                                        \
+  k_gn_nchw_xchg<T, VEC, u><<<NG * kXS, kXT, 0, c->stream>>>(x, gamma, beta, y, xa, G, cpg, HW, \
+                                                              chunk, eps, silu ? 1 : 0, spin)
+  if (rounds <= 1) DI_GN_XCHG_U(1);
+  else if (rounds <= 2) DI_GN_XCHG_U(2);
+  else if (rounds <= 3) DI_GN_XCHG_U(3);
+  else if (rounds <= 4) DI_GN_XCHG_U(4);
+  else if (rounds <= 5) DI_GN_XCHG_U(5);
+  else DI_GN_XCHG_U(8);
+#undef DI_GN_XCHG_U
+  return true;
+}
+
 template <typename T>
 int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* y, uint32_t N,
             uint32_t G, uint32_t cpg, uint32_t HW, float eps, bool silu, float* fixed,
@@ -1020,6 +1221,9 @@ int gn_nchw(Ctx* c, const void* x, const float* gamma, const float* beta, void* 
   DI_REQUIRE((uint64_t)cpg * HW < (1ull << 31), DI_EUNSUPPORTED,
              "group norm: %llu elements per group exceed 2^31", (unsigned long long)cpg * HW);
   constexpr int V = 16 / sizeof(T);
+  if (HW % V == 0 &&
+      gn_xchg<T, V>(c, (const T*)x, gamma, beta, (T*)y, N * G, G, cpg, HW, eps, silu))
+    return DI_OK;
   if (HW % V == 0) {
     const uint32_t S = gn_fused_slices(N * G, cpg * HW, V);
     if (S && gn_fused<T, V>(c->stream, (const T*)x, gamma, beta, (T*)y, N * G, G, cpg, HW, S,
@@ -1042,6 +1246,8 @@ int gn_nchw_dt(Ctx* c, const void* x, const float* gamma, const float* beta, voi
 }
 
 }  // namespace
+
+uint64_t gn_xchg_bytes() { return (uint64_t)kXGroups * kXWords * sizeof(uint64_t); }
 
 int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const float* beta,
                            void* y, uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW,

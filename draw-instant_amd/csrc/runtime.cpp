@@ -224,6 +224,17 @@ int32_t di_create(int32_t device, di_ctx** out) {
   c->clock_khz = prop.clockRate;
   c->hbm_bytes = prop.totalGlobalMem;
   DI_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+  {
+    const uint64_t xb = gn_xchg_bytes();
+    hipError_t xe = hipMalloc(&c->gn_xchg, xb);
+    if (xe == hipSuccess) xe = hipMemset(c->gn_xchg, 0, xb);
+    if (xe != hipSuccess) {
+      (void)hipFree(c->gn_xchg);
+      (void)hipStreamDestroy(c->stream);
+      delete c;
+      DI_REQUIRE(false, DI_EHIP, "di_create: GroupNorm exchange area: %s", hipGetErrorString(xe));
+    }
+  }
   if (const char* lim = getenv("DI_ALLOC_LIMIT")) c->limit = strtoull(lim, nullptr, 10);
   *out = c;
   return DI_OK;
@@ -237,6 +248,7 @@ int32_t di_destroy(di_ctx* ctx) {
     for (void* p : kv.second) (void)hipFree(p);
   if (ctx->ws) (void)hipFree(ctx->ws);
   for (void* p : ctx->ws_retired) (void)hipFree(p);
+  if (ctx->gn_xchg) (void)hipFree(ctx->gn_xchg);
   for (int i = 0; i < kTimerSlots; i++) {
     if (ctx->ev_begin[i]) (void)hipEventDestroy(ctx->ev_begin[i]);
     if (ctx->ev_end[i]) (void)hipEventDestroy(ctx->ev_end[i]);

@@ -66,7 +66,8 @@ def test_group_norm_nchw_f32(dev, N, C, H, W, G, eps, silu):
 
 def test_gn_silu_entry_point_and_repeat(dev):
     """di_gn_silu == group_norm+SiLU; repeated launches give bit-identical
-    results (partials are folded in a fixed order, no atomics)."""
+    results (partials are summed in a fixed order whichever workgroup of a
+    group arrives last)."""
     import drawinstant
     N, C, HW, G = 1, 320, 4096, 32
     x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, HW, 111)
@@ -81,6 +82,64 @@ def test_gn_silu_entry_point_and_repeat(dev):
             first = got
         np.testing.assert_array_equal(got, first)
     assert max_rel(first.reshape(N, C, HW), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("N,C,HW,G,dt", [
+    (1, 320, 4096, 32, F32),   # cfg1: 32 groups, 5 rounds per slice
+    (2, 320, 1024, 32, F32),   # 64 groups: the exchange area's limit
+    (1, 64, 1600, 8, F32),     # slices end inside a round
+    (1, 128, 16384, 32, F32),  # 8 rounds per slice
+    (1, 320, 4096, 32, F16),   # 8-wide vectors, a partial third round
+])
+def test_group_norm_exchange_paths(dev, monkeypatch, N, C, HW, G, dt):
+    """The single-launch NCHW kernel whose slices exchange their statistics:
+    bit-identical over repeated calls (each call a new epoch of the group
+    records, with calls over fewer groups in between), bit-identical to its
+    recomputing path (DI_GN_XCHG_SPIN=0: every workgroup re-derives all slice
+    partials from the input), and within fp32 summation order of the kernel
+    without exchange (DI_GN_XCHG=0) and of the oracle."""
+    import drawinstant
+    print(f"[gn xchg] N={N} C={C} HW={HW} G={G} dt={dt}", flush=True)
+    es = 4 if dt == F32 else 2
+    npdt = np.float32 if dt == F32 else np.float16
+    x, g, b, xh, gh, bh = _gn_inputs(dev, N, C, HW, 141, dt=dt)
+    y = dev.create_buffer(N * C * HW * es)
+    # a smaller call (8 groups) that advances only the first group records
+    x2, g2, b2, _, _, _ = _gn_inputs(dev, 1, 64, 2048, 143, dt=dt)
+    y2 = dev.create_buffer(64 * 2048 * es)
+
+    def run():
+        drawinstant.call("di_group_norm", dev.ctx, x.handle, g.handle, b.handle, y.handle, N, G,
+                         C // G, HW, 1e-5, 1, dt, NCHW)
+        return dev.download(y, npdt).astype(np.float32)
+
+    def small():
+        drawinstant.call("di_group_norm", dev.ctx, x2.handle, g2.handle, b2.handle, y2.handle, 1,
+                         8, 8, 2048, 1e-5, 1, dt, NCHW)
+
+    first = run()
+    for i in range(6):
+        if i % 2:
+            small()
+        np.testing.assert_array_equal(run(), first)
+    monkeypatch.setenv("DI_GN_XCHG_SPIN", "0")
+    np.testing.assert_array_equal(run(), first)
+    small()
+    np.testing.assert_array_equal(run(), first)
+    monkeypatch.delenv("DI_GN_XCHG_SPIN")
+    np.testing.assert_array_equal(run(), first)
+    monkeypatch.setenv("DI_GN_XCHG", "0")
+    other = run()
+    monkeypatch.delenv("DI_GN_XCHG")
+    ref = oracle.group_norm(xh.reshape(N, C, HW), gh, bh, G, eps=1e-5, silu=True)
+    tol = 1e-4 if dt == F32 else 2e-3
+    print(f"   vs no-exchange {max_rel(first, other):.2e}  vs oracle "
+          f"{max_rel(first.reshape(N, C, HW), ref):.2e}", flush=True)
+    assert max_rel(first, other) <= (1e-5 if dt == F32 else 2e-3)
+    assert max_rel(first.reshape(N, C, HW), ref) <= tol
+    np.testing.assert_array_equal(run(), first)
+    for t in (x, g, b, y, x2, g2, b2, y2):
+        t.destroy()
 
 
 @pytest.mark.parametrize("N,C,H,W,G", [(1, 320, 32, 32, 32), (2, 64, 6, 6, 32)])
