@@ -1,6 +1,8 @@
 // Host side of the MFMA GEMM / implicit-GEMM conv (k_gemm_kernel.h): plan
 // selection, the split-K reducers and launch_gemm, which dispatches to the
 // instantiation families of k_gemm_*.hip.
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "k_gemm_kernel.h"
@@ -429,6 +431,11 @@ void launch_splitk_reduce_gn(const GemmArgs& g, const GnFuse& f, hipStream_t s) 
   }
   DI_RGN_CASES(DI_RGN_LAUNCH)
 #undef DI_RGN_LAUNCH
+  // splitk_gn_ok admits only built pairs: reaching here would leave the
+  // output unwritten
+  fprintf(stderr, "launch_splitk_reduce_gn: no instantiation for %u row steps x %u splits\n", im,
+          g.splits);
+  abort();
 }
 
 const uint32_t kTileM[TILE_COUNT] = {64, 128, 64, 128, 128, 64, 64, 128, 64, 64, 128, 128, 64, 128, 64};
