@@ -30,7 +30,14 @@ int run(Ctx* c, GemmArgs& g, int a_mode, StatsOut* st = nullptr, RowStatsOut* rs
   g.splits = plan.splits;
   g.stats = nullptr;
   g.rstats = nullptr;
-  if (gn) gn->done = splitk_gn_ok(g, gn->f);
+  if (gn) {
+    // the reducer's records of the context's statistics-exchange area
+    gn->f.xchg = c->gn_xchg ? (uint64_t*)c->gn_xchg + (uint64_t)kXchgNchwRecs * kXchgWords
+                            : nullptr;
+    const char* e_spin = getenv("DI_GN_XCHG_SPIN");  // 0 forces the recomputing path
+    gn->f.spin = e_spin ? (uint32_t)strtoul(e_spin, nullptr, 10) : 20000u;
+    gn->done = splitk_gn_ok(g, gn->f);
+  }
   if (st) st->done = false;
   if (gn && gn->done) {
     // the reducer writes GN(output) (and the raw output and its statistics

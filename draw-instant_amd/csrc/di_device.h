@@ -76,6 +76,56 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Statistics exchange between the kXchgSlices workgroups that share a
+// GroupNorm group (k_norm.hip's NCHW GroupNorm, k_gemm.hip's fused split-K
+// reducer).  A record of kXchgWords 64-bit words per group holds one (sum,
+// sumsq) word pair per slice, then a 32-bit arrival counter.  Every launch
+// adds exactly kXchgSlices to the counter of each record it uses and the
+// owner's launches are stream-ordered, so o / kXchgSlices + 1 (o: a
+// workgroup's fetch-add result) is an epoch that the workgroups of one
+// launch share and no earlier launch used; a word {epoch, float bits} is
+// written and read whole (relaxed agent-scope atomics), so no fence orders
+// the words.  The context's exchange area: kXchgNchwRecs records for the
+// NCHW GroupNorm, then kXchgRedRecs for the reducer, zeroed at creation.
+constexpr uint32_t kXchgSlices = 8;  // divides 2^32: epochs stay aligned when o wraps
+constexpr uint32_t kXchgWords = 32;  // 256 B per record
+constexpr uint32_t kXchgNchwRecs = 64, kXchgRedRecs = 512;
+static_assert(2 * kXchgSlices + 1 <= kXchgWords && 2 * kXchgSlices <= 64, "record layout");
+
+// The arrival fetch-add on record rec (one thread of the workgroup).
+__device__ __forceinline__ uint32_t xchg_arrive(uint64_t* rec) {
+  return __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(rec + 2 * kXchgSlices), 1u,
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Publish slice s's (a, b) under epoch word ep (thread 0), then wave 0 polls
+// the record's 2 kXchgSlices words until all carry ep, at most `spin` polls,
+// and leaves them in sv[2 kXchgSlices] (LDS).  Returns, in wave 0, whether
+// every slice arrived; the caller shares that through LDS.  No barrier.
+__device__ __forceinline__ bool xchg_publish_poll(uint64_t* rec, uint64_t ep, uint32_t s, float a,
+                                                  float b, uint32_t spin, float* sv) {
+  const uint32_t tid = threadIdx.x;
+  if (tid == 0) {
+    __hip_atomic_store(rec + 2 * s, ep | __float_as_uint(a), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rec + 2 * s + 1, ep | __float_as_uint(b), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  bool all = false;
+  if (tid < (uint32_t)kWave) {
+    uint64_t word = ep;
+    for (uint32_t it = 0; it < spin; it++) {
+      if (tid < 2 * kXchgSlices)
+        word = __hip_atomic_load(rec + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      all = __all((word & 0xffffffff00000000ull) == ep);
+      if (all) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (tid < 2 * kXchgSlices) sv[tid] = __uint_as_float((uint32_t)word);
+  }
+  return all;
+}
+
 template <typename T>
 __device__ __forceinline__ float to_f(T v) {
   return (float)v;

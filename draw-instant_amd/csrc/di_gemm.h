@@ -167,6 +167,11 @@ struct GnFuse {
   // GemmArgs::stats layout (per 64-row chunk and channel), for other
   // GroupNorms that read it; null: none
   float* stats = nullptr;
+  // the reducer records of the context's statistics-exchange area
+  // (di_device.h) and the poll limit: images of more than 256 rows are then
+  // reduced by kXchgSlices workgroups per (group, image); null: one each
+  uint64_t* xchg = nullptr;
+  uint32_t spin = 0;
 };
 // Whether the fused reducer takes this call (g with its plan's splits):
 // batch 1, split-K with a built (rows per thread, split count) pair, a

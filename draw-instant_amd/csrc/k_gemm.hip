@@ -259,81 +259,115 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
 // is a template parameter: the IM x S partial loads are straight-line code
 // in batches of at most 24, each batch issued before any of it is added (a
 // loop over splits would make the compiler wait for every load at its top).
-template <int IM, int S, bool RES>
+// XCH: kXchgSlices workgroups per (group, image) (x = group * kXchgSlices +
+// slice), each taking HW / kXchgSlices = RS IM consecutive rows, exchange
+// their (sum, sumsq) through the group's record of f.xchg (the protocol of
+// di_device.h) and sum the slices' partials in slice order, so all agree
+// bit for bit.  Should a slice not arrive within f.spin polls, the
+// workgroup recomputes every other slice's sums from the split-K partials
+// (written by the launch before) with the same code and order: the same
+// bits, so the kernel always ends.
+template <int IM, int S, bool RES, bool XCH>
 __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, uint32_t Q,
                                                           uint32_t RS) {
   args_warm(g);
   kernarg_warm(f);
   __shared__ float red[2][10];
   __shared__ __attribute__((aligned(16))) float sst[64 * 40];  // one chunk, f.stats only
-  const uint32_t tid = threadIdx.x, grp = blockIdx.x, n = blockIdx.y;
+  __shared__ float sv[2 * kXchgSlices];                        // XCH: the slices' sums
+  __shared__ uint32_t s_o;
+  __shared__ int s_ok;
+  const uint32_t tid = threadIdx.x, n = blockIdx.y;
+  const uint32_t grp = XCH ? blockIdx.x / kXchgSlices : blockIdx.x;
+  const uint32_t sl = XCH ? blockIdx.x % kXchgSlices : 0u;
+  const uint32_t hws = RS * IM, hw = XCH ? hws * kXchgSlices : hws;  // rows: slice, image
   // tid / Q from a float reciprocal: exact for tid < 1024 (the product stays
   // 0.5 / Q away from an integer, far beyond its rounding error)
   const uint32_t r0 = (uint32_t)(((float)tid + 0.5f) * __builtin_amdgcn_rcpf((float)Q));
   const uint32_t q = tid - r0 * Q, c = grp * Q * 4 + q * 4;
-  const uint64_t row0 = (uint64_t)n * (RS * IM) + r0;
+  const uint64_t img0 = (uint64_t)n * hw;  // the image's first row
+  uint64_t* const rec = XCH ? f.xchg + ((uint64_t)n * f.groups + grp) * kXchgWords : nullptr;
   // per-channel and residual operands first: loads retire in order, and
-  // these are needed only after the partials (without a temb bias the bias
-  // is loaded twice rather than a load under a branch)
+  // these are needed only after the partials.  Without a temb bias the bias
+  // is loaded twice rather than a load under a branch; the empty asm hides
+  // where the pointer came from, else the compiler turns the second load
+  // into a copy of the first, which waits for it before any later load
   const f32x4 bb = ld4(g.bias + c);
-  const f32x4 tb = ld4(g.bias2 ? g.bias2 + (uint64_t)n * g.ld_b2 + c : g.bias + c);
+  uint64_t tbase = (uint64_t)(g.bias2 ? g.bias2 + (uint64_t)n * g.ld_b2 : g.bias);
+  asm volatile("" : "+s"(tbase));
+  typedef __attribute__((address_space(1))) const f32x4 gf32x4;  // global, not flat
+  const f32x4 tb = *(gf32x4*)(tbase + (uint64_t)c * 4);
   const f32x4 gm = ld4(f.gamma + c);
   const f32x4 bt = ld4(f.beta + c);
-  f16x4 rr[RES ? IM : 1];
-  if constexpr (RES) {
-    const f16* R = (const f16*)g.res + row0 * g.ldr + c;
+  // the stored values h of slice j's rows (this thread's) and their sum and
+  // sum of squares; `arrive`: the exchange's arrival fetch-add goes out
+  // after the slice's loads (its result is waited for at once, which would
+  // hold back loads issued after it)
+  auto slice = [&](uint32_t j, f16x4(&h)[IM], float& sum, float& sq, bool arrive) {
+    const uint64_t row0 = img0 + (uint64_t)j * hws + r0;
+    f16x4 rr[RES ? IM : 1];
+    if constexpr (RES) {
+      const f16* R = (const f16*)g.res + row0 * g.ldr + c;
 #pragma unroll
-    for (int i = 0; i < IM; i++) rr[i] = *(const f16x4*)(R + (uint64_t)i * RS * g.ldr);
-  }
-  // partials in column groups (part_cpg = cpg): the group's image block is
-  // contiguous, thread t reads quads t, t + RS Q, ... of it
-  const float* p = g.part + ((uint64_t)grp * g.M + row0) * (Q * 4) + q * 4;
-  const uint64_t sstep = (uint64_t)g.M * g.N, rstep = (uint64_t)RS * Q * 4;
-  constexpr int NL = IM * S, NB = NL <= 24 ? NL : IM >= 8 ? 16 : 24;
-  f32x4 acc[IM];
-#pragma unroll
-  for (int i = 0; i < IM; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int b0 = 0; b0 < NL; b0 += NB) {
-    f32x4 t[NB];
-#pragma unroll
-    for (int u = 0; u < NB; u++) {
-      const int j = b0 + u;  // split j / IM of row step j % IM: splits in order per row
-      if (j < NL) t[u] = ld4(p + (uint64_t)(j / IM) * sstep + (uint64_t)(j % IM) * rstep);
+      for (int i = 0; i < IM; i++) rr[i] = *(const f16x4*)(R + (uint64_t)i * RS * g.ldr);
     }
-    // the whole batch is issued before the scheduler may start its adds
-    __builtin_amdgcn_sched_barrier(0);
+    // partials in column groups (part_cpg = cpg): the group's rows are
+    // contiguous, thread t reads quads t, t + RS Q, ... of the slice
+    const float* p = g.part + ((uint64_t)grp * g.M + row0) * (Q * 4) + q * 4;
+    const uint64_t sstep = (uint64_t)g.M * g.N, rstep = (uint64_t)RS * Q * 4;
+    constexpr int NL = IM * S, NB = NL <= 24 ? NL : IM >= 8 ? 16 : 24;
+    f32x4 acc[IM];
 #pragma unroll
-    for (int u = 0; u < NB; u++) {
-      const int j = b0 + u;
-      if (j < NL) acc[j % IM] += t[u];
+    for (int i = 0; i < IM; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b0 = 0; b0 < NL; b0 += NB) {
+      f32x4 t[NB];
+#pragma unroll
+      for (int u = 0; u < NB; u++) {
+        const int jj = b0 + u;  // split jj / IM of row step jj % IM: splits in order per row
+        if (jj < NL) t[u] = ld4(p + (uint64_t)(jj / IM) * sstep + (uint64_t)(jj % IM) * rstep);
+      }
+      if constexpr (XCH) {
+        if (arrive && b0 + NB >= NL && tid == 0) s_o = xchg_arrive(rec);
+      }
+      // the whole batch is issued before the scheduler may start its adds
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < NB; u++) {
+        const int jj = b0 + u;
+        if (jj < NL) acc[jj % IM] += t[u];
+      }
     }
-  }
+    sum = 0.0f;
+    sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < IM; i++) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float v = acc[i][k] * g.alpha;
+        v += bb[k];
+        if (g.bias2) v += tb[k];
+        if constexpr (RES) v += (float)rr[i][k];
+        h[i][k] = (f16)v;
+        const float x = (float)h[i][k];
+        sum += x;
+        sq += __fmul_rn(x, x);
+      }
+    }
+  };
   f16x4 h[IM];
-  float sum = 0.0f, sq = 0.0f;
-#pragma unroll
-  for (int i = 0; i < IM; i++) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float v = acc[i][j] * g.alpha;
-      v += bb[j];
-      if (g.bias2) v += tb[j];
-      if constexpr (RES) v += (float)rr[i][j];
-      h[i][j] = (f16)v;
-      const float x = (float)h[i][j];
-      sum += x;
-      sq += __fmul_rn(x, x);
-    }
-  }
+  float sum, sq;
+  slice(sl, h, sum, sq, true);
   sum = wave_sum(sum);
   sq = wave_sum(sq);
   if (tid % 64 == 0) {
     red[0][tid / 64] = sum;
     red[1][tid / 64] = sq;
   }
+  const uint64_t row0 = img0 + (uint64_t)sl * hws + r0;
   if (f.stats) {
     // per 64-row chunk and channel (sum, sum of squares) of the stored
-    // values, the GemmArgs::stats layout: row step i holds the image's
+    // values, the GemmArgs::stats layout: row step i holds the slice's
     // chunks i * RS / 64 .. + RS / 64 - 1.  Step by step through LDS
     // ([RS][cpg] floats, RS * cpg = 16 * blockDim <= 64 * 40): 8 adjacent
     // lanes per (chunk, statistic, channel) each take every eighth row of
@@ -342,7 +376,7 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
     const uint32_t cpg = Q * 4, task = tid >> 3, part = tid & 7;
     const uint32_t cs = (uint32_t)(((float)task + 0.5f) * __builtin_amdgcn_rcpf((float)cpg));
     const uint32_t ch = task - cs * cpg, lc = cs >> 1, st = cs & 1;
-    const uint64_t chunk0 = (uint64_t)n * (RS * IM / 64) + lc;
+    const uint64_t chunk0 = (img0 + (uint64_t)sl * hws) / 64 + lc;
 #pragma unroll
     for (int i = 0; i < IM; i++) {
       *(f32x4*)&sst[r0 * cpg + q * 4] =
@@ -368,7 +402,51 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
     ps += red[0][w];
     pq += red[1][w];
   }
-  const float L = (float)(Q * 4) * (float)(RS * IM);
+  if constexpr (XCH) {
+    const uint64_t ep = (uint64_t)(s_o / kXchgSlices + 1u) << 32;  // s_o: before the barrier
+    const bool all = xchg_publish_poll(rec, ep, sl, ps, pq, f.spin, sv);
+    if (tid == 0) s_ok = all ? 1 : 0;
+    __syncthreads();
+    if (!s_ok) {
+      for (uint32_t j = 0; j < kXchgSlices; j++) {
+        if (j == sl) {
+          if (tid == 0) {
+            sv[2 * j] = ps;
+            sv[2 * j + 1] = pq;
+          }
+          continue;
+        }
+        f16x4 ht[IM];
+        float s2, q2;
+        slice(j, ht, s2, q2, false);
+        s2 = wave_sum(s2);
+        q2 = wave_sum(q2);
+        __syncthreads();  // every read of red before is done
+        if (tid % 64 == 0) {
+          red[0][tid / 64] = s2;
+          red[1][tid / 64] = q2;
+        }
+        __syncthreads();
+        if (tid == 0) {
+          float a = 0.0f, b = 0.0f;
+          for (uint32_t w = 0; w < blockDim.x / 64; w++) {
+            a += red[0][w];
+            b += red[1][w];
+          }
+          sv[2 * j] = a;
+          sv[2 * j + 1] = b;
+        }
+      }
+      __syncthreads();
+    }
+    ps = 0.0f;
+    pq = 0.0f;
+    for (uint32_t j = 0; j < kXchgSlices; j++) {
+      ps += sv[2 * j];
+      pq += sv[2 * j + 1];
+    }
+  }
+  const float L = (float)(Q * 4) * (float)hw;
   const float mean = ps / L;
   const float var = fmaxf(pq / L - mean * mean, 0.0f);
   const float rstd = 1.0f / sqrtf(var + f.eps);
@@ -397,15 +475,22 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
 }
 
 // (row steps, split count) pairs the fused reducer is built for (16 row
-// steps would spill its accumulators to scratch)
+// steps would spill its accumulators to scratch); with the exchange
+// (images of 512 or 1024 rows: slices of 64 or 128 rows)
 #define DI_RGN_CASES(X)                                                                   \
   X(1, 2) X(1, 3) X(1, 4) X(1, 5) X(1, 6) X(1, 8) X(1, 12) X(2, 2) X(2, 3) X(2, 4) X(2, 5) \
   X(2, 6) X(2, 8) X(2, 12) X(4, 2) X(4, 3) X(4, 4) X(4, 5) X(4, 6) X(4, 8) X(4, 12)       \
   X(8, 2) X(8, 3) X(8, 4) X(8, 5) X(8, 6)
+#define DI_RGNX_CASES(X) \
+  X(1, 2) X(1, 3) X(1, 4) X(1, 5) X(1, 6) X(2, 2) X(2, 3) X(2, 4) X(2, 5) X(2, 6)
 
-bool splitk_gn_built(uint32_t im, uint32_t splits) {
+bool splitk_gn_built(uint32_t im, uint32_t splits, bool xch) {
 #define DI_RGN_HAS(IMV, SV) if (im == IMV && splits == SV) return true;
-  DI_RGN_CASES(DI_RGN_HAS)
+  if (xch) {
+    DI_RGNX_CASES(DI_RGN_HAS)
+  } else {
+    DI_RGN_CASES(DI_RGN_HAS)
+  }
 #undef DI_RGN_HAS
   return false;
 }
@@ -418,19 +503,41 @@ uint32_t splitk_gn_rs(uint32_t q, uint32_t hw) {
   return rs;
 }
 
+// whether the exchange variant takes images of f.hw rows (DI_GN_REDUCE_XCHG=0
+// keeps one workgroup per group and image)
+bool splitk_gn_xch(const GnFuse& f) {
+  const char* e = getenv("DI_GN_REDUCE_XCHG");
+  return f.xchg != nullptr && f.hw > 256 && !(e && e[0] == '0');
+}
+
 void launch_splitk_reduce_gn(const GemmArgs& g, const GnFuse& f, hipStream_t s) {
-  const uint32_t q = g.N / f.groups / 4, rs = splitk_gn_rs(q, f.hw), im = f.hw / rs;
-  const dim3 grid(f.groups, g.M / f.hw), block(rs * q);
-#define DI_RGN_LAUNCH(IMV, SV)                                                \
-  if (im == IMV && g.splits == SV) {                                          \
-    if (g.res)                                                                \
-      k_splitk_reduce_gn<IMV, SV, true><<<grid, block, 0, s>>>(g, f, q, rs);  \
-    else                                                                      \
-      k_splitk_reduce_gn<IMV, SV, false><<<grid, block, 0, s>>>(g, f, q, rs); \
-    return;                                                                   \
+  const bool xch = splitk_gn_xch(f);
+  const uint32_t hws = xch ? f.hw / kXchgSlices : f.hw;
+  const uint32_t q = g.N / f.groups / 4, rs = splitk_gn_rs(q, hws), im = hws / rs;
+  const dim3 grid(f.groups * (xch ? kXchgSlices : 1u), g.M / f.hw), block(rs * q);
+#define DI_RGN_LAUNCH(IMV, SV)                                                       \
+  if (im == IMV && g.splits == SV) {                                                 \
+    if (g.res)                                                                       \
+      k_splitk_reduce_gn<IMV, SV, true, false><<<grid, block, 0, s>>>(g, f, q, rs);  \
+    else                                                                             \
+      k_splitk_reduce_gn<IMV, SV, false, false><<<grid, block, 0, s>>>(g, f, q, rs); \
+    return;                                                                          \
   }
-  DI_RGN_CASES(DI_RGN_LAUNCH)
+#define DI_RGNX_LAUNCH(IMV, SV)                                                     \
+  if (im == IMV && g.splits == SV) {                                                \
+    if (g.res)                                                                      \
+      k_splitk_reduce_gn<IMV, SV, true, true><<<grid, block, 0, s>>>(g, f, q, rs);  \
+    else                                                                            \
+      k_splitk_reduce_gn<IMV, SV, false, true><<<grid, block, 0, s>>>(g, f, q, rs); \
+    return;                                                                         \
+  }
+  if (xch) {
+    DI_RGNX_CASES(DI_RGNX_LAUNCH)
+  } else {
+    DI_RGN_CASES(DI_RGN_LAUNCH)
+  }
 #undef DI_RGN_LAUNCH
+#undef DI_RGNX_LAUNCH
   // splitk_gn_ok admits only built pairs: reaching here would leave the
   // output unwritten
   fprintf(stderr, "launch_splitk_reduce_gn: no instantiation for %u row steps x %u splits\n", im,
@@ -662,15 +769,20 @@ uint32_t gemm_rstats_tiles(const GemmArgs& g, int tile_cfg) {
 bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f) {
   if (g.splits <= 1 || g.batch != 1 || !f.groups || !f.hw || !f.gamma || !f.beta || !f.y)
     return false;
-  // keeping the raw output (a residual read and a second store per value)
-  // pays at 16 x 16 and below: at 32 x 32 the fused conv2 reducer took
-  // 11.2 us against 5.0 + 5.0 us for the reducer and apply it replaces
-  if (f.raw && f.hw > 256) return false;
+  // images of more than 256 rows: kXchgSlices workgroups per (group,
+  // image) exchanging their statistics (with the raw output one workgroup
+  // per group did not pay: at 32 x 32 the fused conv2 reducer took 11.2 us
+  // against 5.0 + 5.0 us for the reducer and apply it replaces)
+  const bool xch = splitk_gn_xch(f);
+  if (f.raw && f.hw > 256 && !xch) return false;
+  const uint32_t hws = xch ? f.hw / kXchgSlices : f.hw;  // rows per workgroup
+  if (xch && (f.hw % kXchgSlices != 0 || (uint64_t)(g.M / f.hw) * f.groups > kXchgRedRecs))
+    return false;
   // statistics of the stored values only with the raw output
   if (f.stats && (!f.raw || ((uintptr_t)f.stats & 7) != 0)) return false;
   const uint32_t cpg = g.N / f.groups, slots = g.part_slots ? g.part_slots : g.splits;
-  return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && f.hw % 64 == 0 &&
-         splitk_gn_built(f.hw / splitk_gn_rs(cpg / 4, f.hw), slots) && g.M % f.hw == 0 &&
+  return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && hws % 64 == 0 &&
+         splitk_gn_built(hws / splitk_gn_rs(cpg / 4, hws), slots, xch) && g.M % f.hw == 0 &&
          g.bias && (!g.bias2 || (g.rows_b2 == f.hw && g.ld_b2 % 4 == 0)) &&
          (!g.res || (!g.res_f32 && g.ldr % 4 == 0 && ((uintptr_t)g.res & 7) == 0)) &&
          (!f.raw || (g.c && g.ldc % 4 == 0 && ((uintptr_t)g.c & 7) == 0)) &&

@@ -300,31 +300,20 @@ __global__ __launch_bounds__(kFusedT) void k_gn_nchw_fused(
 }
 
 // Single-launch NCHW GroupNorm whose workgroups read only their own slice and
-// exchange the slice statistics.  kXS workgroups per group, each holding its
-// slice (<= kXU rounds of kXT vectors) in registers:
-//  1. at entry, one fetch-add on the group's arrival counter (agent scope,
-//     relaxed) returns o; every launch adds exactly kXS per group and the
-//     context's launches are stream-ordered, so o / kXS + 1 is an epoch that
-//     all workgroups of this launch share and no earlier launch used;
-//  2. the slice's (sum, sumsq) are reduced in a fixed order and published as
-//     two 64-bit words {epoch, float bits} with relaxed agent-scope atomic
-//     stores: each word is read whole or not at all, so no fence orders them;
-//  3. one wave polls the group's 2 kXS words (relaxed agent-scope atomic
-//     loads) until every word carries this epoch, at most `spin` polls;
-//  4. the kXS partials are summed in slice order by every workgroup alike,
-//     so the S slices normalise with bit-identical statistics.
-// Should a slice not arrive within `spin` polls (a workgroup not resident,
-// or spin = 0), the workgroup recomputes every slice's partials itself from
-// the input with the same thread mapping and reduction order - the same
-// bits, from one group's worth of extra reads - so the kernel always ends.
-// The exchange area (zeroed at context creation) holds per group kXS x 2
-// words and the counter; concurrent launches on one context would race,
-// which the context's single stream rules out.
-constexpr int kXT = 256;           // threads per workgroup
-constexpr uint32_t kXS = 8;        // workgroups (slices) per group; divides 2^32
-constexpr uint32_t kXWords = 32;   // 64-bit words per group record (256 B)
-constexpr uint32_t kXGroups = 64;  // groups the exchange area serves
-static_assert(2 * kXS + 1 <= kXWords && 2 * kXS <= 64, "slot words and counter in one record");
+// exchange the slice statistics (the record protocol of di_device.h):
+// kXchgSlices workgroups per group, each holding its slice (<= kXU rounds of
+// kXT vectors) in registers, reduce (sum, sumsq) in a fixed order, publish
+// them under the launch's epoch and poll the group's record; the kXchgSlices
+// partials are summed in slice order by every workgroup alike, so the slices
+// normalise with bit-identical statistics.  Should a slice not arrive within
+// `spin` polls (a workgroup not resident, or spin = 0), the workgroup
+// recomputes every slice's partials itself from the input with the same
+// thread mapping and reduction order - the same bits, from one group's worth
+// of extra reads - so the kernel always ends.  The arrival fetch-add is
+// issued after the slice's loads: its result is waited for at once, which
+// would hold back loads issued after it.
+constexpr int kXT = 256;  // threads per workgroup
+constexpr uint32_t kXS = kXchgSlices;
 
 template <typename T, int VEC, int U>
 __device__ __forceinline__ void xslice_load(const T* __restrict__ x, uint32_t lo, uint32_t hi,
@@ -374,8 +363,7 @@ __global__ __launch_bounds__(kXT) void k_gn_nchw_xchg(
   const uint32_t w = xcd < extra ? xcd * (per + 1) + idx : extra * (per + 1) + (xcd - extra) * per + idx;
   const uint32_t ng = w / kXS, s = w % kXS;
   const uint32_t L = cpg * HW;
-  uint64_t* const rec = xchg + (uint64_t)ng * kXWords;
-  uint32_t* const arrive = reinterpret_cast<uint32_t*>(rec + 2 * kXS);
+  uint64_t* const rec = xchg + (uint64_t)ng * kXchgWords;
   const T* const xg = x + (uint64_t)ng * L;
   auto bounds = [&](uint32_t j, uint32_t& lo, uint32_t& hi) {
     lo = min(j * chunk, L);
@@ -394,31 +382,11 @@ __global__ __launch_bounds__(kXT) void k_gn_nchw_xchg(
     bt[u] = beta[c];
   }
   sched_fence();
-  // after the slice's loads: the atomic's round trip overlaps them (its
-  // result is waited for at once, which would hold back loads issued later)
-  if (tid == 0) s_o = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) s_o = xchg_arrive(rec);
   const float2 p = xslice_partial<VEC, U>(v, lo, hi, sh);  // barrier: s_o visible
   const uint64_t ep = (uint64_t)(s_o / kXS + 1u) << 32;
-  if (tid == 0) {
-    __hip_atomic_store(rec + 2 * s, ep | __float_as_uint(p.x), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(rec + 2 * s + 1, ep | __float_as_uint(p.y), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (tid < kWave) {
-    const uint32_t lane = tid;
-    uint64_t word = ep;
-    bool all = false;
-    for (uint32_t it = 0; it < spin; it++) {
-      if (lane < 2 * kXS)
-        word = __hip_atomic_load(rec + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      all = __all((word & 0xffffffff00000000ull) == ep);
-      if (all) break;
-      __builtin_amdgcn_s_sleep(2);
-    }
-    if (lane < 2 * kXS) sv[lane] = __uint_as_float((uint32_t)word);
-    if (lane == 0) s_ok = all ? 1 : 0;
-  }
+  const bool all = xchg_publish_poll(rec, ep, s, p.x, p.y, spin, sv);
+  if (tid == 0) s_ok = all ? 1 : 0;
   __syncthreads();
   if (!s_ok) {
     // recompute every slice's partials exactly as its own workgroup does
@@ -1181,7 +1149,7 @@ bool gn_fused(hipStream_t st, const T* x, const float* gamma, const float* beta,
   return true;
 }
 
-// The exchange kernel for NG <= kXGroups groups whose slices fit kXU rounds
+// The exchange kernel for NG <= kXchgNchwRecs groups whose slices fit kXU rounds
 // of kXT vectors; false: nothing launched.  Read at every call (tests switch
 // them between calls): DI_GN_XCHG=0 turns the kernel off, DI_GN_XCHG_SPIN
 // sets the poll limit (0 forces the recomputing path).
@@ -1193,7 +1161,8 @@ bool gn_xchg(Ctx* c, const T* x, const float* gamma, const float* beta, T* y, ui
   const char* e_spin = getenv("DI_GN_XCHG_SPIN");
   const uint32_t spin = e_spin ? (uint32_t)strtoul(e_spin, nullptr, 10) : 20000u;
   const uint32_t L = cpg * HW;
-  if ((e_on && !atoi(e_on)) || !c->gn_xchg || NG == 0 || NG > kXGroups || L < kXS * kXT) return false;
+  if ((e_on && !atoi(e_on)) || !c->gn_xchg || NG == 0 || NG > kXchgNchwRecs || L < kXS * kXT)
+    return false;
   uint32_t chunk = (L + kXS - 1) / kXS;
   chunk = (chunk + VEC - 1) / VEC * VEC;
   const uint32_t rounds = (chunk + kXT * VEC - 1) / (kXT * VEC);
@@ -1247,7 +1216,9 @@ int gn_nchw_dt(Ctx* c, const void* x, const float* gamma, const float* beta, voi
 
 }  // namespace
 
-uint64_t gn_xchg_bytes() { return (uint64_t)kXGroups * kXWords * sizeof(uint64_t); }
+uint64_t gn_xchg_bytes() {
+  return (uint64_t)(kXchgNchwRecs + kXchgRedRecs) * kXchgWords * sizeof(uint64_t);
+}
 
 int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const float* beta,
                            void* y, uint32_t N, uint32_t G, uint32_t cpg, uint32_t HW,

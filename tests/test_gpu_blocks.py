@@ -93,7 +93,7 @@ def test_resnet_block(dev, rng, B, cin, cout, H, W, temb):
 @pytest.mark.parametrize("B,cin,cout,H,W", [
     (1, 1280, 1280, 8, 8),    # conv1 split 12: one row-step of 64 pixels per thread
     (2, 1280, 1280, 16, 16),  # split 5, four row-steps, two images
-    (1, 640, 640, 32, 32),    # 20 channels per group: 128-row steps, eight of them, split 2
+    (1, 640, 640, 32, 32),    # 20 channels per group, split 2: eight 128-row slices exchanging
     (1, 2560, 1280, 8, 8),    # up-block input width (K = 23040)
 ])
 def test_resnet_gn_reducer_matches_apply(dev, rng, monkeypatch, B, cin, cout, H, W):
@@ -110,13 +110,28 @@ def test_resnet_gn_reducer_matches_apply(dev, rng, monkeypatch, B, cin, cout, H,
     w = blocks.upload_resnet(dev, sd, "r")
     bx = dev.storage(x.transpose(0, 2, 3, 1).astype(np.float16))
     bt = dev.storage(t)
-    outs = []
-    for mode in ("1", "0"):
-        monkeypatch.setenv("DI_GN_REDUCE_FUSE", mode)
+    def run():
         y = dev.create_buffer(B * H * W * cout * 2)
         blocks.resnet_block(dev, w, bx, bt, y, B, cin, cout, H, W, 1280)
-        outs.append(dev.download(y, np.float16).astype(np.float32))
-    fused, sep = outs
+        return dev.download(y, np.float16).astype(np.float32)
+
+    monkeypatch.setenv("DI_GN_REDUCE_FUSE", "1")
+    fused = run()
+    if H * W > 256:
+        # eight workgroups per (group, image) exchanging their statistics:
+        # the recomputing path (no slice awaited) gives the same bits, one
+        # workgroup per group the same values up to the order of the sums
+        monkeypatch.setenv("DI_GN_XCHG_SPIN", "0")
+        np.testing.assert_array_equal(run(), fused)
+        monkeypatch.delenv("DI_GN_XCHG_SPIN")
+        monkeypatch.setenv("DI_GN_REDUCE_XCHG", "0")
+        one = run()
+        monkeypatch.delenv("DI_GN_REDUCE_XCHG")
+        print(f"   exchange vs one workgroup per group: rel-L2 {rel_l2(fused, one):.2e}",
+              flush=True)
+        assert rel_l2(fused, one) <= 1e-3
+    monkeypatch.setenv("DI_GN_REDUCE_FUSE", "0")
+    sep = run()
     err = rel_l2(fused, sep)
     scale = float(np.max(np.abs(sep)))
     print(f"   rel-L2 {err:.2e} max-abs {np.max(np.abs(fused - sep)):.2e} (max |y| {scale:.2f})",

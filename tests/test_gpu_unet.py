@@ -196,6 +196,28 @@ def test_sd21_gn_in_reducers_matches_separate(sd21, rng, monkeypatch):
     assert np.isfinite(fused).all() and err <= 5e-3
 
 
+def test_sd21_gn_exchange_reducers(sd21, rng, monkeypatch):
+    """cfg5 at B=1: the 32 x 32 split-K reducers that apply a GroupNorm with
+    eight workgroups per (group, image) exchanging their statistics give the
+    same bits when every workgroup recomputes the other slices' sums itself
+    (DI_GN_XCHG_SPIN=0, the path a workgroup takes when a slice does not
+    arrive), and agree with one workgroup per group or a separate apply
+    launch (DI_GN_REDUCE_XCHG=0) up to the fp32 summation order."""
+    x, ctx = _inputs(rng, 1, 64, 64, 77, 1024)
+    xch = sd21(x, 999.0, ctx)
+    monkeypatch.setenv("DI_GN_XCHG_SPIN", "0")
+    rec = sd21(x, 999.0, ctx)
+    monkeypatch.delenv("DI_GN_XCHG_SPIN")
+    np.testing.assert_array_equal(rec, xch)
+    monkeypatch.setenv("DI_GN_REDUCE_XCHG", "0")
+    one = sd21(x, 999.0, ctx)
+    monkeypatch.delenv("DI_GN_REDUCE_XCHG")
+    err = rel_l2(xch, one)
+    print(f"[sd21 gn exchange] rel-L2 {err:.2e} vs one workgroup per group", flush=True)
+    assert np.isfinite(xch).all() and err <= 5e-3
+    np.testing.assert_array_equal(sd21(x, 999.0, ctx), xch)
+
+
 def test_sd21_shortcut_partials_match_separate(sd21, rng, monkeypatch):
     """cfg5 at B=1 with each split-K ResNet shortcut's partials summed by its
     conv2's reducer (with the summed bias) against the same step with the
