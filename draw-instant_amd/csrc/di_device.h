@@ -89,7 +89,10 @@ __device__ __forceinline__ float wave_max(float v) {
 // NCHW GroupNorm, then kXchgRedRecs for the reducer, zeroed at creation.
 constexpr uint32_t kXchgSlices = 8;  // divides 2^32: epochs stay aligned when o wraps
 constexpr uint32_t kXchgWords = 32;  // 256 B per record
-constexpr uint32_t kXchgNchwRecs = 64, kXchgRedRecs = 512;
+// regions: the NCHW GroupNorm's, then the reducer's with eight and with four
+// slices per record (a record serves one slice count only, so its counter
+// advances by that count at every launch)
+constexpr uint32_t kXchgNchwRecs = 64, kXchgRedRecs = 512, kXchgRed4Recs = 512;
 static_assert(2 * kXchgSlices + 1 <= kXchgWords && 2 * kXchgSlices <= 64, "record layout");
 
 // The arrival fetch-add on record rec (one thread of the workgroup).
@@ -99,11 +102,13 @@ __device__ __forceinline__ uint32_t xchg_arrive(uint64_t* rec) {
 }
 
 // Publish slice s's (a, b) under epoch word ep (thread 0), then wave 0 polls
-// the record's 2 kXchgSlices words until all carry ep, at most `spin` polls,
-// and leaves them in sv[2 kXchgSlices] (LDS).  Returns, in wave 0, whether
-// every slice arrived; the caller shares that through LDS.  No barrier.
+// the record's 2 NS words until all carry ep, at most `spin` polls, and
+// leaves them in sv[2 NS] (LDS).  Returns, in wave 0, whether every slice
+// arrived; the caller shares that through LDS.  No barrier.
+template <uint32_t NS = kXchgSlices>
 __device__ __forceinline__ bool xchg_publish_poll(uint64_t* rec, uint64_t ep, uint32_t s, float a,
                                                   float b, uint32_t spin, float* sv) {
+  static_assert(NS <= kXchgSlices && (NS & (NS - 1)) == 0, "a power of two up to the record's");
   const uint32_t tid = threadIdx.x;
   if (tid == 0) {
     __hip_atomic_store(rec + 2 * s, ep | __float_as_uint(a), __ATOMIC_RELAXED,
@@ -115,13 +120,13 @@ __device__ __forceinline__ bool xchg_publish_poll(uint64_t* rec, uint64_t ep, ui
   if (tid < (uint32_t)kWave) {
     uint64_t word = ep;
     for (uint32_t it = 0; it < spin; it++) {
-      if (tid < 2 * kXchgSlices)
+      if (tid < 2 * NS)
         word = __hip_atomic_load(rec + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       all = __all((word & 0xffffffff00000000ull) == ep);
       if (all) break;
       __builtin_amdgcn_s_sleep(2);
     }
-    if (tid < 2 * kXchgSlices) sv[tid] = __uint_as_float((uint32_t)word);
+    if (tid < 2 * NS) sv[tid] = __uint_as_float((uint32_t)word);
   }
   return all;
 }

@@ -259,34 +259,37 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_stats(GemmArgs g) {
 // is a template parameter: the IM x S partial loads are straight-line code
 // in batches of at most 24, each batch issued before any of it is added (a
 // loop over splits would make the compiler wait for every load at its top).
-// XCH: kXchgSlices workgroups per (group, image) (x = group * kXchgSlices +
-// slice), each taking HW / kXchgSlices = RS IM consecutive rows, exchange
-// their (sum, sumsq) through the group's record of f.xchg (the protocol of
+// NS > 1: NS workgroups per (group, image) (x = group * NS + slice), each
+// taking HW / NS = RS IM consecutive rows, exchange their (sum, sumsq)
+// through the group's record in f.xchg's region for NS (the protocol of
 // di_device.h) and sum the slices' partials in slice order, so all agree
 // bit for bit.  Should a slice not arrive within f.spin polls, the
 // workgroup recomputes every other slice's sums from the split-K partials
 // (written by the launch before) with the same code and order: the same
 // bits, so the kernel always ends.
-template <int IM, int S, bool RES, bool XCH>
+template <int IM, int S, bool RES, int NS>
 __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, uint32_t Q,
                                                           uint32_t RS) {
   args_warm(g);
   kernarg_warm(f);
   __shared__ float red[2][10];
   __shared__ __attribute__((aligned(16))) float sst[64 * 40];  // one chunk, f.stats only
-  __shared__ float sv[2 * kXchgSlices];                        // XCH: the slices' sums
+  constexpr bool XCH = NS > 1;
+  static_assert(NS == 1 || NS == 4 || NS == kXchgSlices, "record regions");
+  __shared__ float sv[2 * NS];                                 // XCH: the slices' sums
   __shared__ uint32_t s_o;
   __shared__ int s_ok;
   const uint32_t tid = threadIdx.x, n = blockIdx.y;
-  const uint32_t grp = XCH ? blockIdx.x / kXchgSlices : blockIdx.x;
-  const uint32_t sl = XCH ? blockIdx.x % kXchgSlices : 0u;
-  const uint32_t hws = RS * IM, hw = XCH ? hws * kXchgSlices : hws;  // rows: slice, image
+  const uint32_t grp = blockIdx.x / NS, sl = blockIdx.x % NS;
+  const uint32_t hws = RS * IM, hw = hws * NS;  // rows: slice, image
   // tid / Q from a float reciprocal: exact for tid < 1024 (the product stays
   // 0.5 / Q away from an integer, far beyond its rounding error)
   const uint32_t r0 = (uint32_t)(((float)tid + 0.5f) * __builtin_amdgcn_rcpf((float)Q));
   const uint32_t q = tid - r0 * Q, c = grp * Q * 4 + q * 4;
   const uint64_t img0 = (uint64_t)n * hw;  // the image's first row
-  uint64_t* const rec = XCH ? f.xchg + ((uint64_t)n * f.groups + grp) * kXchgWords : nullptr;
+  uint64_t* const rec =
+      XCH ? f.xchg + ((NS == 4 ? kXchgRedRecs : 0u) + (uint64_t)n * f.groups + grp) * kXchgWords
+          : nullptr;
   // per-channel and residual operands first: loads retire in order, and
   // these are needed only after the partials.  Without a temb bias the bias
   // is loaded twice rather than a load under a branch; the empty asm hides
@@ -403,12 +406,12 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
     pq += red[1][w];
   }
   if constexpr (XCH) {
-    const uint64_t ep = (uint64_t)(s_o / kXchgSlices + 1u) << 32;  // s_o: before the barrier
-    const bool all = xchg_publish_poll(rec, ep, sl, ps, pq, f.spin, sv);
+    const uint64_t ep = (uint64_t)(s_o / NS + 1u) << 32;  // s_o: before the barrier
+    const bool all = xchg_publish_poll<NS>(rec, ep, sl, ps, pq, f.spin, sv);
     if (tid == 0) s_ok = all ? 1 : 0;
     __syncthreads();
     if (!s_ok) {
-      for (uint32_t j = 0; j < kXchgSlices; j++) {
+      for (uint32_t j = 0; j < NS; j++) {
         if (j == sl) {
           if (tid == 0) {
             sv[2 * j] = ps;
@@ -441,7 +444,7 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
     }
     ps = 0.0f;
     pq = 0.0f;
-    for (uint32_t j = 0; j < kXchgSlices; j++) {
+    for (uint32_t j = 0; j < NS; j++) {
       ps += sv[2 * j];
       pq += sv[2 * j + 1];
     }
@@ -475,19 +478,23 @@ __global__ __launch_bounds__(640) void k_splitk_reduce_gn(GemmArgs g, GnFuse f, 
 }
 
 // (row steps, split count) pairs the fused reducer is built for (16 row
-// steps would spill its accumulators to scratch); with the exchange
-// (images of 512 or 1024 rows: slices of 64 or 128 rows)
+// steps would spill its accumulators to scratch); with the exchange, eight
+// slices (images of 512 or 1024 rows: slices of 64 or 128) and four (256
+// rows: slices of 64)
 #define DI_RGN_CASES(X)                                                                   \
   X(1, 2) X(1, 3) X(1, 4) X(1, 5) X(1, 6) X(1, 8) X(1, 12) X(2, 2) X(2, 3) X(2, 4) X(2, 5) \
   X(2, 6) X(2, 8) X(2, 12) X(4, 2) X(4, 3) X(4, 4) X(4, 5) X(4, 6) X(4, 8) X(4, 12)       \
   X(8, 2) X(8, 3) X(8, 4) X(8, 5) X(8, 6)
 #define DI_RGNX_CASES(X) \
   X(1, 2) X(1, 3) X(1, 4) X(1, 5) X(1, 6) X(2, 2) X(2, 3) X(2, 4) X(2, 5) X(2, 6)
+#define DI_RGNX4_CASES(X) X(1, 2) X(1, 3) X(1, 4) X(1, 5) X(1, 6) X(1, 8) X(1, 12)
 
-bool splitk_gn_built(uint32_t im, uint32_t splits, bool xch) {
+bool splitk_gn_built(uint32_t im, uint32_t splits, uint32_t ns) {
 #define DI_RGN_HAS(IMV, SV) if (im == IMV && splits == SV) return true;
-  if (xch) {
+  if (ns == kXchgSlices) {
     DI_RGNX_CASES(DI_RGN_HAS)
+  } else if (ns == 4) {
+    DI_RGNX4_CASES(DI_RGN_HAS)
   } else {
     DI_RGN_CASES(DI_RGN_HAS)
   }
@@ -503,41 +510,42 @@ uint32_t splitk_gn_rs(uint32_t q, uint32_t hw) {
   return rs;
 }
 
-// whether the exchange variant takes images of f.hw rows (DI_GN_REDUCE_XCHG=0
-// keeps one workgroup per group and image)
-bool splitk_gn_xch(const GnFuse& f) {
+// Workgroups per (group, image) of the fused reducer: eight exchanging their
+// statistics for images of more than 256 rows, four for 256 rows, else one
+// (DI_GN_REDUCE_XCHG=0: one always)
+uint32_t splitk_gn_slices(const GnFuse& f) {
   const char* e = getenv("DI_GN_REDUCE_XCHG");
-  return f.xchg != nullptr && f.hw > 256 && !(e && e[0] == '0');
+  if (!f.xchg || (e && e[0] == '0')) return 1;
+  return f.hw > 256 ? kXchgSlices : f.hw == 256 ? 4u : 1u;
 }
 
 void launch_splitk_reduce_gn(const GemmArgs& g, const GnFuse& f, hipStream_t s) {
-  const bool xch = splitk_gn_xch(f);
-  const uint32_t hws = xch ? f.hw / kXchgSlices : f.hw;
+  const uint32_t ns = splitk_gn_slices(f), hws = f.hw / ns;
   const uint32_t q = g.N / f.groups / 4, rs = splitk_gn_rs(q, hws), im = hws / rs;
-  const dim3 grid(f.groups * (xch ? kXchgSlices : 1u), g.M / f.hw), block(rs * q);
-#define DI_RGN_LAUNCH(IMV, SV)                                                       \
-  if (im == IMV && g.splits == SV) {                                                 \
-    if (g.res)                                                                       \
-      k_splitk_reduce_gn<IMV, SV, true, false><<<grid, block, 0, s>>>(g, f, q, rs);  \
-    else                                                                             \
-      k_splitk_reduce_gn<IMV, SV, false, false><<<grid, block, 0, s>>>(g, f, q, rs); \
-    return;                                                                          \
-  }
-#define DI_RGNX_LAUNCH(IMV, SV)                                                     \
+  const dim3 grid(f.groups * ns, g.M / f.hw), block(rs * q);
+#define DI_RGN_LAUNCH_NS(IMV, SV, NSV)                                              \
   if (im == IMV && g.splits == SV) {                                                \
     if (g.res)                                                                      \
-      k_splitk_reduce_gn<IMV, SV, true, true><<<grid, block, 0, s>>>(g, f, q, rs);  \
+      k_splitk_reduce_gn<IMV, SV, true, NSV><<<grid, block, 0, s>>>(g, f, q, rs);  \
     else                                                                            \
-      k_splitk_reduce_gn<IMV, SV, false, true><<<grid, block, 0, s>>>(g, f, q, rs); \
+      k_splitk_reduce_gn<IMV, SV, false, NSV><<<grid, block, 0, s>>>(g, f, q, rs); \
     return;                                                                         \
   }
-  if (xch) {
+#define DI_RGN_LAUNCH(IMV, SV) DI_RGN_LAUNCH_NS(IMV, SV, 1)
+#define DI_RGNX_LAUNCH(IMV, SV) DI_RGN_LAUNCH_NS(IMV, SV, 8)
+#define DI_RGNX4_LAUNCH(IMV, SV) DI_RGN_LAUNCH_NS(IMV, SV, 4)
+  static_assert(kXchgSlices == 8, "DI_RGNX_LAUNCH");
+  if (ns == kXchgSlices) {
     DI_RGNX_CASES(DI_RGNX_LAUNCH)
+  } else if (ns == 4) {
+    DI_RGNX4_CASES(DI_RGNX4_LAUNCH)
   } else {
     DI_RGN_CASES(DI_RGN_LAUNCH)
   }
+#undef DI_RGN_LAUNCH_NS
 #undef DI_RGN_LAUNCH
 #undef DI_RGNX_LAUNCH
+#undef DI_RGNX4_LAUNCH
   // splitk_gn_ok admits only built pairs: reaching here would leave the
   // output unwritten
   fprintf(stderr, "launch_splitk_reduce_gn: no instantiation for %u row steps x %u splits\n", im,
@@ -773,16 +781,17 @@ bool splitk_gn_ok(const GemmArgs& g, const GnFuse& f) {
   // image) exchanging their statistics (with the raw output one workgroup
   // per group did not pay: at 32 x 32 the fused conv2 reducer took 11.2 us
   // against 5.0 + 5.0 us for the reducer and apply it replaces)
-  const bool xch = splitk_gn_xch(f);
-  if (f.raw && f.hw > 256 && !xch) return false;
-  const uint32_t hws = xch ? f.hw / kXchgSlices : f.hw;  // rows per workgroup
-  if (xch && (f.hw % kXchgSlices != 0 || (uint64_t)(g.M / f.hw) * f.groups > kXchgRedRecs))
+  const uint32_t ns = splitk_gn_slices(f);
+  if (f.raw && f.hw > 256 && ns == 1) return false;
+  const uint32_t hws = f.hw / ns;  // rows per workgroup
+  if (ns > 1 && (f.hw % ns != 0 || (uint64_t)(g.M / f.hw) * f.groups >
+                                       (ns == 4 ? kXchgRed4Recs : kXchgRedRecs)))
     return false;
   // statistics of the stored values only with the raw output
   if (f.stats && (!f.raw || ((uintptr_t)f.stats & 7) != 0)) return false;
   const uint32_t cpg = g.N / f.groups, slots = g.part_slots ? g.part_slots : g.splits;
   return g.N % f.groups == 0 && cpg % 4 == 0 && cpg <= 40 && hws % 64 == 0 &&
-         splitk_gn_built(hws / splitk_gn_rs(cpg / 4, hws), slots, xch) && g.M % f.hw == 0 &&
+         splitk_gn_built(hws / splitk_gn_rs(cpg / 4, hws), slots, ns) && g.M % f.hw == 0 &&
          g.bias && (!g.bias2 || (g.rows_b2 == f.hw && g.ld_b2 % 4 == 0)) &&
          (!g.res || (!g.res_f32 && g.ldr % 4 == 0 && ((uintptr_t)g.res & 7) == 0)) &&
          (!f.raw || (g.c && g.ldc % 4 == 0 && ((uintptr_t)g.c & 7) == 0)) &&

@@ -1217,7 +1217,7 @@ int gn_nchw_dt(Ctx* c, const void* x, const float* gamma, const float* beta, voi
 }  // namespace
 
 uint64_t gn_xchg_bytes() {
-  return (uint64_t)(kXchgNchwRecs + kXchgRedRecs) * kXchgWords * sizeof(uint64_t);
+  return (uint64_t)(kXchgNchwRecs + kXchgRedRecs + kXchgRed4Recs) * kXchgWords * sizeof(uint64_t);
 }
 
 int launch_group_norm_nchw(Ctx* c, const void* x, const float* gamma, const float* beta,

@@ -92,7 +92,7 @@ def test_resnet_block(dev, rng, B, cin, cout, H, W, temb):
 
 @pytest.mark.parametrize("B,cin,cout,H,W", [
     (1, 1280, 1280, 8, 8),    # conv1 split 12: one row-step of 64 pixels per thread
-    (2, 1280, 1280, 16, 16),  # split 5, four row-steps, two images
+    (2, 1280, 1280, 16, 16),  # split 5, two images: four 64-row slices exchanging
     (1, 640, 640, 32, 32),    # 20 channels per group, split 2: eight 128-row slices exchanging
     (1, 2560, 1280, 8, 8),    # up-block input width (K = 23040)
 ])
@@ -117,8 +117,9 @@ def test_resnet_gn_reducer_matches_apply(dev, rng, monkeypatch, B, cin, cout, H,
 
     monkeypatch.setenv("DI_GN_REDUCE_FUSE", "1")
     fused = run()
-    if H * W > 256:
-        # eight workgroups per (group, image) exchanging their statistics:
+    if H * W >= 256:
+        # four (16 x 16) or eight (32 x 32) workgroups per (group, image)
+        # exchanging their statistics:
         # the recomputing path (no slice awaited) gives the same bits, one
         # workgroup per group the same values up to the order of the sums
         monkeypatch.setenv("DI_GN_XCHG_SPIN", "0")

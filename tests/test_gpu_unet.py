@@ -197,8 +197,9 @@ def test_sd21_gn_in_reducers_matches_separate(sd21, rng, monkeypatch):
 
 
 def test_sd21_gn_exchange_reducers(sd21, rng, monkeypatch):
-    """cfg5 at B=1: the 32 x 32 split-K reducers that apply a GroupNorm with
-    eight workgroups per (group, image) exchanging their statistics give the
+    """cfg5 at B=1: the 16 x 16 and 32 x 32 split-K reducers that apply a
+    GroupNorm with four or eight workgroups per (group, image) exchanging
+    their statistics give the
     same bits when every workgroup recomputes the other slices' sums itself
     (DI_GN_XCHG_SPIN=0, the path a workgroup takes when a slice does not
     arrive), and agree with one workgroup per group or a separate apply
