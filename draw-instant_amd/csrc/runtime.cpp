@@ -226,8 +226,11 @@ int32_t di_create(int32_t device, di_ctx** out) {
   DI_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
   {
     const uint64_t xb = gn_xchg_bytes();
+    // zeroed on the context's own stream (non-blocking: it does not wait for
+    // the legacy default stream) and waited for before any kernel uses it
     hipError_t xe = hipMalloc(&c->gn_xchg, xb);
-    if (xe == hipSuccess) xe = hipMemset(c->gn_xchg, 0, xb);
+    if (xe == hipSuccess) xe = hipMemsetAsync(c->gn_xchg, 0, xb, c->stream);
+    if (xe == hipSuccess) xe = hipStreamSynchronize(c->stream);
     if (xe != hipSuccess) {
       (void)hipFree(c->gn_xchg);
       (void)hipStreamDestroy(c->stream);
