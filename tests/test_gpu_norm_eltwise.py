@@ -90,6 +90,8 @@ def test_gn_silu_entry_point_and_repeat(dev):
     (1, 64, 1600, 8, F32),     # slices end inside a round
     (1, 128, 16384, 32, F32),  # 8 rounds per slice
     (1, 320, 4096, 32, F16),   # 8-wide vectors, a partial third round
+    (1, 8, 1024, 4, F32),      # the smallest group it takes (2048 elements, one round)
+    (1, 2, 1028, 1, F32),      # one group, a ragged last slice (8 slices of 260 and 236)
 ])
 def test_group_norm_exchange_paths(dev, monkeypatch, N, C, HW, G, dt):
     """The single-launch NCHW kernel whose slices exchange their statistics:
