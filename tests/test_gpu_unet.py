@@ -197,13 +197,19 @@ def test_sd21_gn_in_reducers_matches_separate(sd21, rng, monkeypatch):
 
 
 def test_sd21_gn_exchange_reducers(sd21, rng, monkeypatch):
-    """cfg5 at B=1: the 16 x 16 and 32 x 32 split-K reducers that apply a
+    """cfg5 at B=4 and B=1: the 16 x 16 and 32 x 32 split-K reducers that apply a
     GroupNorm with four or eight workgroups per (group, image) exchanging
     their statistics give the
     same bits when every workgroup recomputes the other slices' sums itself
     (DI_GN_XCHG_SPIN=0, the path a workgroup takes when a slice does not
     arrive), and agree with one workgroup per group or a separate apply
     launch (DI_GN_REDUCE_XCHG=0) up to the fp32 summation order."""
+    x4, ctx4 = _inputs(rng, 4, 64, 64, 77, 1024)
+    t4 = np.array([999.0, 750.0, 500.0, 250.0], np.float32)
+    b4 = sd21(x4, t4, ctx4)  # four images: four records per group
+    monkeypatch.setenv("DI_GN_XCHG_SPIN", "0")
+    np.testing.assert_array_equal(sd21(x4, t4, ctx4), b4)
+    monkeypatch.delenv("DI_GN_XCHG_SPIN")
     x, ctx = _inputs(rng, 1, 64, 64, 77, 1024)
     xch = sd21(x, 999.0, ctx)
     monkeypatch.setenv("DI_GN_XCHG_SPIN", "0")
