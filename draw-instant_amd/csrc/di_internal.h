@@ -57,12 +57,14 @@ struct Ctx {
   // of the free list; the capturing owner takes them over.
   bool hold_releases = false;
   std::vector<std::pair<void*, uint64_t>> held;
-  // GroupNorm statistics exchange area (k_norm.hip), zeroed at creation and
-  // kept for the context's life: its counters must only ever grow
+  // statistics-exchange records of the GroupNorm kernels (layout and
+  // regions in di_device.h: the NCHW GroupNorm's, then the split-K
+  // reducer's), zeroed at creation and kept for the context's life: their
+  // counters must only ever grow
   void* gn_xchg = nullptr;
 };
 
-// bytes of a context's GroupNorm exchange area (k_norm.hip)
+// bytes of a context's statistics-exchange area (every region)
 uint64_t gn_xchg_bytes();
 
 // ---- error reporting (thread-local message, status code returned) ----
